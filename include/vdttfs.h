@@ -1,0 +1,241 @@
+/*
+ * vdttfs.h -- C ABI of the MI355X-native VD-TTFS engine (libvdttfs.so).
+ *
+ * Plain C types only: device pointers are `float*` / `int32_t*` returned by
+ * vdttfs_dev_alloc() (or any hipMalloc'ed memory), sizes are int / int64_t.
+ * Every entry point returns an int status (VDTTFS_OK = 0, negative = error
+ * class) and never calls exit(); vdttfs_last_error() describes the last
+ * failure on the calling thread.  Work is stream-ordered on the context's
+ * stream; the `_sync` launch wrappers also synchronise, as the reference's
+ * launch_* helpers do.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   T1V = task1_lenet_mnist/vdttfs_cuda/snn_timesorted_earlyexit.cu
+ *   T2V = task2_vgg16_cifar10/vdttfs_cuda/bench_vgg_eventdriven_timesorted_earlyexit.cu
+ *   T2M = task2_vgg16_cifar10/macs/stat_timesorted_macs.cu
+ *   WIO = task1_lenet_mnist/torch_ann/weights_io.py (blob format)
+ */
+#ifndef VDTTFS_H
+#define VDTTFS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define VDTTFS_OK             0
+#define VDTTFS_E_INVALID     -1  /* bad argument / inconsistent shapes     */
+#define VDTTFS_E_HIP         -2  /* HIP runtime error                      */
+#define VDTTFS_E_IO          -3  /* file missing / unreadable              */
+#define VDTTFS_E_FORMAT      -4  /* malformed weights blob                 */
+#define VDTTFS_E_NOMEM       -5  /* host or device allocation failed       */
+#define VDTTFS_E_UNSUPPORTED -6  /* shape outside what the kernels handle  */
+#define VDTTFS_E_NODEVICE    -7  /* no HIP device visible                  */
+
+#define VDTTFS_INF_TIME 9999.0f  /* "no spike" (T1V:14, T2V:15) */
+
+/* Last error message of the calling thread ("" if none). */
+const char* vdttfs_last_error(void);
+/* Library version string. */
+const char* vdttfs_version(void);
+
+/* ---- per-task constants: the reference's compile-time macros ---------- */
+/* T1V:12-19 (TIME_WINDOW, VTH_INIT, TIME_FIRE_START, CHUNK) and T2V:12-18.
+ * alpha_by_time = 0 reproduces T1V's alpha[tb] indexing (T1V:128,144);
+ * 1 reproduces T2V's alpha[clamp((int)t,0,T)] (T2V:132,150).
+ * conv_same_pad = 0 is T1V's valid convolution (T1V:131-133); 1 is T2V's
+ * zero-padded "same" convolution with out-of-bounds columns skipped
+ * (T2V:112-113,136-141). */
+typedef struct vdttfs_consts {
+    int32_t T;             /* TIME_WINDOW, 1..256                       */
+    float   tfs;           /* TIME_FIRE_START                           */
+    int32_t delta;         /* CHUNK, 1..T                               */
+    float   vth;           /* VTH_INIT                                  */
+    int32_t alpha_by_time;
+    int32_t conv_same_pad;
+} vdttfs_consts;
+
+typedef struct vdttfs_ctx vdttfs_ctx;
+
+/* Replaces the reference's file-static state (T2V:246-248, 321-329): the
+ * context owns the constants, a HIP stream and the bucket scratch. */
+int vdttfs_create(const vdttfs_consts* consts, int device, vdttfs_ctx** out);
+int vdttfs_destroy(vdttfs_ctx* ctx);
+int vdttfs_get_consts(const vdttfs_ctx* ctx, vdttfs_consts* out);
+/* NC = ceil(T/delta) and OFF_STRIDE = NC+1 (T1V:18-19, T2V:17-18). */
+int vdttfs_num_chunks(const vdttfs_ctx* ctx);
+int vdttfs_synchronize(vdttfs_ctx* ctx);
+int vdttfs_device_count(int* out);
+
+/* ---- device memory plumbing (cudaMalloc/cudaMemcpy in the reference) -- */
+int vdttfs_dev_alloc(vdttfs_ctx* ctx, size_t bytes, void** dptr);
+int vdttfs_dev_free(vdttfs_ctx* ctx, void* dptr);
+int vdttfs_h2d(vdttfs_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+int vdttfs_d2h(vdttfs_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+int vdttfs_memset(vdttfs_ctx* ctx, void* dptr, int value, size_t bytes);
+
+/* ---- LUT builder: update_LUTs (T1V:208-216, T2V:236-243) -------------- */
+/* alpha[t] = expf(-((float)t - td_integ)/tc_integ), t in [0,T] (T+1 entries);
+ * theta[t] = vth*expf(-((float)t - td_fire)/tc_fire), t in [0,T).
+ * Host libm expf, then a blocking upload to d_lut_decay / d_lut_th. */
+int vdttfs_update_luts(vdttfs_ctx* ctx, float* d_lut_decay, float* d_lut_th,
+                       float tc_integ, float td_integ, float tc_fire, float td_fire);
+/* The same tables on the host (what update_LUTs uploads). */
+int vdttfs_build_luts_host(const vdttfs_consts* c, float tc_integ, float td_integ,
+                           float tc_fire, float td_fire, float* alpha, float* theta);
+
+/* ---- encoders: k_encode_image (T1V:32-42, T2V:32-42) ------------------ */
+int vdttfs_encode_image(vdttfs_ctx* ctx, const float* d_img, float* d_out, int64_t size,
+                        float tc, float td);
+/* Synthetic configs' rule: x<1e-5 -> INF, else floorf(T*(1-x)). */
+int vdttfs_encode_linear(vdttfs_ctx* ctx, const float* d_img, float* d_out, int64_t size);
+
+/* ---- k_bucketize (T1V:45-80, T2V:45-81) -------------------------------- */
+/* Reference layout, bit-exact: out_off[col*OS + c] (OS = NC+1) holds the
+ * chunk offsets, out_cin/out_tin[col*C_in + pos] the events of each chunk in
+ * ascending cin order (the raw float spike time is copied). */
+int vdttfs_bucketize(vdttfs_ctx* ctx, const float* d_in, int64_t n_cols, int c_in,
+                     int32_t* d_out_cin, float* d_out_tin, int32_t* d_out_off);
+
+/* ---- k_conv_bucketed (T1V:83-162, T2V:84-170) -------------------------- */
+/* Consumes the reference bucket layout; writes first-spike times (INF if a
+ * neuron never fires), NHWC with c_out fastest. */
+int vdttfs_integrate(vdttfs_ctx* ctx, float* d_out, const int32_t* d_bkt_cin,
+                     const float* d_bkt_tin, const int32_t* d_bkt_off, const float* d_kernel,
+                     const float* d_bias, const float* d_lut_decay, const float* d_lut_th,
+                     int t_min, int B, int H_in, int W_in, int C_in, int H_out, int W_out,
+                     int C_out, int K_h, int K_w, int is_fc);
+
+/* ---- fused path: bucketize + integrate from a spike-time map ----------- */
+/* The engine's own path (same results as vdttfs_bucketize followed by
+ * vdttfs_integrate): events are sorted per arrival bin into context scratch
+ * and integrated by the wave-per-pixel kernel.  eproc / ebin (nullable,
+ * host pointers) receive the integrated-synapse counts: eproc under the
+ * reference's chunk-granular early exit (T2M:136,155,176), ebin under the
+ * per-bin exit this kernel executes.  Counting adds a device counter and a
+ * synchronisation; pass NULL for both on the hot path. */
+int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
+                         const float* d_kernel, const float* d_bias, const float* d_lut_decay,
+                         const float* d_lut_th, int t_min, int B, int H_in, int W_in, int C_in,
+                         int H_out, int W_out, int C_out, int K_h, int K_w, int is_fc,
+                         uint64_t* eproc, uint64_t* ebin);
+
+/* ---- k_pooling (T1V:164-181, T2V:192-209) ------------------------------ */
+int vdttfs_pool_min(vdttfs_ctx* ctx, const float* d_in, float* d_out, int B, int H_in,
+                    int W_in, int C);
+
+/* ---- k_layer_vmem (T2V:172-190) ---------------------------------------- */
+int vdttfs_fc_vmem(vdttfs_ctx* ctx, const float* d_in, float* d_out, const float* d_kernel,
+                   const float* d_bias, const float* d_lut_decay, int B, int C_in, int C_out);
+
+/* ---- readout (T1V:312-319 argmin, T2V:389-396 argmax) on the device ---- */
+int vdttfs_readout_argmin(vdttfs_ctx* ctx, const float* d_out, int B, int C, int32_t* d_pred);
+int vdttfs_readout_argmax(vdttfs_ctx* ctx, const float* d_out, int B, int C, int32_t* d_pred);
+
+/* ---- per-layer launch wrappers (T1V:222-240, T2V:250-287) -------------- */
+/* Synchronous like the reference: bucketize + integrate (+ sync) with the
+ * context's bucket scratch.  t_min = max(0, ceilf(td)) as T1V:225. */
+int vdttfs_launch_layer_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, int H_in,
+                             int W_in, int C_in, int H_out, int W_out, int C_out, int K_h,
+                             int K_w, float td, const float* d_kernel, const float* d_bias,
+                             const float* d_lut_decay, const float* d_lut_th, int B, int is_fc);
+int vdttfs_launch_pool_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, int H_in,
+                            int W_in, int C, int B);
+int vdttfs_launch_fc_vmem_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, int C_in,
+                               int C_out, const float* d_kernel, const float* d_bias,
+                               const float* d_lut_decay, int B);
+
+/* ---- weights blob (T1V:185-206, T2V:213-234; format WIO:1-13) ---------- */
+typedef struct vdttfs_blob_layer {
+    int32_t ndim;          /* 4: [k_h,k_w,c_in,c_out] (HWIO); 2: [c_in,c_out] */
+    int32_t shape[4];
+    int32_t k_h, k_w, c_in, c_out;
+    int64_t kernel_elems;
+    float*  kernel;        /* host, C order of `shape`                       */
+    int32_t bias_ndim;
+    int32_t bias_size;
+    float*  bias;          /* host                                           */
+    int32_t tc_ndim, td_ndim;
+    float   tc_fire, td;
+} vdttfs_blob_layer;
+
+typedef struct vdttfs_blob {
+    int32_t num_layers;
+    vdttfs_blob_layer* layers;
+} vdttfs_blob;
+
+/* Parses and validates the whole file (ndim in {2,4}, positive shapes,
+ * bias size = c_out, one tc and one td float, no short read, no trailing
+ * bytes -- the consumption check of WIO:69). */
+int vdttfs_blob_read(const char* path, vdttfs_blob** out);
+int vdttfs_blob_write(const char* path, const vdttfs_blob* blob);
+int vdttfs_blob_free(vdttfs_blob* blob);
+
+/* load_weights: the reference's LayerWeights (T1V:26-30) on the device. */
+typedef struct vdttfs_dev_layer {
+    float*  d_kernel;
+    float*  d_bias;
+    float   tc_fire, td;
+    int32_t k_h, k_w, c_in, c_out;
+} vdttfs_dev_layer;
+int vdttfs_load_weights(vdttfs_ctx* ctx, const char* path, vdttfs_dev_layer** layers,
+                        int* num_layers);
+int vdttfs_free_weights(vdttfs_ctx* ctx, vdttfs_dev_layer* layers, int num_layers);
+
+/* ---- network engine: the driver main()s (T1V:286-319, T2V:337-396) ----- */
+#define VDTTFS_LAYER_CONV 0
+#define VDTTFS_LAYER_FC   1
+#define VDTTFS_LAYER_POOL 2   /* 2x2 min pool  */
+#define VDTTFS_LAYER_VMEM 3   /* readout vmem  */
+#define VDTTFS_ENCODE_LINEAR 0
+#define VDTTFS_ENCODE_LOG    1
+#define VDTTFS_READOUT_ARGMIN 0
+#define VDTTFS_READOUT_ARGMAX 1
+
+typedef struct vdttfs_layer_desc {
+    int32_t kind;
+    int32_t H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w;
+    const float* kernel;   /* host, reference layout (HWIO / [C_in][C_out]) */
+    const float* bias;     /* host, C_out floats                            */
+    float tc_fire, td;
+} vdttfs_layer_desc;
+
+typedef struct vdttfs_net vdttfs_net;
+
+/* Uploads weights, builds every layer's LUTs once (kept resident on the
+ * device) and allocates activations and scratch for batch B.
+ * img_elems = H*W*C of one input image (NHWC). */
+int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
+                      int64_t img_elems, int encode_mode, float tc_in, float td_in,
+                      int readout, vdttfs_net** out);
+int vdttfs_net_destroy(vdttfs_net* net);
+/* encode -> every layer -> readout, stream-ordered, no host sync.  d_img is
+ * [B][img_elems]; d_pred (nullable) receives B int32 classes. */
+int vdttfs_net_forward(vdttfs_net* net, const float* d_img, int32_t* d_pred);
+/* Device pointer to layer i's output map (valid after a forward). */
+int vdttfs_net_layer_output(vdttfs_net* net, int layer, const float** d_out, int64_t* elems);
+/* One instrumented forward: per-layer integrated-synapse counts (see
+ * vdttfs_layer_forward), retained events N_ev and bucket columns N_cols. */
+int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint64_t* ebin,
+                     uint64_t* n_ev, uint64_t* n_cols);
+/* Event timing of integrator launches: when enabled, forward() brackets
+ * each integrator launch with HIP events on the context stream; read_timing
+ * synchronises and returns the summed milliseconds and launch count since
+ * the last reset. */
+int vdttfs_net_set_timing(vdttfs_net* net, int enable);
+int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
+                           double* bucket_ms, int64_t* bucket_launches);
+
+/* ---- synthetic workloads (counter-mode splitmix64; host) --------------- */
+/* u = (z>>40) * 2^-24 with z = mix(seed + 0x9E3779B97F4A7C15*(stream*2^40+i+1)). */
+int vdttfs_synth_uniform(uint64_t seed, uint64_t stream, float* out, int64_t n);
+/* Box-Muller in fp64, scaled by sigma, rounded to fp32. */
+int vdttfs_synth_normal(uint64_t seed, uint64_t stream, float* out, int64_t n, double sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,244 @@
+"""GPU parity of every kernel against the CPU oracle, through the C ABI.
+
+Bar: bucket offsets and event order bit-exact; first-spike times bit-exact;
+integrated-synapse counts exact; vmem within 1e-5 relative (fp32 dot
+product in the reference's order, so in practice exact)."""
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle
+import vdttfs
+
+pytestmark = pytest.mark.gpu
+INF = np.float32(9999.0)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def spikes(rng, n, T, p=0.55, edge=True):
+    t = rng.integers(0, T + 6, n).astype(np.float32)
+    s = np.where(rng.random(n) < p, t, INF).astype(np.float32)
+    if edge and n > 6:
+        s[0] = np.float32(np.nan)
+        s[1] = np.float32(-2.0)
+        s[2] = np.float32(T)
+        s[3] = np.float32(T - 1)
+        s[4] = np.float32(3.5)
+    return s
+
+
+def consts(T, tfs, delta, task2):
+    return vdttfs.TaskConsts(T=T, tfs=tfs, delta=delta, vth=1.0, alpha_by_time=task2,
+                             conv_same_pad=task2)
+
+
+def valid_rows(cin, tin, off, n_cols, c_in, OS):
+    """Each column's valid prefix (the reference leaves the tail unwritten)."""
+    out_c, out_t = [], []
+    for col in range(n_cols):
+        n = off[col * OS + OS - 1]
+        out_c.append(cin[col * c_in: col * c_in + n])
+        out_t.append(tin[col * c_in: col * c_in + n])
+    return np.concatenate(out_c), np.concatenate(out_t)
+
+
+BKT_CASES = [
+    # T, tfs, delta, c_in, n_cols
+    (64, 0.0, 16, 1, 5000),
+    (64, 32.0, 8, 3, 4097),
+    (64, 32.0, 8, 64, 3000),
+    (80, 40.0, 8, 100, 513),
+    (64, 0.0, 16, 512, 300),
+    (16, 0.0, 5, 4096, 40),
+    (255, 0.0, 1, 6, 777),
+    (64, 0.0, 1, 130, 200),
+]
+
+
+@pytest.mark.parametrize("T,tfs,delta,c_in,n_cols", BKT_CASES)
+def test_bucketize_bitexact(gpu_ctx_factory, T, tfs, delta, c_in, n_cols):
+    say(f"bucketize T={T} tfs={tfs} delta={delta} c_in={c_in} n_cols={n_cols}")
+    rng = np.random.default_rng(c_in * 7 + n_cols)
+    sp = spikes(rng, n_cols * c_in, T)
+    tc = consts(T, tfs, delta, False)
+    ctx = gpu_ctx_factory(tc)
+    OS = tc.num_chunks + 1
+    d_in = ctx.to_device(sp)
+    d_cin = ctx.empty(n_cols * c_in, np.int32)
+    d_tin = ctx.empty(n_cols * c_in, np.float32)
+    d_off = ctx.empty(n_cols * OS, np.int32)
+    ctx.bucketize(d_in, n_cols, c_in, d_cin, d_tin, d_off)
+    ctx.synchronize()
+    g_off = d_off.download()
+    ocin, otin, ooff = oracle.bucketize(oracle.Consts.from_task(tc), sp, n_cols, c_in)
+    np.testing.assert_array_equal(g_off, ooff)
+    gc, gt = valid_rows(d_cin.download(), d_tin.download(), g_off, n_cols, c_in, OS)
+    oc, ot = valid_rows(ocin, otin, ooff, n_cols, c_in, OS)
+    np.testing.assert_array_equal(gc, oc)
+    np.testing.assert_array_equal(gt.view(np.int32), ot.view(np.int32))
+
+
+LAYER_CASES = [
+    # name, T, tfs, delta, task2, is_fc, B, H, W, C_in, C_out, K
+    ("t1-conv5x5-c6", 64, 0.0, 16, False, False, 3, 12, 12, 6, 16, 5),
+    ("t1-conv5x5-c1", 64, 0.0, 16, False, False, 4, 28, 28, 1, 6, 5),
+    ("t2-conv3x3-c64", 64, 32.0, 8, True, False, 2, 16, 16, 64, 64, 3),
+    ("t2-conv3x3-c128-o192", 64, 32.0, 8, True, False, 2, 8, 8, 128, 192, 3),
+    ("t2-conv3x3-2x2", 64, 32.0, 8, True, False, 3, 2, 2, 512, 128, 3),
+    ("t1-fc-256-120", 64, 0.0, 16, False, True, 37, 1, 1, 256, 120, 1),
+    ("t2-fc-512-512", 64, 32.0, 8, True, True, 20, 1, 1, 512, 512, 1),
+    ("t1-fc-4096-96-delta32", 32, 0.0, 32, False, True, 9, 1, 1, 4096, 96, 1),
+    ("t2-conv-T80", 80, 40.0, 8, True, False, 2, 6, 6, 32, 64, 3),
+]
+
+
+def layer_inputs(rng, tc, is_fc, B, H, W, C_in, C_out, K, dense_early=False):
+    if is_fc:
+        n_cols, kshape = B, (C_in, C_out)
+        H_in = W_in = H_out = W_out = 1
+        K_h = K_w = 1
+    else:
+        n_cols, kshape = B * H * W, (K, K, C_in, C_out)
+        H_in, W_in = H, W
+        H_out, W_out = (H, W) if tc.conv_same_pad else (H - K + 1, W - K + 1)
+        K_h = K_w = K
+    sp = spikes(rng, n_cols * C_in, tc.T, edge=False)
+    if dense_early:
+        sp = np.where(rng.random(sp.size) < 0.9, np.float32(0.0), sp).astype(np.float32)
+    fan = int(np.prod(kshape[:-1]))
+    Wt = (rng.standard_normal(int(np.prod(kshape))) * np.sqrt(2.0 / fan)).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.05).astype(np.float32)
+    shape = dict(B=B, H_in=H_in, W_in=W_in, C_in=C_in, H_out=H_out, W_out=W_out, C_out=C_out,
+                 K_h=K_h, K_w=K_w)
+    return sp, Wt, bias, n_cols, shape
+
+
+def oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shape, t_min, is_fc):
+    c = oracle.Consts.from_task(tc)
+    cin, tin, off = oracle.bucketize(c, sp, n_cols, shape["C_in"])
+    pad = shape["K_h"] // 2 if (tc.conv_same_pad and not is_fc) else 0
+    return oracle.integrate(c, cin, tin, off, Wt, bias, alpha, theta, t_min, pad=pad,
+                            is_fc=is_fc, **shape)
+
+
+@pytest.mark.parametrize("case", LAYER_CASES, ids=[c[0] for c in LAYER_CASES])
+def test_integrate_paths_bitexact(gpu_ctx_factory, case):
+    name, T, tfs, delta, task2, is_fc, B, H, W, C_in, C_out, K = case
+    say(f"integrate {name}")
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    tc = consts(T, tfs, delta, task2)
+    ctx = gpu_ctx_factory(tc)
+    sp, Wt, bias, n_cols, shape = layer_inputs(rng, tc, is_fc, B, H, W, C_in, C_out, K)
+    alpha, theta = vdttfs.build_luts_host(tc, T / 4.0, 0.0, T / 4.0, 0.0)
+    t_min = 1
+    exp, ep, eb = oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shape, t_min, is_fc)
+    assert 0.02 < float(np.mean(exp < INF)) < 0.98, "degenerate case"
+    n_out = exp.size
+    d_in, d_W, d_b = ctx.to_device(sp), ctx.to_device(Wt), ctx.to_device(bias)
+    d_a, d_t = ctx.to_device(alpha), ctx.to_device(theta)
+    # (1) the drop-in pair: reference-layout bucketize + integrate
+    OS = tc.num_chunks + 1
+    d_cin = ctx.empty(n_cols * C_in, np.int32)
+    d_tin = ctx.empty(n_cols * C_in, np.float32)
+    d_off = ctx.empty(n_cols * OS, np.int32)
+    d_out = ctx.empty(n_out, np.float32)
+    ctx.bucketize(d_in, n_cols, C_in, d_cin, d_tin, d_off)
+    ctx.integrate(d_out, d_cin, d_tin, d_off, d_W, d_b, d_a, d_t, t_min, is_fc=is_fc, **shape)
+    ctx.synchronize()
+    np.testing.assert_array_equal(d_out.download(), exp)
+    # (2) the engine path, with exact synapse counts
+    d_out2 = ctx.empty(n_out, np.float32)
+    gp, gb = ctx.layer_forward(d_out2, d_in, d_W, d_b, d_a, d_t, t_min, is_fc=is_fc, count=True,
+                               **shape)
+    np.testing.assert_array_equal(d_out2.download(), exp)
+    assert (gp, gb) == (ep, eb)
+    # (3) engine path without counters (the hot-path kernel variant)
+    d_out3 = ctx.empty(n_out, np.float32)
+    ctx.layer_forward(d_out3, d_in, d_W, d_b, d_a, d_t, t_min, is_fc=is_fc, **shape)
+    ctx.synchronize()
+    np.testing.assert_array_equal(d_out3.download(), exp)
+
+
+def test_integrate_oversized_bins(gpu_ctx_factory):
+    """Bins holding more events than the wave's merged list (windowed path)."""
+    say("integrate oversized bins")
+    rng = np.random.default_rng(99)
+    tc = consts(64, 32.0, 8, True)
+    ctx = gpu_ctx_factory(tc)
+    for is_fc, B, H, W, C_in, C_out, K in [(True, 6, 1, 1, 4096, 64, 1), (False, 1, 4, 4, 512, 64, 3)]:
+        sp, Wt, bias, n_cols, shape = layer_inputs(rng, tc, is_fc, B, H, W, C_in, C_out, K,
+                                                   dense_early=True)
+        Wt *= 0.05  # keep neurons from firing at the first bin
+        alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+        exp, ep, eb = oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shape, 0, is_fc)
+        d_out = ctx.empty(exp.size, np.float32)
+        gp, gb = ctx.layer_forward(d_out, ctx.to_device(sp), ctx.to_device(Wt), ctx.to_device(bias),
+                                   ctx.to_device(alpha), ctx.to_device(theta), 0, is_fc=is_fc,
+                                   count=True, **shape)
+        np.testing.assert_array_equal(d_out.download(), exp)
+        assert (gp, gb) == (ep, eb)
+
+
+def test_launch_layer_sync_matches_oracle(gpu_ctx_factory):
+    say("launch_layer_sync")
+    rng = np.random.default_rng(5)
+    tc = consts(64, 0.0, 16, False)
+    ctx = gpu_ctx_factory(tc)
+    sp, Wt, bias, n_cols, shape = layer_inputs(rng, tc, False, 2, 12, 12, 6, 16, 5)
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_a, d_t = ctx.empty(tc.T + 1), ctx.empty(tc.T)
+    ctx.update_LUTs(d_a, d_t, 16.0, 0.0, 16.0, 0.0)
+    np.testing.assert_array_equal(d_a.download(), alpha)
+    np.testing.assert_array_equal(d_t.download(), theta)
+    exp, _, _ = oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shape, 0, False)
+    d_out = ctx.empty(exp.size)
+    ctx.launch_layer(ctx.to_device(sp), d_out, 12, 12, 6, 8, 8, 16, 5, 5, -0.5, ctx.to_device(Wt),
+                     ctx.to_device(bias), d_a, d_t, 2, False)
+    np.testing.assert_array_equal(d_out.download(), exp)
+
+
+def test_pool_vmem_readout_encode(gpu_ctx_factory):
+    say("pool / vmem / readout / encoders")
+    rng = np.random.default_rng(8)
+    tc = consts(64, 32.0, 8, True)
+    ctx = gpu_ctx_factory(tc)
+    B, H, W, Cc = 5, 9, 8, 7
+    x = np.where(rng.random(B * H * W * Cc) < 0.5, rng.integers(0, 64, B * H * W * Cc), 9999).astype(np.float32)
+    d_o = ctx.empty(B * (H // 2) * (W // 2) * Cc)
+    ctx.pool_min(ctx.to_device(x), d_o, B, H, W, Cc)
+    np.testing.assert_array_equal(d_o.download(), oracle.pool_min(x, B, H, W, Cc))
+    C_in, C_out = 512, 10
+    xs = np.where(rng.random(B * C_in) < 0.6, rng.integers(0, 100, B * C_in), 9999).astype(np.float32)
+    Wt = rng.standard_normal(C_in * C_out).astype(np.float32)
+    bias = rng.standard_normal(C_out).astype(np.float32)
+    alpha, _ = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_v = ctx.empty(B * C_out)
+    ctx.fc_vmem(ctx.to_device(xs), d_v, ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha),
+                B, C_in, C_out)
+    got = d_v.download()
+    exp = oracle.fc_vmem(oracle.Consts.from_task(tc), xs, Wt, bias, alpha, B, C_in, C_out)
+    scale = np.abs(exp) + 1e-3
+    assert np.all(np.abs(got - exp) <= 1e-5 * scale)
+    for argmax in (False, True):
+        d_p = ctx.empty(B, np.int32)
+        ctx.readout(ctx.to_device(got if argmax else x[:B * 4]), B, 10 if argmax else 4, argmax, d_p)
+        ref = oracle.readout(got if argmax else x[:B * 4], B, 10 if argmax else 4,
+                             oracle.READ_ARGMAX if argmax else oracle.READ_ARGMIN)
+        np.testing.assert_array_equal(d_p.download(), ref)
+    img = rng.random(4096).astype(np.float32)
+    img[:5] = [0.0, 1e-6, 1e-5, 1.0, 0.5]
+    d_e = ctx.empty(img.size)
+    ctx.encode_linear(ctx.to_device(img), d_e)
+    np.testing.assert_array_equal(d_e.download(), oracle.encode_linear(img, tc.T))
+    ctx.encode_image(ctx.to_device(img), d_e, 17.452274, 0.0)
+    g = d_e.download()
+    o = oracle.encode_log(img, 17.452274, 0.0, tc.T)
+    # device logf may differ from glibc by an ulp: only ceil-boundary ties may move
+    diff = np.flatnonzero(g != o)
+    assert diff.size <= 2, diff

@@ -1,0 +1,329 @@
+"""Pins the CPU oracle (oracle/vdttfs_oracle.c) against checks that do not
+re-type its formulas: exact-rational brute force (tests/pyref.py), closed
+forms, invariants and hand-computed values.  The reference repository holds
+no golden vectors or fixtures for this path, so these are the pins; the
+committed fixtures in tests/golden/ were produced by pyref.py.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import pyref
+
+INF = np.float32(9999.0)
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def rand_spikes(rng, n, T, p_active=0.6, extra_cases=True):
+    t = rng.integers(0, T + 8, size=n).astype(np.float32)  # some beyond the window
+    act = rng.random(n) < p_active
+    s = np.where(act, t, INF).astype(np.float32)
+    if extra_cases and n > 8:
+        s[0] = np.float32(np.nan)           # NaN: dropped (t < INF is false)
+        s[1] = np.float32(-3.0)             # negative: clamped to bin 0
+        s[2] = np.float32(T - 1)            # last bin
+        s[3] = np.float32(T)                # at the window edge
+        s[4] = np.float32(2.5)              # non-integer time
+    return s
+
+
+# ---------------------------------------------------------------- LUTs
+def test_luts_closed_form_and_one_ulp():
+    T = 64
+    a, th = oracle.build_luts(T, 1.0, 16.0, 3.0, 20.0, 5.0)
+    assert a[3] == np.float32(1.0)                  # alpha(td_i) = expf(0) = 1
+    assert th[5] == np.float32(1.0)                 # theta(td_f) = vth
+    assert np.all(np.diff(th.astype(np.float64)) <= 0)
+    ea, et = pyref.luts(T, 1.0, 16.0, 3.0, 20.0, 5.0)
+    ulp = np.spacing(np.abs(ea.astype(np.float32)))
+    assert np.all(np.abs(a.astype(np.float64) - ea.astype(np.float64)) <= ulp)
+    assert np.all(np.abs(th.astype(np.float64) - et.astype(np.float64)) <= np.spacing(et))
+
+
+# ---------------------------------------------------------------- encoders
+def test_encode_linear_hand_values():
+    x = np.array([0.0, 1e-6, 1e-5, 1.0, 0.5, 0.25, 0.999, 1.0 / 64, 0.75], np.float32)
+    out = oracle.encode_linear(x, 64)
+    # float32(1e-5) < 1e-5 (double), so it is "no spike" too
+    exp = [9999, 9999, 9999, 0, 32, 48, 0, 63, 16]
+    assert out.tolist() == exp
+
+
+def test_encode_log_hand_values():
+    x = np.array([1.0, math.exp(-1.0), 0.0, 1e-30], np.float32)
+    out = oracle.encode_log(x, 16.0, 0.0, 80)
+    assert out[0] == 0.0                  # -tc*log(1) = 0
+    assert out[1] == 16.0 or out[1] == 17.0  # tc*1 at a ceil boundary (documented tie)
+    assert out[2] == INF
+    assert out[3] == INF                  # 16*69 > 80
+
+
+# ---------------------------------------------------------------- bucketize
+@pytest.mark.parametrize("T,tfs,delta,c_in", [(64, 0.0, 16, 5), (64, 32.0, 8, 7), (80, 40.0, 8, 3),
+                                              (16, 0.0, 1, 9), (20, 0.0, 6, 4)])
+def test_bucketize_matches_stable_sort(T, tfs, delta, c_in):
+    rng = np.random.default_rng(T * 100 + c_in)
+    n_cols = 11
+    sp = rand_spikes(rng, n_cols * c_in, T)
+    c = oracle.Consts(T, tfs, delta)
+    got = oracle.bucketize(c, sp, n_cols, c_in)
+    exp = pyref.bucketize(sp, n_cols, c_in, T, tfs, delta)
+    for g, e in zip(got, exp):
+        np.testing.assert_array_equal(g, e)
+
+
+def test_bucketize_invariants():
+    rng = np.random.default_rng(7)
+    T, delta, c_in, n_cols = 64, 8, 64, 50
+    sp = rand_spikes(rng, n_cols * c_in, T)
+    c = oracle.Consts(T, 32.0, delta)
+    cin, tin, off = oracle.bucketize(c, sp, n_cols, c_in)
+    OS = c.num_chunks + 1
+    for col in range(n_cols):
+        o = off[col * OS:(col + 1) * OS]
+        assert np.all(np.diff(o) >= 0)
+        n = o[-1]
+        row = sp[col * c_in:(col + 1) * c_in]
+        keep = [i for i in range(c_in) if pyref.arrival_bin(row[i], 32.0, T) >= 0]
+        assert n == len(keep)
+        assert sorted(cin[col * c_in: col * c_in + n].tolist()) == keep
+        for k in range(c.num_chunks):
+            seg = cin[col * c_in + o[k]: col * c_in + o[k + 1]]
+            assert np.all(np.diff(seg) > 0)  # ascending cin inside a chunk
+
+
+# ---------------------------------------------------------------- integrator
+def layer_case(rng, T, tfs, delta, alpha_by_time, is_fc, same, B=2, H=5, W=4, C_in=3, C_out=4, K=3,
+               bias_scale=0.3):
+    if is_fc:
+        H_in = W_in = H_out = W_out = 1
+        K_h = K_w = 1
+        pad = 0
+        n_cols = B
+    else:
+        H_in, W_in = H, W
+        pad = K // 2 if same else 0
+        H_out = H if same else H - K + 1
+        W_out = W if same else W - K + 1
+        K_h = K_w = K
+        n_cols = B * H_in * W_in
+    sp = rand_spikes(rng, n_cols * C_in, T, extra_cases=False)
+    Wt = (rng.standard_normal(K_h * K_w * C_in * C_out) * 0.6).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * bias_scale).astype(np.float32)
+    alpha, theta = oracle.build_luts(T, 1.0, T / 4.0, 0.0, T / 4.0, 0.0)
+    c = oracle.Consts(T, tfs, delta, alpha_by_time)
+    shape = dict(B=B, H_in=H_in, W_in=W_in, C_in=C_in, H_out=H_out, W_out=W_out, C_out=C_out,
+                 K_h=K_h, K_w=K_w, pad=pad, is_fc=is_fc)
+    return c, sp, Wt, bias, alpha, theta, n_cols, shape
+
+
+def run_oracle(c, sp, Wt, bias, alpha, theta, n_cols, shape, t_min=0, no_ee=False):
+    cin, tin, off = oracle.bucketize(c, sp, n_cols, shape["C_in"])
+    return oracle.integrate(c, cin, tin, off, Wt, bias, alpha, theta, t_min, no_early_exit=no_ee,
+                            **shape)
+
+
+CASES = [
+    # T, tfs, delta, alpha_by_time, is_fc, same
+    (16, 0.0, 4, False, False, False),   # Task-1 semantics, valid conv
+    (16, 6.0, 4, True, False, True),     # Task-2 semantics, same-pad conv, TFS shift
+    (12, 0.0, 5, False, True, False),    # FC, Delta not dividing T
+    (12, 4.0, 3, True, True, False),
+]
+
+
+@pytest.mark.parametrize("T,tfs,delta,abt,is_fc,same", CASES)
+def test_integrate_matches_exact_bruteforce(T, tfs, delta, abt, is_fc, same):
+    rng = np.random.default_rng(T + int(tfs) + delta)
+    c, sp, Wt, bias, alpha, theta, n_cols, shape = layer_case(rng, T, tfs, delta, abt, is_fc, same)
+    got, _, _ = run_oracle(c, sp, Wt, bias, alpha, theta, n_cols, shape, t_min=1)
+    exp = pyref.integrate_dense(sp, Wt, bias, alpha, theta, 1, T=T, tfs=tfs, alpha_by_time=abt,
+                                **shape)
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.parametrize("T,tfs,delta,abt,is_fc,same", CASES)
+def test_integrate_matches_timedriven(T, tfs, delta, abt, is_fc, same):
+    rng = np.random.default_rng(1000 + T)
+    c, sp, Wt, bias, alpha, theta, n_cols, shape = layer_case(rng, T, tfs, delta, abt, is_fc, same,
+                                                              B=3, H=7, W=6, C_in=8, C_out=16)
+    got, _, _ = run_oracle(c, sp, Wt, bias, alpha, theta, n_cols, shape)
+    td = oracle.integrate_timedriven(c, sp, Wt, bias, alpha, theta, 0, **shape)
+    np.testing.assert_array_equal(got, td)
+
+
+def test_integrate_delta_invariance_and_counts():
+    rng = np.random.default_rng(42)
+    T = 32
+    outs, ebins = [], []
+    base = layer_case(rng, T, 8.0, 1, True, False, True, B=2, H=6, W=6, C_in=16, C_out=32)
+    _, sp, Wt, bias, alpha, theta, n_cols, shape = base
+    for delta in (1, 2, 3, 4, 8, 16, 32):
+        c = oracle.Consts(T, 8.0, delta, True)
+        o, ep, eb = run_oracle(c, sp, Wt, bias, alpha, theta, n_cols, shape)
+        outs.append(o)
+        ebins.append(eb)
+        # E_proc is chunk-granular: never below the per-bin count
+        assert ep >= eb
+        # NOEARLYEXIT integrates every retained receptive-field event
+        _, ep_all, _ = run_oracle(c, sp, Wt, bias, alpha, theta, n_cols, shape, no_ee=True)
+        assert ep_all == total_receptive_events(sp, shape, T, 8.0)
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    assert len(set(ebins)) == 1  # the per-bin count does not depend on Delta
+
+
+def total_receptive_events(sp, shape, T, tfs):
+    B, H_in, W_in, C_in = shape["B"], shape["H_in"], shape["W_in"], shape["C_in"]
+    keep = np.array([pyref.arrival_bin(t, tfs, T) >= 0 for t in sp]).reshape(-1, C_in).sum(1)
+    if shape["is_fc"]:
+        return int(keep.sum() * shape["C_out"])
+    keep = keep.reshape(B, H_in, W_in)
+    tot = 0
+    for b in range(B):
+        for ho in range(shape["H_out"]):
+            for wo in range(shape["W_out"]):
+                for kh in range(shape["K_h"]):
+                    for kw in range(shape["K_w"]):
+                        hi, wi = ho - shape["pad"] + kh, wo - shape["pad"] + kw
+                        if 0 <= hi < H_in and 0 <= wi < W_in:
+                            tot += keep[b, hi, wi]
+    return int(tot * shape["C_out"])
+
+
+def test_single_input_closed_form():
+    T = 20
+    alpha, theta = oracle.build_luts(T, 1.0, 5.0, 0.0, 5.0, 0.0)
+    c = oracle.Consts(T, 0.0, 4, False)
+    for w, t_in, bias, t_min in [(1.5, 3.0, 0.0, 0), (0.2, 2.0, 0.0, 0), (0.5, 7.0, 0.01, 2),
+                                 (-1.0, 1.0, 0.5, 0), (0.0, 0.0, 0.0, 0), (3.0, 0.0, 0.0, 4)]:
+        sp = np.array([t_in], np.float32)
+        Wt = np.array([w], np.float32)
+        b = np.array([bias], np.float32)
+        cin, tin, off = oracle.bucketize(c, sp, 1, 1)
+        got, _, _ = oracle.integrate(c, cin, tin, off, Wt, b, alpha, theta, t_min, 1, 1, 1, 1, 1,
+                                     1, 1, 1, 1, 0, True)
+        contrib = pyref.mul32(w, alpha[int(t_in)])
+        exp = INF
+        for t in range(t_min, T):
+            carry = pyref.add32(bias, contrib) if t >= int(t_in) else float(np.float32(bias))
+            if carry >= theta[t] and theta[t] >= np.float32(1e-5):
+                exp = float(t)
+                break
+        assert got[0] == exp, (w, t_in, bias, t_min)
+
+
+def test_zero_weight_layer_fires_on_bias_only():
+    T = 32
+    alpha, theta = oracle.build_luts(T, 1.0, 8.0, 0.0, 8.0, 0.0)
+    c = oracle.Consts(T, 0.0, 8, False)
+    rng = np.random.default_rng(3)
+    sp = rand_spikes(rng, 4 * 6, T, extra_cases=False)
+    bias = np.array([0.5, 0.1, 0.0, -0.2], np.float32)
+    cin, tin, off = oracle.bucketize(c, sp, 4, 6)
+    got, _, _ = oracle.integrate(c, cin, tin, off, np.zeros(6 * 4, np.float32), bias, alpha, theta,
+                                 0, 4, 1, 1, 6, 1, 1, 4, 1, 1, 0, True)
+    for co in range(4):
+        exp = next((float(t) for t in range(T) if bias[co] >= theta[t] and theta[t] >= 1e-5), 9999.0)
+        assert np.all(got.reshape(4, 4)[:, co] == exp)
+
+
+# ---------------------------------------------------------------- pool / vmem / readout
+def test_pool_min():
+    rng = np.random.default_rng(5)
+    B, H, W, Cc = 2, 6, 5, 3
+    x = np.where(rng.random(B * H * W * Cc) < 0.5, rng.integers(0, 64, B * H * W * Cc), 9999).astype(np.float32)
+    got = oracle.pool_min(x, B, H, W, Cc).reshape(B, H // 2, W // 2, Cc)
+    xr = x.reshape(B, H, W, Cc)[:, :H // 2 * 2, :W // 2 * 2, :]
+    exp = xr.reshape(B, H // 2, 2, W // 2, 2, Cc).min(axis=(2, 4))
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_fc_vmem_fp64():
+    rng = np.random.default_rng(6)
+    T, tfs, B, C_in, C_out = 64, 32.0, 3, 50, 10
+    x = np.where(rng.random(B * C_in) < 0.7, rng.integers(0, T + 40, B * C_in), 9999).astype(np.float32)
+    Wt = rng.standard_normal(C_in * C_out).astype(np.float32)
+    bias = rng.standard_normal(C_out).astype(np.float32)
+    alpha, _ = oracle.build_luts(T, 1.0, 16.0, 0.0, 16.0, 0.0)
+    c = oracle.Consts(T, tfs, 8, True)
+    got = oracle.fc_vmem(c, x, Wt, bias, alpha, B, C_in, C_out).reshape(B, C_out)
+    xr = x.reshape(B, C_in).astype(np.float64)
+    valid = (xr < 9999) & ((xr - tfs) <= T)
+    ti = np.clip(np.trunc(xr), 0, T).astype(int)
+    a = np.where(valid, alpha.astype(np.float64)[ti], 0.0)
+    exp = a @ Wt.reshape(C_in, C_out).astype(np.float64) + bias
+    scale = np.abs(a) @ np.abs(Wt.reshape(C_in, C_out).astype(np.float64)) + np.abs(bias)
+    assert np.all(np.abs(got - exp) <= 1e-5 * scale + 1e-7)
+
+
+def test_readout_tie_rules():
+    rows = np.array([[5, 3, 3, 9], [9999, 9999, 9999, 9999], [2, 1, 1, 0]], np.float32)
+    assert oracle.readout(rows, 3, 4, oracle.READ_ARGMIN).tolist() == [1, -1, 3]
+    assert oracle.readout(rows, 3, 4, oracle.READ_ARGMAX).tolist() == [3, 0, 0]
+    ties = np.array([[1, 7, 7, 2]], np.float32)  # first maximal index wins
+    assert oracle.readout(ties, 1, 4, oracle.READ_ARGMAX).tolist() == [1]
+    assert oracle.readout(rows, 3, 4, oracle.READ_T3).tolist() == [1, 0, 3]
+    v = np.array([[-1e10, -2e10]], np.float32)  # nothing above -1e9: class -1
+    assert oracle.readout(v, 1, 2, oracle.READ_ARGMAX).tolist() == [-1]
+
+
+# ---------------------------------------------------------------- golden fixtures
+def test_golden_fixtures():
+    with open(os.path.join(HERE, "golden", "integrate_golden.json")) as f:
+        cases = json.load(f)
+    assert len(cases) >= 4
+    for case in cases:
+        k = case["consts"]
+        c = oracle.Consts(k["T"], k["tfs"], k["delta"], k["alpha_by_time"])
+        sh = case["shape"]
+        sp = np.array(case["spikes"], np.float32)
+        n_cols = sh["B"] if sh["is_fc"] else sh["B"] * sh["H_in"] * sh["W_in"]
+        cin, tin, off = oracle.bucketize(c, sp, n_cols, sh["C_in"])
+        assert off.tolist() == case["off"]
+        assert cin.tolist() == case["cin"]
+        assert tin.tolist() == case["tin"]
+        got, ep, eb = oracle.integrate(c, cin, tin, off, np.array(case["W"], np.float32),
+                                       np.array(case["bias"], np.float32),
+                                       np.array(case["alpha"], np.float32),
+                                       np.array(case["theta"], np.float32), case["t_min"], **sh)
+        assert got.tolist() == case["out"]
+
+
+# ---------------------------------------------------------------- CuLIF
+def test_culif_fc_matches_steps():
+    rng = np.random.default_rng(11)
+    T, delta, N, F, O = 64, 32, 3, 40, 5
+    sp = np.where(rng.random(N * F) < 0.5, rng.integers(0, T, N * F), 9999).astype(np.float32)
+    w = (rng.standard_normal(O * F) * 0.4).astype(np.float32)
+    cin = np.zeros(N * F, np.int32)
+    tin = np.zeros(N * F, np.float32)
+    OS = (T + delta - 1) // delta + 1
+    off = np.zeros(N * OS, np.int32)
+    L = oracle.lib()
+    P = oracle._p
+    L.orc_culif_bucketize_fc(P(sp), N, F, T, delta, P(cin), P(tin), P(off), 0)
+    out = np.empty(N * O, np.float32)
+    import ctypes as C
+    L.orc_culif_fc(P(cin), P(tin), P(off), P(out), P(w), N, F, O, T, delta, C.c_float(0.5),
+                   C.c_float(1.0), 0)
+    for n in range(N):
+        for i in range(O):
+            cur = [0.0] * T
+            for j in range(F):
+                t = sp[n * F + j]
+                if t < 9999:
+                    cur[int(t)] = pyref.add32(cur[int(t)], w[i * F + j])
+            I = V = 0.0
+            exp = 9999.0
+            for t in range(T):
+                I = pyref.fma32(I, 0.5, cur[t])
+                V = pyref.add32(V, I)
+                if V >= 1.0:
+                    exp = float(t)
+                    break
+            assert out[n * O + i] == exp

@@ -1,0 +1,92 @@
+// Internal declarations shared by the HIP kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#include "vdttfs.h"
+
+// One retained spike event of the engine's bin-sorted layout: presynaptic
+// index and arrival bin packed in `key` (cin in bits 0..23, bin in 24..31),
+// and the decay-LUT value alpha already gathered for this event.
+struct __align__(8) vd_event {
+    uint32_t key;
+    float alpha;
+};
+
+struct vdttfs_ctx {
+    vdttfs_consts c;
+    int NC;  // ceil(T/delta)
+    int OS;  // NC + 1
+    int device;
+    hipStream_t stream;
+    // reference-layout bucket scratch (launch wrappers)
+    void* ref_cin;
+    void* ref_tin;
+    void* ref_off;
+    size_t ref_elems, ref_cols;
+    // engine bin-layout scratch
+    void* bin_ev;
+    void* bin_off;
+    size_t bin_elems, bin_cols;
+    unsigned long long* d_counters;  // 4 x u64
+};
+
+namespace vdttfs {
+
+int set_error(int code, const char* fmt, ...);
+int hip_error(hipError_t e, const char* what, int line);
+int check_ctx(vdttfs_ctx* ctx);
+
+#define VD_HIP(call)                                                        \
+    do {                                                                    \
+        hipError_t vd_e_ = (call);                                          \
+        if (vd_e_ != hipSuccess) return vdttfs::hip_error(vd_e_, #call, __LINE__); \
+    } while (0)
+
+#define VD_TRY(expr)                  \
+    do {                              \
+        int vd_rc_ = (expr);          \
+        if (vd_rc_ != VDTTFS_OK) return vd_rc_; \
+    } while (0)
+
+// scratch management (ctx-owned, grown on demand; hipMalloc outside any
+// timed region of the engine, which pre-sizes at net creation)
+int ensure_ref_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols);
+int ensure_bin_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols);
+
+// ---- kernel launchers (stream-ordered on ctx->stream) ----
+int launch_encode_log(vdttfs_ctx* ctx, const float* img, float* out, int64_t n, float tc, float td);
+int launch_encode_linear(vdttfs_ctx* ctx, const float* img, float* out, int64_t n);
+
+int launch_bucketize_ref(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
+                         int32_t* out_cin, float* out_tin, int32_t* out_off);
+int launch_bucketize_bins(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
+                          const float* alpha, vd_event* out_ev, int32_t* out_off,
+                          unsigned long long* n_ev_counter);
+
+int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const float* tin,
+                         const int32_t* off, const float* W, const float* bias,
+                         const float* alpha, const float* theta, int t_min, int B, int H_in,
+                         int W_in, int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
+                         int is_fc);
+
+struct IntegShape {
+    int B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+};
+// counters: nullable; [0] += eproc, [1] += ebin
+int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
+                          const float* W, const float* bias, const float* theta, int t_min,
+                          const IntegShape& s, unsigned long long* counters);
+
+int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
+int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,
+                   const float* alpha, int B, int C_in, int C_out);
+int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int argmax);
+
+// shape validation shared by the entry points
+int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s);
+
+}  // namespace vdttfs

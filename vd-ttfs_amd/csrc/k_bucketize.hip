@@ -1,0 +1,187 @@
+// Arrival-time counting sort of each input column's spikes (the reference's
+// k_bucketize, T1V:45-80 / T2V:45-81), rebuilt for wave64:
+//  * a wave owns 64/SEG columns, SEG = next_pow2(C_in) capped at 64, so even
+//    C_in = 1 or 3 keeps every lane busy and reads stay coalesced;
+//  * pass 1 builds a wave-private histogram in LDS (order-free atomics);
+//  * a wave prefix scan turns it into bucket offsets, written coalesced;
+//  * pass 2 scatters stably: lanes sharing a bucket are ranked in lane
+//    (= ascending cin) order with ballot + popcount, one distinct bucket per
+//    iteration, so the output order is exactly the reference's serial loop.
+// Two output layouts share the code:
+//  * REF  - buckets are Delta-wide chunks, events (cin, raw t): bit-exact
+//           reference layout (off[col*(NC+1)+c], cin/tin[col*C_in+pos]);
+//  * BINS - buckets are single arrival bins (T+1 offsets per column), events
+//           packed as (cin | bin<<24, alpha[idx]) for the engine's integrator.
+#include "common.h"
+#include "wave.h"
+
+namespace vdttfs {
+namespace {
+
+struct BktParams {
+    int T;
+    float tfs;
+    int delta;
+    int alpha_by_time;
+};
+
+template <bool BINS>
+__global__ __launch_bounds__(256) void k_bucketize(
+    const float* __restrict__ in, int64_t n_cols, int c_in, int seg_log2, BktParams p, int nb,
+    int32_t* __restrict__ out_cin, float* __restrict__ out_tin, vd_event* __restrict__ out_ev,
+    const float* __restrict__ alpha, int32_t* __restrict__ out_off,
+    unsigned long long* __restrict__ n_ev_counter) {
+    extern __shared__ int lds[];
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int seg_size = 1 << seg_log2;
+    const int cpw = 64 >> seg_log2;  // columns per wave
+    const int OS = nb + 1;
+    int* cur = lds + wave * cpw * OS;
+    const int64_t col0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave) * cpw;
+    if (col0 >= n_cols) return;  // uniform per wave
+    const int seg = lane >> seg_log2;
+    const int l = lane & (seg_size - 1);
+    const int64_t col = col0 + seg;
+    const bool col_ok = col < n_cols;
+    const uint64_t segmask =
+        (seg_size == 64) ? ~0ull : (((1ull << seg_size) - 1ull) << (seg * seg_size));
+    const uint64_t lt = lanemask_lt();
+
+    for (int i = lane; i < cpw * OS; i += 64) cur[i] = 0;
+    wave_sync();
+    const float* src = in + (col_ok ? col : col0) * (int64_t)c_in;
+
+    // pass 1: per-column histogram
+    for (int base = 0; base < c_in; base += seg_size) {
+        const int i = base + l;
+        if (col_ok && i < c_in) {
+            const int tb = arrival_bin(src[i], p.tfs, p.T);
+            if (tb >= 0) atomicAdd(&cur[seg * OS + (BINS ? tb : tb / p.delta)], 1);
+        }
+    }
+    wave_sync();
+
+    // exclusive scan of each column's counts; slot nb receives the total
+    if (cpw == 1) {
+        int run = 0;
+        for (int b0 = 0; b0 < OS; b0 += 64) {
+            const int b = b0 + lane;
+            const int v = (b < nb) ? cur[b] : 0;
+            const int incl = wave_incl_scan(v);
+            if (b < OS) cur[b] = run + incl - v;
+            run += __shfl(incl, 63, 64);
+        }
+    } else if (l == 0 && col_ok) {
+        int run = 0;
+        for (int b = 0; b < nb; ++b) {
+            const int v = cur[seg * OS + b];
+            cur[seg * OS + b] = run;
+            run += v;
+        }
+        cur[seg * OS + nb] = run;
+    }
+    wave_sync();
+
+    // offsets of the wave's columns are one contiguous block
+    {
+        const int64_t ncol_here = (n_cols - col0) < cpw ? (n_cols - col0) : cpw;
+        const int total = (int)ncol_here * OS;
+        for (int i = lane; i < total; i += 64) out_off[col0 * OS + i] = cur[i];
+        if (n_ev_counter != nullptr) {
+            int mine = (l == 0 && col_ok) ? cur[seg * OS + nb] : 0;
+            for (int off = 32; off > 0; off >>= 1) mine += __shfl_xor(mine, off, 64);
+            if (lane == 0) atomicAdd(n_ev_counter, (unsigned long long)mine);
+        }
+    }
+    wave_sync();
+
+    // pass 2: stable scatter
+    for (int base = 0; base < c_in; base += seg_size) {
+        const int i = base + l;
+        float t = 0.0f;
+        int tb = -1;
+        if (col_ok && i < c_in) {
+            t = src[i];
+            tb = arrival_bin(t, p.tfs, p.T);
+        }
+        const int b = (tb < 0) ? -1 : (BINS ? tb : tb / p.delta);
+        bool active = b >= 0;
+        while (true) {
+            const uint64_t act = __ballot(active);
+            if (act == 0) break;
+            const int first = __ffsll((unsigned long long)act) - 1;
+            const int bsel = __shfl(b, first, 64);
+            const bool mine = active && (b == bsel);
+            const uint64_t ms = __ballot(mine) & segmask;
+            int pos = 0;
+            if (mine) {
+                pos = cur[seg * OS + bsel] + __popcll(ms & lt);
+                const int64_t dst = col * (int64_t)c_in + pos;
+                if (BINS) {
+                    vd_event e;
+                    e.key = (uint32_t)i | ((uint32_t)tb << 24);
+                    e.alpha = alpha[alpha_index(t, tb, p.alpha_by_time, p.T)];
+                    out_ev[dst] = e;
+                } else {
+                    out_cin[dst] = i;
+                    out_tin[dst] = t;
+                }
+            }
+            wave_sync();
+            if (mine && (ms & lt) == 0) cur[seg * OS + bsel] += __popcll(ms);
+            wave_sync();
+            active = active && !mine;
+        }
+    }
+}
+
+int seg_log2_for(int c_in) {
+    int s = 0;
+    while ((1 << s) < c_in && s < 6) ++s;
+    return s;
+}
+
+template <bool BINS>
+int launch_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in, int nb,
+                     int32_t* out_cin, float* out_tin, vd_event* out_ev, const float* alpha,
+                     int32_t* out_off, unsigned long long* n_ev_counter) {
+    if (n_cols <= 0 || c_in <= 0) return VDTTFS_OK;
+    // one segment per column; widen segments (fewer columns per wave) until
+    // the wave's bucket counters fit 16 KB, so 4 waves stay within 64 KB
+    int sl = seg_log2_for(c_in);
+    while (sl < 6 && (size_t)(64 >> sl) * (nb + 1) * sizeof(int) > 16 * 1024) ++sl;
+    const int cpw = 64 >> sl;
+    const size_t wave_lds = (size_t)cpw * (nb + 1) * sizeof(int);
+    const int waves = 4;
+    if (wave_lds * waves > 64 * 1024)
+        return set_error(VDTTFS_E_UNSUPPORTED, "bucketize: %d buckets exceed LDS", nb);
+    const int64_t n_waves = (n_cols + cpw - 1) / cpw;
+    const int64_t blocks = (n_waves + waves - 1) / waves;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "bucketize: grid too large");
+    BktParams p{ctx->c.T, ctx->c.tfs, ctx->c.delta, ctx->c.alpha_by_time};
+    hipLaunchKernelGGL(k_bucketize<BINS>, dim3((unsigned)blocks), dim3(64 * waves),
+                       wave_lds * waves, ctx->stream, in, n_cols, c_in, sl, p, nb, out_cin,
+                       out_tin, out_ev, alpha, out_off, n_ev_counter);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+}  // namespace
+
+int launch_bucketize_ref(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
+                         int32_t* out_cin, float* out_tin, int32_t* out_off) {
+    return launch_bucketize<false>(ctx, in, n_cols, c_in, ctx->NC, out_cin, out_tin, nullptr,
+                                   nullptr, out_off, nullptr);
+}
+
+int launch_bucketize_bins(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
+                          const float* alpha, vd_event* out_ev, int32_t* out_off,
+                          unsigned long long* n_ev_counter) {
+    if (c_in >= (1 << 24))
+        return set_error(VDTTFS_E_UNSUPPORTED, "bucketize: C_in %d >= 2^24", c_in);
+    return launch_bucketize<true>(ctx, in, n_cols, c_in, ctx->c.T, nullptr, nullptr, out_ev,
+                                  alpha, out_off, n_ev_counter);
+}
+
+}  // namespace vdttfs

@@ -1,0 +1,168 @@
+// Element-wise and readout kernels around the integrator: spike encoders
+// (k_encode_image, T1V:32-42), 2x2 min pool (k_pooling, T1V:164-181 /
+// T2V:192-209), output membrane potential (k_layer_vmem, T2V:172-190) and
+// the argmin / argmax readouts (T1V:312-319, T2V:389-396).  All are
+// grid-stride over a flat index, 256 threads per block.
+#include "common.h"
+#include "wave.h"
+
+namespace vdttfs {
+namespace {
+
+constexpr int kThreads = 256;
+
+unsigned grid_for(int64_t n) {
+    int64_t b = (n + kThreads - 1) / kThreads;
+    if (b > 1 << 20) b = 1 << 20;  // grid-stride beyond this
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+// T1V:32-42.  nvcc contracts td - tc*logf(x) into one fma.
+__global__ void k_encode_log(const float* __restrict__ img, float* __restrict__ out, int64_t n,
+                             float tc, float td, int T) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float pixel = img[i];
+        if ((double)pixel < 1e-5) {
+            out[i] = kInfTime;
+            continue;
+        }
+        float tf = __builtin_fmaf(-tc, logf(pixel), td);
+        if (tf < 0.0f) tf = 0.0f;
+        const float ts = ceilf(tf);
+        out[i] = (ts > (float)T) ? kInfTime : ts;
+    }
+}
+
+// Synthetic configs: t = floor(T*(1-x)); x < 1e-5 -> no spike.
+__global__ void k_encode_linear(const float* __restrict__ img, float* __restrict__ out, int64_t n,
+                                int T) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = img[i];
+        out[i] = ((double)x < 1e-5) ? kInfTime : floorf((float)T * (1.0f - x));
+    }
+}
+
+// T1V:164-181 / T2V:192-209 (NHWC)
+__global__ void k_pool_min(const float* __restrict__ in, float* __restrict__ out, int B, int H_in,
+                           int W_in, int C) {
+    const int H_out = H_in / 2, W_out = W_in / 2;
+    const int64_t per = (int64_t)H_out * W_out * C;
+    const int64_t n = (int64_t)B * per;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = idx / per, local = idx % per;
+        const int c = (int)(local % C);
+        const int w = (int)((local / C) % W_out);
+        const int h = (int)(local / C / W_out);
+        float m = kInfTime;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int hh = h * 2 + i, ww = w * 2 + j;
+                if (hh < H_in && ww < W_in) {
+                    const float t = in[b * ((int64_t)H_in * W_in * C) + ((int64_t)hh * W_in + ww) * C + c];
+                    if (t < m) m = t;
+                }
+            }
+        out[idx] = m;
+    }
+}
+
+// T2V:172-190: acc over inputs in cin order, then + bias.
+__global__ void k_fc_vmem(const float* __restrict__ in, float* __restrict__ out,
+                          const float* __restrict__ W, const float* __restrict__ bias,
+                          const float* __restrict__ alpha, int B, int C_in, int C_out, int T,
+                          float tfs) {
+    const int64_t n = (int64_t)B * C_out;
+    for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < n;
+         id += (int64_t)gridDim.x * blockDim.x) {
+        const int img = (int)(id / C_out), c = (int)(id % C_out);
+        const float* src = in + (int64_t)img * C_in;
+        float acc = 0.0f;
+        for (int i = 0; i < C_in; ++i) {
+            const float t_in = src[i];
+            if (t_in < kInfTime && (t_in - tfs) <= (float)T) {
+                int ti = (int)t_in;
+                ti = ti < 0 ? 0 : (ti > T ? T : ti);
+                acc = __builtin_fmaf(W[(int64_t)i * C_out + c], alpha[ti], acc);
+            }
+        }
+        out[id] = acc + bias[c];
+    }
+}
+
+// T1V:312-319 (argmin from INF, strict <, -1 if nothing fired) and
+// T2V:389-396 (argmax from -1e9, strict >).
+__global__ void k_readout(const float* __restrict__ out, int B, int C, int32_t* __restrict__ pred,
+                          int argmax) {
+    for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < B; b += gridDim.x * blockDim.x) {
+        const float* row = out + (int64_t)b * C;
+        int p = -1;
+        if (argmax) {
+            float m = -1e9f;
+            for (int i = 0; i < C; ++i)
+                if (row[i] > m) {
+                    m = row[i];
+                    p = i;
+                }
+        } else {
+            float m = kInfTime;
+            for (int i = 0; i < C; ++i)
+                if (row[i] < m) {
+                    m = row[i];
+                    p = i;
+                }
+        }
+        pred[b] = p;
+    }
+}
+
+}  // namespace
+
+int launch_encode_log(vdttfs_ctx* ctx, const float* img, float* out, int64_t n, float tc, float td) {
+    if (n <= 0) return VDTTFS_OK;
+    hipLaunchKernelGGL(k_encode_log, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, img, out, n,
+                       tc, td, ctx->c.T);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_encode_linear(vdttfs_ctx* ctx, const float* img, float* out, int64_t n) {
+    if (n <= 0) return VDTTFS_OK;
+    hipLaunchKernelGGL(k_encode_linear, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, img, out,
+                       n, ctx->c.T);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C) {
+    const int64_t n = (int64_t)B * (H_in / 2) * (W_in / 2) * C;
+    if (n <= 0) return VDTTFS_OK;
+    hipLaunchKernelGGL(k_pool_min, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, in, out, B,
+                       H_in, W_in, C);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,
+                   const float* alpha, int B, int C_in, int C_out) {
+    const int64_t n = (int64_t)B * C_out;
+    if (n <= 0) return VDTTFS_OK;
+    hipLaunchKernelGGL(k_fc_vmem, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, in, out, W,
+                       bias, alpha, B, C_in, C_out, ctx->c.T, ctx->c.tfs);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int argmax) {
+    if (B <= 0) return VDTTFS_OK;
+    hipLaunchKernelGGL(k_readout, dim3(grid_for(B)), dim3(kThreads), 0, ctx->stream, out, B, C, pred,
+                       argmax);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+}  // namespace vdttfs

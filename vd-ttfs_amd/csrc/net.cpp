@@ -1,0 +1,388 @@
+// Network engine: the sequencing of the reference driver main()s
+// (T1V:286-319, T2V:337-396) as one stream-ordered forward with no host
+// synchronisation.  Differences from the reference drivers, all
+// result-neutral: weights, biases and every layer's LUTs are uploaded once at
+// creation and stay resident (update_LUTs per layer per batch becomes a
+// pointer switch); each layer has its own output map; bucket scratch is
+// pre-sized here, so forward() allocates nothing.
+#include <cmath>
+#include <cstdlib>
+#include <new>
+#include <vector>
+
+#include "common.h"
+
+using namespace vdttfs;
+
+namespace {
+
+struct NetLayer {
+    vdttfs_layer_desc d{};
+    float* W = nullptr;
+    float* bias = nullptr;
+    float* alpha = nullptr;
+    float* theta = nullptr;
+    float* out = nullptr;
+    int64_t out_elems = 0;
+    int64_t cols = 0;  // bucket columns (CONV/FC)
+    int cin_col = 0;   // elements per column
+    int t_min = 0;
+};
+
+struct TimedPair {
+    hipEvent_t a, b;
+    int kind;  // 0 integrate, 1 bucketize
+};
+
+}  // namespace
+
+struct vdttfs_net {
+    vdttfs_ctx* ctx = nullptr;
+    std::vector<NetLayer> L;
+    int B = 0;
+    int64_t img_elems = 0;
+    int encode_mode = 0;
+    float tc_in = 0, td_in = 0;
+    int readout = 0;
+    float* enc = nullptr;
+    vd_event* ev = nullptr;
+    int32_t* off = nullptr;
+    bool timing = false;
+    std::vector<hipEvent_t> pool;
+    size_t pool_used = 0;
+    std::vector<TimedPair> pending;
+    double ms[2] = {0, 0};
+    int64_t launches[2] = {0, 0};
+};
+
+namespace {
+
+int fail_layer(int i, const char* what) {
+    return set_error(VDTTFS_E_INVALID, "net layer %d: %s", i, what);
+}
+
+int validate(const vdttfs_consts& c, const vdttfs_layer_desc* ls, int n, int64_t img_elems) {
+    int64_t prev_elems = img_elems;
+    int ph = -1, pw = -1, pc = -1;  // previous spatial shape, -1 if flattened
+    for (int i = 0; i < n; ++i) {
+        const vdttfs_layer_desc& d = ls[i];
+        const int64_t in_e = (int64_t)d.H_in * d.W_in * d.C_in;
+        if (d.H_in <= 0 || d.W_in <= 0 || d.C_in <= 0 || d.H_out <= 0 || d.W_out <= 0 || d.C_out <= 0)
+            return fail_layer(i, "non-positive dimension");
+        if (in_e != prev_elems) return fail_layer(i, "input size does not match the previous output");
+        if (d.kind == VDTTFS_LAYER_CONV) {
+            if (ph >= 0 && (d.H_in != ph || d.W_in != pw || d.C_in != pc))
+                return fail_layer(i, "conv input shape does not match the previous map");
+            if (d.K_h <= 0 || d.K_w <= 0) return fail_layer(i, "kernel size");
+            if (c.conv_same_pad) {
+                if (d.H_out != d.H_in || d.W_out != d.W_in || d.K_h % 2 == 0 || d.K_w % 2 == 0)
+                    return fail_layer(i, "same-pad conv needs odd K and H_out == H_in");
+            } else if (d.H_out != d.H_in - d.K_h + 1 || d.W_out != d.W_in - d.K_w + 1) {
+                return fail_layer(i, "valid conv needs H_out = H_in - K_h + 1");
+            }
+            if (!d.kernel || !d.bias) return fail_layer(i, "null weights");
+        } else if (d.kind == VDTTFS_LAYER_FC || d.kind == VDTTFS_LAYER_VMEM) {
+            if (d.H_out != 1 || d.W_out != 1) return fail_layer(i, "fc output must be 1x1xC");
+            if (!d.kernel || !d.bias) return fail_layer(i, "null weights");
+        } else if (d.kind == VDTTFS_LAYER_POOL) {
+            if (d.H_out != d.H_in / 2 || d.W_out != d.W_in / 2 || d.C_out != d.C_in)
+                return fail_layer(i, "pool needs H_out = H_in/2, C_out = C_in");
+        } else {
+            return fail_layer(i, "unknown layer kind");
+        }
+        prev_elems = (int64_t)d.H_out * d.W_out * d.C_out;
+        if (d.kind == VDTTFS_LAYER_FC || d.kind == VDTTFS_LAYER_VMEM) {
+            ph = pw = pc = -1;
+        } else {
+            ph = d.H_out;
+            pw = d.W_out;
+            pc = d.C_out;
+        }
+    }
+    return VDTTFS_OK;
+}
+
+hipEvent_t take_event(vdttfs_net* net) {
+    if (net->pool_used == net->pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        net->pool.push_back(e);
+    }
+    return net->pool[net->pool_used++];
+}
+
+int mark(vdttfs_net* net, hipEvent_t* e) {
+    *e = take_event(net);
+    if (!*e) return set_error(VDTTFS_E_HIP, "hipEventCreate failed");
+    VD_HIP(hipEventRecord(*e, net->ctx->stream));
+    return VDTTFS_OK;
+}
+
+// counters: nullable; when set, per-layer instrumented run
+int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t* eproc,
+                 uint64_t* ebin, uint64_t* n_ev, uint64_t* n_cols) {
+    vdttfs_ctx* ctx = net->ctx;
+    const bool count = eproc || ebin || n_ev;
+    const int64_t n_img = (int64_t)net->B * net->img_elems;
+    if (net->encode_mode == VDTTFS_ENCODE_LOG)
+        VD_TRY(launch_encode_log(ctx, d_img, net->enc, n_img, net->tc_in, net->td_in));
+    else
+        VD_TRY(launch_encode_linear(ctx, d_img, net->enc, n_img));
+    const float* cur = net->enc;
+    for (size_t i = 0; i < net->L.size(); ++i) {
+        NetLayer& l = net->L[i];
+        const vdttfs_layer_desc& d = l.d;
+        if (d.kind == VDTTFS_LAYER_POOL) {
+            VD_TRY(launch_pool_min(ctx, cur, l.out, net->B, d.H_in, d.W_in, d.C_in));
+        } else if (d.kind == VDTTFS_LAYER_VMEM) {
+            VD_TRY(launch_fc_vmem(ctx, cur, l.out, l.W, l.bias, l.alpha, net->B,
+                                  d.H_in * d.W_in * d.C_in, d.C_out));
+        } else {
+            const bool fc = d.kind == VDTTFS_LAYER_FC;
+            IntegShape s{};
+            s.B = net->B;
+            s.is_fc = fc;
+            s.H_in = fc ? 1 : d.H_in;
+            s.W_in = fc ? 1 : d.W_in;
+            s.C_in = l.cin_col;
+            s.H_out = fc ? 1 : d.H_out;
+            s.W_out = fc ? 1 : d.W_out;
+            s.C_out = d.C_out;
+            s.K_h = fc ? 1 : d.K_h;
+            s.K_w = fc ? 1 : d.K_w;
+            s.pad = (fc || !ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
+            if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
+            TimedPair tb{}, ti{};
+            if (net->timing && !count) VD_TRY(mark(net, &tb.a));
+            VD_TRY(launch_bucketize_bins(ctx, cur, l.cols, l.cin_col, l.alpha, net->ev, net->off,
+                                         count ? ctx->d_counters + 2 : nullptr));
+            if (net->timing && !count) {
+                VD_TRY(mark(net, &tb.b));
+                tb.kind = 1;
+                net->pending.push_back(tb);
+                ti.a = tb.b;
+            }
+            VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, l.W, l.bias, l.theta, l.t_min,
+                                         s, count ? ctx->d_counters : nullptr));
+            if (net->timing && !count) {
+                VD_TRY(mark(net, &ti.b));
+                ti.kind = 0;
+                net->pending.push_back(ti);
+            }
+            if (count) {
+                unsigned long long h[4];
+                VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
+                VD_HIP(hipStreamSynchronize(ctx->stream));
+                if (eproc) eproc[i] = h[0];
+                if (ebin) ebin[i] = h[1];
+                if (n_ev) n_ev[i] = h[2];
+                if (n_cols) n_cols[i] = (uint64_t)l.cols;
+            }
+        }
+        if (count && (d.kind == VDTTFS_LAYER_POOL || d.kind == VDTTFS_LAYER_VMEM)) {
+            if (eproc) eproc[i] = 0;
+            if (ebin) ebin[i] = 0;
+            if (n_ev) n_ev[i] = 0;
+            if (n_cols) n_cols[i] = 0;
+        }
+        cur = l.out;
+    }
+    if (d_pred) {
+        const vdttfs_layer_desc& last = net->L.back().d;
+        VD_TRY(launch_readout(ctx, cur, net->B, last.H_out * last.W_out * last.C_out, d_pred,
+                              net->readout == VDTTFS_READOUT_ARGMAX));
+    }
+    return VDTTFS_OK;
+}
+
+void release(vdttfs_net* net) {
+    if (!net) return;
+    if (net->ctx) {
+        (void)hipSetDevice(net->ctx->device);
+        (void)hipStreamSynchronize(net->ctx->stream);
+    }
+    for (NetLayer& l : net->L) {
+        void* p[] = {l.W, l.bias, l.alpha, l.theta, l.out};
+        for (void* q : p)
+            if (q) (void)hipFree(q);
+    }
+    if (net->enc) (void)hipFree(net->enc);
+    if (net->ev) (void)hipFree(net->ev);
+    if (net->off) (void)hipFree(net->off);
+    for (hipEvent_t e : net->pool) (void)hipEventDestroy(e);
+    delete net;
+}
+
+int upload(vdttfs_ctx* ctx, float** dst, const float* src, size_t n) {
+    if (hipMalloc((void**)dst, n * 4 ? n * 4 : 4) != hipSuccess) {
+        *dst = nullptr;
+        return set_error(VDTTFS_E_NOMEM, "device allocation of %zu bytes failed", n * 4);
+    }
+    if (n) VD_HIP(hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+    (void)ctx;
+    return VDTTFS_OK;
+}
+
+int dalloc(void** p, size_t bytes) {
+    if (hipMalloc(p, bytes ? bytes : 4) != hipSuccess) {
+        *p = nullptr;
+        return set_error(VDTTFS_E_NOMEM, "device allocation of %zu bytes failed", bytes);
+    }
+    return VDTTFS_OK;
+}
+
+int create_impl(vdttfs_net* net, const vdttfs_layer_desc* layers, int n) {
+    vdttfs_ctx* ctx = net->ctx;
+    const vdttfs_consts& c = ctx->c;
+    VD_TRY(dalloc((void**)&net->enc, (size_t)net->B * net->img_elems * 4));
+    int64_t max_elems = 1, max_cols = 1;
+    float tc_i = net->tc_in, td_i = net->td_in;
+    std::vector<float> ha(c.T + 1), ht(c.T);
+    net->L.resize(n);
+    for (int i = 0; i < n; ++i) {
+        NetLayer& l = net->L[i];
+        l.d = layers[i];
+        const vdttfs_layer_desc& d = layers[i];
+        l.out_elems = (int64_t)net->B * d.H_out * d.W_out * d.C_out;
+        VD_TRY(dalloc((void**)&l.out, (size_t)l.out_elems * 4));
+        if (d.kind == VDTTFS_LAYER_POOL) continue;
+        const bool fc = d.kind != VDTTFS_LAYER_CONV;
+        const int64_t kel = fc ? (int64_t)d.H_in * d.W_in * d.C_in * d.C_out
+                               : (int64_t)d.K_h * d.K_w * d.C_in * d.C_out;
+        VD_TRY(upload(ctx, &l.W, d.kernel, (size_t)kel));
+        VD_TRY(upload(ctx, &l.bias, d.bias, (size_t)d.C_out));
+        VD_TRY(vdttfs_build_luts_host(&c, tc_i, td_i, d.tc_fire, d.td, ha.data(), ht.data()));
+        VD_TRY(upload(ctx, &l.alpha, ha.data(), ha.size()));
+        VD_TRY(upload(ctx, &l.theta, ht.data(), ht.size()));
+        int t_min = (int)ceilf(d.td);
+        l.t_min = t_min < 0 ? 0 : t_min;
+        tc_i = d.tc_fire;
+        td_i = d.td;
+        l.d.kernel = nullptr;
+        l.d.bias = nullptr;
+        if (d.kind == VDTTFS_LAYER_VMEM) continue;
+        l.cols = fc ? net->B : (int64_t)net->B * d.H_in * d.W_in;
+        l.cin_col = fc ? d.H_in * d.W_in * d.C_in : d.C_in;
+        IntegShape s{};
+        s.B = net->B;
+        s.is_fc = fc;
+        s.H_in = fc ? 1 : d.H_in;
+        s.W_in = fc ? 1 : d.W_in;
+        s.C_in = l.cin_col;
+        s.H_out = fc ? 1 : d.H_out;
+        s.W_out = fc ? 1 : d.W_out;
+        s.C_out = d.C_out;
+        s.K_h = fc ? 1 : d.K_h;
+        s.K_w = fc ? 1 : d.K_w;
+        s.pad = (fc || !c.conv_same_pad) ? 0 : d.K_h / 2;
+        VD_TRY(check_integ_shape(ctx, s));
+        if (l.cols * l.cin_col > max_elems) max_elems = l.cols * l.cin_col;
+        if (l.cols > max_cols) max_cols = l.cols;
+    }
+    for (int i = 0; i < n; ++i) net->L[i].d.kernel = net->L[i].d.bias = nullptr;
+    VD_TRY(dalloc((void**)&net->ev, (size_t)max_elems * sizeof(vd_event)));
+    VD_TRY(dalloc((void**)&net->off, (size_t)max_cols * (c.T + 1) * 4));
+    VD_HIP(hipDeviceSynchronize());
+    return VDTTFS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
+                      int64_t img_elems, int encode_mode, float tc_in, float td_in, int readout,
+                      vdttfs_net** out) {
+    VD_TRY(check_ctx(ctx));
+    if (!out || !layers || n_layers <= 0 || B <= 0 || img_elems <= 0)
+        return set_error(VDTTFS_E_INVALID, "net_create: bad argument");
+    *out = nullptr;
+    if (encode_mode != VDTTFS_ENCODE_LINEAR && encode_mode != VDTTFS_ENCODE_LOG)
+        return set_error(VDTTFS_E_INVALID, "net_create: encode mode %d", encode_mode);
+    if (readout != VDTTFS_READOUT_ARGMIN && readout != VDTTFS_READOUT_ARGMAX)
+        return set_error(VDTTFS_E_INVALID, "net_create: readout %d", readout);
+    VD_TRY(validate(ctx->c, layers, n_layers, img_elems));
+    vdttfs_net* net = new (std::nothrow) vdttfs_net();
+    if (!net) return set_error(VDTTFS_E_NOMEM, "net_create: out of memory");
+    net->ctx = ctx;
+    net->B = B;
+    net->img_elems = img_elems;
+    net->encode_mode = encode_mode;
+    net->tc_in = tc_in;
+    net->td_in = td_in;
+    net->readout = readout;
+    const int rc = create_impl(net, layers, n_layers);
+    if (rc != VDTTFS_OK) {
+        release(net);
+        return rc;
+    }
+    *out = net;
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_destroy(vdttfs_net* net) {
+    release(net);
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_forward(vdttfs_net* net, const float* d_img, int32_t* d_pred) {
+    if (!net || !d_img) return set_error(VDTTFS_E_INVALID, "net_forward: null argument");
+    VD_TRY(check_ctx(net->ctx));
+    return forward_impl(net, d_img, d_pred, nullptr, nullptr, nullptr, nullptr);
+}
+
+int vdttfs_net_layer_output(vdttfs_net* net, int layer, const float** d_out, int64_t* elems) {
+    if (!net || !d_out || layer < 0 || layer >= (int)net->L.size())
+        return set_error(VDTTFS_E_INVALID, "net_layer_output: bad argument");
+    *d_out = net->L[layer].out;
+    if (elems) *elems = net->L[layer].out_elems;
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint64_t* ebin,
+                     uint64_t* n_ev, uint64_t* n_cols) {
+    if (!net || !d_img) return set_error(VDTTFS_E_INVALID, "net_count: null argument");
+    VD_TRY(check_ctx(net->ctx));
+    uint64_t dummy[1];
+    (void)dummy;
+    std::vector<uint64_t> a(net->L.size()), b(net->L.size()), c(net->L.size()), d(net->L.size());
+    VD_TRY(forward_impl(net, d_img, nullptr, a.data(), b.data(), c.data(), d.data()));
+    VD_HIP(hipStreamSynchronize(net->ctx->stream));
+    for (size_t i = 0; i < net->L.size(); ++i) {
+        if (eproc) eproc[i] = a[i];
+        if (ebin) ebin[i] = b[i];
+        if (n_ev) n_ev[i] = c[i];
+        if (n_cols) n_cols[i] = d[i];
+    }
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_set_timing(vdttfs_net* net, int enable) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    net->timing = enable != 0;
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
+                           double* bucket_ms, int64_t* bucket_launches) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    VD_TRY(check_ctx(net->ctx));
+    VD_HIP(hipStreamSynchronize(net->ctx->stream));
+    for (const TimedPair& p : net->pending) {
+        float ms = 0;
+        VD_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+        net->ms[p.kind] += ms;
+        net->launches[p.kind] += 1;
+    }
+    net->pending.clear();
+    net->pool_used = 0;
+    if (integ_ms) *integ_ms = net->ms[0];
+    if (integ_launches) *integ_launches = net->launches[0];
+    if (bucket_ms) *bucket_ms = net->ms[1];
+    if (bucket_launches) *bucket_launches = net->launches[1];
+    net->ms[0] = net->ms[1] = 0;
+    net->launches[0] = net->launches[1] = 0;
+    return VDTTFS_OK;
+}
+
+}  // extern "C"

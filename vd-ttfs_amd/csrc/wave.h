@@ -1,0 +1,56 @@
+// Wave64 helpers for gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vdttfs {
+
+constexpr float kInfTime = 9999.0f;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Orders LDS traffic between lanes of one wave (LDS ops of a wave execute in
+// program order; this keeps the compiler from reordering across the point).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    return (1ull << lane_id()) - 1ull;
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int u = __shfl_up(v, off, 64);
+        if (lane >= off) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Arrival bin of a spike (T1V:58-59 / T2V:59-60): -1 if no spike or outside
+// the window.
+__device__ __forceinline__ int arrival_bin(float t, float tfs, int T) {
+    if (!(t < kInfTime)) return -1;
+    int tb = (int)floorf(t - tfs);
+    if (tb < 0) tb = 0;
+    return tb < T ? tb : -1;
+}
+
+// Decay-LUT index of an event: tb (T1V:128,144) or clamp((int)t,0,T)
+// (T2V:132,150).
+__device__ __forceinline__ int alpha_index(float t, int tb, int alpha_by_time, int T) {
+    if (!alpha_by_time) return tb;
+    int ti = (int)t;
+    return ti < 0 ? 0 : (ti > T ? T : ti);
+}
+
+}  // namespace vdttfs

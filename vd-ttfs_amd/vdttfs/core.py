@@ -1,0 +1,283 @@
+"""Python host-side mirror of the reference driver surface over the C ABI.
+
+Function names and argument meaning follow the reference programs
+(T1V = task1_lenet_mnist/vdttfs_cuda/snn_timesorted_earlyexit.cu,
+ T2V = task2_vgg16_cifar10/vdttfs_cuda/bench_vgg_eventdriven_timesorted_earlyexit.cu):
+``update_LUTs``, ``k_bucketize``, ``k_conv_bucketed``, ``k_pooling``,
+``k_layer_vmem``, ``launch_layer`` / ``launch_conv`` / ``launch_fc`` ...
+Every call runs the HIP kernels of libvdttfs.so; errors raise VdttfsError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import (Consts, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
+                   LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG,
+                   READOUT_ARGMIN, READOUT_ARGMAX)
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().vdttfs_device_count(C.byref(n)))
+    return n.value
+
+
+@dataclass(frozen=True)
+class TaskConsts:
+    """The reference's compile-time macros (T1V:12-19, T2V:12-18)."""
+    T: int                 # TIME_WINDOW
+    tfs: float = 0.0       # TIME_FIRE_START
+    delta: int = 16        # CHUNK
+    vth: float = 1.0       # VTH_INIT
+    alpha_by_time: bool = False  # T2V alpha[clamp((int)t,0,T)] instead of T1V alpha[tb]
+    conv_same_pad: bool = False  # T2V same padding instead of T1V valid
+
+    @property
+    def num_chunks(self) -> int:
+        return (self.T + self.delta - 1) // self.delta
+
+    def to_c(self) -> Consts:
+        return Consts(self.T, self.tfs, self.delta, self.vth, int(self.alpha_by_time),
+                      int(self.conv_same_pad))
+
+
+# Task 1 (LeNet, T1V:12-19) and Task 2 (VGG, T2V:12-18) semantics
+def task1_consts(T=80, delta=16) -> TaskConsts:
+    return TaskConsts(T=T, tfs=0.0, delta=delta, vth=1.0, alpha_by_time=False, conv_same_pad=False)
+
+
+def task2_consts(T=80, delta=8, tfs=40.0) -> TaskConsts:
+    return TaskConsts(T=T, tfs=tfs, delta=delta, vth=1.0, alpha_by_time=True, conv_same_pad=True)
+
+
+def build_luts_host(consts: TaskConsts, tc_integ, td_integ, tc_fire, td_fire):
+    """update_LUTs' tables on the host (T1V:208-216, T2V:236-243)."""
+    a = np.empty(consts.T + 1, np.float32)
+    t = np.empty(consts.T, np.float32)
+    c = consts.to_c()
+    check(lib().vdttfs_build_luts_host(C.byref(c), tc_integ, td_integ, tc_fire, td_fire, _ptr(a),
+                                       _ptr(t)))
+    return a, t
+
+
+class DeviceArray:
+    """A device allocation with a numpy view of its shape/dtype."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        check(lib().vdttfs_dev_alloc(ctx.handle, self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    @property
+    def size(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def upload(self, host: np.ndarray) -> "DeviceArray":
+        h = np.ascontiguousarray(host, dtype=self.dtype)
+        if h.nbytes != self.nbytes:
+            raise ValueError(f"upload of {h.nbytes} bytes into {self.nbytes}-byte buffer")
+        check(lib().vdttfs_h2d(self.ctx.handle, self.ptr, _ptr(h), self.nbytes))
+        return self
+
+    def download(self) -> np.ndarray:
+        h = np.empty(self.shape, self.dtype)
+        check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), self.ptr, self.nbytes))
+        return h
+
+    def fill(self, byte_value: int) -> "DeviceArray":
+        check(lib().vdttfs_memset(self.ctx.handle, self.ptr, byte_value, self.nbytes))
+        return self
+
+    def free(self):
+        if self.ptr is not None and self.ptr.value and self.ctx.handle is not None:
+            check(lib().vdttfs_dev_free(self.ctx.handle, self.ptr))
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """A device context holding the per-task constants and a HIP stream."""
+
+    def __init__(self, consts: TaskConsts, device: int = 0):
+        self.consts = consts
+        h = C.c_void_p()
+        c = consts.to_c()
+        check(lib().vdttfs_create(C.byref(c), device, C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle is not None:
+            lib().vdttfs_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- memory ----
+    def empty(self, shape, dtype=np.float32) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def to_device(self, host: np.ndarray, dtype=None) -> DeviceArray:
+        h = np.ascontiguousarray(host, dtype=dtype or host.dtype)
+        return DeviceArray(self, h.shape, h.dtype).upload(h)
+
+    def synchronize(self):
+        check(lib().vdttfs_synchronize(self.handle))
+
+    # ---- the reference surface ----
+    def update_LUTs(self, d_lut_decay: DeviceArray, d_lut_th: DeviceArray, tc_integ, td_integ,
+                    tc_fire, td_fire):
+        check(lib().vdttfs_update_luts(self.handle, d_lut_decay.ptr, d_lut_th.ptr, tc_integ,
+                                       td_integ, tc_fire, td_fire))
+
+    def encode_image(self, d_img: DeviceArray, d_out: DeviceArray, tc: float, td: float):
+        check(lib().vdttfs_encode_image(self.handle, d_img.ptr, d_out.ptr, d_img.size, tc, td))
+
+    def encode_linear(self, d_img: DeviceArray, d_out: DeviceArray):
+        check(lib().vdttfs_encode_linear(self.handle, d_img.ptr, d_out.ptr, d_img.size))
+
+    def bucketize(self, d_in: DeviceArray, n_cols: int, c_in: int, d_cin: DeviceArray,
+                  d_tin: DeviceArray, d_off: DeviceArray):
+        check(lib().vdttfs_bucketize(self.handle, d_in.ptr, n_cols, c_in, d_cin.ptr, d_tin.ptr,
+                                     d_off.ptr))
+
+    def integrate(self, d_out, d_cin, d_tin, d_off, d_kernel, d_bias, d_alpha, d_theta, t_min, B,
+                  H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, is_fc):
+        check(lib().vdttfs_integrate(self.handle, d_out.ptr, d_cin.ptr, d_tin.ptr, d_off.ptr,
+                                     d_kernel.ptr, d_bias.ptr, d_alpha.ptr, d_theta.ptr, t_min, B,
+                                     H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, int(is_fc)))
+
+    def layer_forward(self, d_out, d_in, d_kernel, d_bias, d_alpha, d_theta, t_min, B, H_in, W_in,
+                      C_in, H_out, W_out, C_out, K_h, K_w, is_fc, count=False):
+        ep = C.c_uint64(0)
+        eb = C.c_uint64(0)
+        check(lib().vdttfs_layer_forward(self.handle, d_out.ptr, d_in.ptr, d_kernel.ptr, d_bias.ptr,
+                                         d_alpha.ptr, d_theta.ptr, t_min, B, H_in, W_in, C_in,
+                                         H_out, W_out, C_out, K_h, K_w, int(is_fc),
+                                         C.byref(ep) if count else None,
+                                         C.byref(eb) if count else None))
+        return (ep.value, eb.value) if count else None
+
+    def pool_min(self, d_in, d_out, B, H_in, W_in, Cc):
+        check(lib().vdttfs_pool_min(self.handle, d_in.ptr, d_out.ptr, B, H_in, W_in, Cc))
+
+    def fc_vmem(self, d_in, d_out, d_kernel, d_bias, d_alpha, B, C_in, C_out):
+        check(lib().vdttfs_fc_vmem(self.handle, d_in.ptr, d_out.ptr, d_kernel.ptr, d_bias.ptr,
+                                   d_alpha.ptr, B, C_in, C_out))
+
+    def readout(self, d_out, B, Cc, argmax: bool, d_pred):
+        fn = lib().vdttfs_readout_argmax if argmax else lib().vdttfs_readout_argmin
+        check(fn(self.handle, d_out.ptr, B, Cc, d_pred.ptr))
+
+    # launch wrappers (synchronous, T1V:222-240 / T2V:250-287)
+    def launch_layer(self, d_in, d_out, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, td,
+                     d_kernel, d_bias, d_alpha, d_theta, B, is_fc):
+        check(lib().vdttfs_launch_layer_sync(self.handle, d_in.ptr, d_out.ptr, H_in, W_in, C_in,
+                                             H_out, W_out, C_out, K_h, K_w, td, d_kernel.ptr,
+                                             d_bias.ptr, d_alpha.ptr, d_theta.ptr, B, int(is_fc)))
+
+    def launch_pool(self, d_in, d_out, H_in, W_in, Cc, B):
+        check(lib().vdttfs_launch_pool_sync(self.handle, d_in.ptr, d_out.ptr, H_in, W_in, Cc, B))
+
+    def launch_fc_vmem(self, d_in, d_out, C_in, C_out, d_kernel, d_bias, d_alpha, B):
+        check(lib().vdttfs_launch_fc_vmem_sync(self.handle, d_in.ptr, d_out.ptr, C_in, C_out,
+                                               d_kernel.ptr, d_bias.ptr, d_alpha.ptr, B))
+
+
+@dataclass
+class Layer:
+    """One row of the network table (host weights in the reference layout)."""
+    kind: int
+    H_in: int
+    W_in: int
+    C_in: int
+    H_out: int
+    W_out: int
+    C_out: int
+    K_h: int = 1
+    K_w: int = 1
+    kernel: np.ndarray | None = None   # HWIO (conv) / [C_in][C_out] (fc)
+    bias: np.ndarray | None = None
+    tc_fire: float = 16.0
+    td: float = 0.0
+
+    def to_c(self) -> LayerDesc:
+        k = self.kernel
+        b = self.bias
+        fp = C.POINTER(C.c_float)
+        return LayerDesc(self.kind, self.H_in, self.W_in, self.C_in, self.H_out, self.W_out,
+                         self.C_out, self.K_h, self.K_w,
+                         k.ctypes.data_as(fp) if k is not None else fp(),
+                         b.ctypes.data_as(fp) if b is not None else fp(),
+                         self.tc_fire, self.td)
+
+
+class Net:
+    """The engine: encode -> layers -> readout, weights and LUTs resident."""
+
+    def __init__(self, ctx: Context, layers: list[Layer], B: int, img_elems: int,
+                 encode_mode=ENCODE_LINEAR, tc_in=16.0, td_in=0.0, readout=READOUT_ARGMIN):
+        self.ctx = ctx
+        self.layers = layers
+        self.B = B
+        for l in layers:
+            if l.kernel is not None:
+                l.kernel = np.ascontiguousarray(l.kernel, np.float32)
+            if l.bias is not None:
+                l.bias = np.ascontiguousarray(l.bias, np.float32)
+        arr = (LayerDesc * len(layers))(*[l.to_c() for l in layers])
+        h = C.c_void_p()
+        check(lib().vdttfs_net_create(ctx.handle, arr, len(layers), B, img_elems, encode_mode,
+                                      tc_in, td_in, readout, C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle is not None:
+            lib().vdttfs_net_destroy(self.handle)
+            self.handle = None
+
+    def forward(self, d_img: DeviceArray, d_pred: DeviceArray | None = None):
+        check(lib().vdttfs_net_forward(self.handle, d_img.ptr, d_pred.ptr if d_pred else None))
+
+    def layer_output(self, i: int) -> np.ndarray:
+        p = C.c_void_p()
+        n = C.c_int64()
+        check(lib().vdttfs_net_layer_output(self.handle, i, C.byref(p), C.byref(n)))
+        h = np.empty(n.value, np.float32)
+        check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), p, h.nbytes))
+        return h
+
+    def count(self, d_img: DeviceArray):
+        n = len(self.layers)
+        arrs = [(C.c_uint64 * n)() for _ in range(4)]
+        check(lib().vdttfs_net_count(self.handle, d_img.ptr, *arrs))
+        return [np.array(list(a), dtype=np.uint64) for a in arrs]
+
+    def set_timing(self, on: bool):
+        check(lib().vdttfs_net_set_timing(self.handle, int(on)))
+
+    def read_timing(self):
+        im, bm = C.c_double(), C.c_double()
+        il, bl = C.c_int64(), C.c_int64()
+        check(lib().vdttfs_net_read_timing(self.handle, C.byref(im), C.byref(il), C.byref(bm),
+                                           C.byref(bl)))
+        return im.value, il.value, bm.value, bl.value
