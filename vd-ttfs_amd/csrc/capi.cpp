@@ -80,6 +80,23 @@ int ensure_bin_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols) {
     return VDTTFS_OK;
 }
 
+int ensure_merge_scratch(vdttfs_ctx* ctx, size_t list_elems, size_t bstart_elems) {
+    if (list_elems > ctx->mrg_list_elems || bstart_elems > ctx->mrg_bstart_elems || !ctx->mrg_list) {
+        VD_HIP(hipStreamSynchronize(ctx->stream));
+        size_t e = list_elems > ctx->mrg_list_elems ? list_elems : ctx->mrg_list_elems;
+        size_t b = bstart_elems > ctx->mrg_bstart_elems ? bstart_elems : ctx->mrg_bstart_elems;
+        size_t h1 = 0, h2 = 0;
+        if (ctx->mrg_list) VD_HIP(hipFree(ctx->mrg_list));
+        if (ctx->mrg_bstart) VD_HIP(hipFree(ctx->mrg_bstart));
+        ctx->mrg_list = ctx->mrg_bstart = nullptr;
+        VD_TRY(grow(&ctx->mrg_list, &h1, e * sizeof(int2)));
+        VD_TRY(grow(&ctx->mrg_bstart, &h2, b * 4));
+        ctx->mrg_list_elems = e;
+        ctx->mrg_bstart_elems = b;
+    }
+    return VDTTFS_OK;
+}
+
 static int check_consts(const vdttfs_consts* c) {
     if (!c) return set_error(VDTTFS_E_INVALID, "null constants");
     if (c->T < 1 || c->T > 255)
@@ -140,7 +157,8 @@ int vdttfs_destroy(vdttfs_ctx* ctx) {
     if (!ctx) return VDTTFS_OK;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    void* bufs[] = {ctx->ref_cin, ctx->ref_tin, ctx->ref_off, ctx->bin_ev, ctx->bin_off, ctx->d_counters};
+    void* bufs[] = {ctx->ref_cin, ctx->ref_tin,    ctx->ref_off,   ctx->bin_ev,
+                    ctx->bin_off, ctx->mrg_list, ctx->mrg_bstart, ctx->d_counters};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     (void)hipStreamDestroy(ctx->stream);
@@ -297,12 +315,16 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
         return set_error(VDTTFS_E_INVALID, "layer_forward: null buffer");
     const int64_t cols = is_fc ? B : (int64_t)B * H_in * W_in;
     VD_TRY(ensure_bin_scratch(ctx, (size_t)cols * C_in, (size_t)cols));
+    const int64_t n_pix = is_fc ? B : (int64_t)B * H_out * W_out;
+    const int64_t cap = merged_list_cap(s);
+    VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     const bool count = eproc || ebin;
     if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
     VD_TRY(launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, (vd_event*)ctx->bin_ev,
                                  (int32_t*)ctx->bin_off, nullptr));
     VD_TRY(launch_integrate_bins(ctx, d_out, (const vd_event*)ctx->bin_ev,
-                                 (const int32_t*)ctx->bin_off, d_kernel, d_bias, d_lut_th, t_min, s,
+                                 (const int32_t*)ctx->bin_off, (int2*)ctx->mrg_list, cap,
+                                 (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
                                  count ? ctx->d_counters : nullptr));
     if (count) {
         unsigned long long h[4];

@@ -31,6 +31,10 @@ struct vdttfs_ctx {
     void* bin_ev;
     void* bin_off;
     size_t bin_elems, bin_cols;
+    // engine merged per-pixel event lists
+    void* mrg_list;
+    void* mrg_bstart;
+    size_t mrg_list_elems, mrg_bstart_elems;
     unsigned long long* d_counters;  // 4 x u64
 };
 
@@ -56,6 +60,7 @@ int check_ctx(vdttfs_ctx* ctx);
 // timed region of the engine, which pre-sizes at net creation)
 int ensure_ref_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols);
 int ensure_bin_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols);
+int ensure_merge_scratch(vdttfs_ctx* ctx, size_t list_elems, size_t bstart_elems);
 
 // ---- kernel launchers (stream-ordered on ctx->stream) ----
 int launch_encode_log(vdttfs_ctx* ctx, const float* img, float* out, int64_t n, float tc, float td);
@@ -76,10 +81,15 @@ int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const 
 struct IntegShape {
     int B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
 };
-// counters: nullable; [0] += eproc, [1] += ebin
+// Entries per pixel of the merged event list (receptive events + padding).
+int merged_list_cap(const IntegShape& s);
+// Engine integrator over the bin layout: merge per pixel, then stream.
+// list/bstart: merged-list scratch of n_pix*list_cap entries and
+// n_pix*(T+1) bin starts.  counters: nullable; [0] += eproc, [1] += ebin.
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
-                          const float* W, const float* bias, const float* theta, int t_min,
-                          const IntegShape& s, unsigned long long* counters);
+                          int2* list, int64_t list_cap, int32_t* bstart, const float* W,
+                          const float* bias, const float* theta, int t_min, const IntegShape& s,
+                          unsigned long long* counters);
 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
 int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,

@@ -8,14 +8,17 @@
 // below keep exactly that per-bin order, so their output is bit-identical to
 // the reference for every chunk width (chunking only regroups whole bins).
 //
-// k_integrate_wave (engine path): one wave64 per (output pixel, 64-wide
-// c_out block); lanes are c_out, so every event is wave-uniform and each
-// weight gather is one coalesced 256-byte row segment.  Per chunk the wave
-// merges the receptive columns' bin-sorted lists into (bin, column, cin)
-// order in LDS using a closed-form position table, then streams the merged
-// list in batches of 8 independent gathers, finalising one bin at a time;
-// lanes that fired are masked off (no fetch) and the wave leaves as soon as
-// its ballot of live lanes is empty.
+// Engine path, two kernels per layer:
+//  k_merge  - one wave per output pixel: the in-bounds receptive columns'
+//             bin-sorted event lists are merged into (bin, column, cin)
+//             order with a closed-form position table and written to HBM as
+//             {weight-row byte offset, alpha} pairs plus T+1 bin starts.
+//  k_stream - one wave64 per (output pixel, c_out block); lanes are c_out, so
+//             each event is wave-uniform: the list is read through the scalar
+//             cache 8 events at a time and every weight gather is one
+//             coalesced row segment (dword or dwordx4 per lane).  Bins are
+//             closed between fmas; lanes that fired stop fetching and the wave
+//             leaves once its ballot of live lanes is empty.
 //
 // k_integrate_generic: one thread per neuron, the reference loop nest over
 // either the reference bucket layout (drop-in) or the engine's bin layout
@@ -26,113 +29,40 @@
 namespace vdttfs {
 namespace {
 
-struct WaveArgs {
-    float* out;
-    const vd_event* ev;
-    const int32_t* off;
-    const float* W;
-    const float* bias;
-    const float* theta;
-    unsigned long long* counters;
-    int64_t n_units;
-    int T, D, t_min;
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
-    int n_cblk, nk_max, pmax;
-    int lds_wave_ints, lds_flat_off;
+constexpr int kBlockBins = 64;  // arrival bins handled per table / per VGPR of bin starts
+constexpr int kListPad = 8;     // zeroed entries after each pixel's merged list
+constexpr int kMergeWaves = 4;
+
+// ---------------------------------------------------------------------------
+// k_merge: one wave per output pixel.  The in-bounds receptive columns' bin
+// lists are merged into (bin, column, cin) order -- the per-bin fma order of
+// the reference -- with a closed-form position table: event i of column k in
+// bin t lands at D[k][t] + i, D[k][t] = sum_{k'<k} O_k'[t+1] + sum_{k'>k} O_k'[t]
+// (O_k = the column's bin offsets).  Entries are (weight-row byte offset,
+// alpha bits); bstart[pix][t] is the merged start of bin t.  The list is read
+// by every c_out block of the pixel, so it is built once.
+struct MergeArgs {
+    int2* list;            // [n_pix][cap]
+    int32_t* bstart;       // [n_pix][T+1]
+    const vd_event* ev;    // bin layout [n_cols][C_in]
+    const int32_t* off;    // [n_cols][T+1]
+    int64_t n_pix;
+    int64_t cap;
+    int T;
+    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad, is_fc;
+    int rowbytes;          // C_out * 4
 };
 
-struct WaveLds {
-    int* kcol;  // [nk_max] column index of each in-bounds receptive column
-    int* krow;  // [nk_max] byte offset of its (kh,kw) weight plane
-    int* kcum;  // [nk_max+1] exclusive prefix of column run lengths
-    int* otab;  // [nk_max][D+1] bin offsets O_k[t0+d]
-    int* dtab;  // [nk_max][D] merged-position bases
-    int* bst;   // [D+1] bin starts in merged order
-    int2* flat; // [pmax] merged events: (weight byte offset, alpha bits)
-};
-
-// Merge the events of bins [d0,d1) of the current chunk into lds.flat.
-// multi: positions from the table (whole bins); otherwise a single bin whose
-// merged order equals the column-major order, windowed to [lo,hi).
-__device__ __forceinline__ void fill_flat(const WaveArgs& a, const WaveLds& s, int nk, int t0,
-                                          int d0, int d1, int lo, int hi, bool multi,
-                                          int rowbytes) {
+template <int KMAX>
+__global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
+    __shared__ int dtab_all[kMergeWaves][KMAX * kBlockBins];
+    __shared__ int kinfo_all[kMergeWaves][2 * KMAX];
     const int lane = lane_id();
-    const int os = a.D + 1;
-    int len = 0;
-    if (lane < nk) len = s.otab[lane * os + d1] - s.otab[lane * os + d0];
-    const int incl = wave_incl_scan(len);
-    if (lane < nk) s.kcum[lane] = incl - len;
-    wave_sync();
-    const int base = multi ? uniform(s.bst[d0]) : 0;
-    for (int f0 = lo; f0 < hi; f0 += 64) {
-        const int f = f0 + lane;
-        if (f < hi) {
-            int k = 0;
-            for (int kk = 1; kk < nk; ++kk) k += (s.kcum[kk] <= f) ? 1 : 0;
-            const int i = s.otab[k * os + d0] + (f - s.kcum[k]);
-            const vd_event e = a.ev[(int64_t)s.kcol[k] * a.C_in + i];
-            int pos;
-            if (multi) {
-                const int br = (int)(e.key >> 24) - t0;
-                pos = s.dtab[k * a.D + br] + i - base;
-            } else {
-                pos = f - lo;
-            }
-            s.flat[pos] = make_int2(s.krow[k] + (int)(e.key & 0xFFFFFFu) * rowbytes,
-                                    __float_as_int(e.alpha));
-        }
-    }
-    wave_sync();
-}
-
-// acc = fma-chain over merged events [j0, j1), in order.  Only live lanes
-// fetch; the batch of 8 gathers is issued before the first fma.
-__device__ __forceinline__ float stream_events(const WaveArgs& a, const int2* flat, int j0,
-                                               int j1, float acc, bool live, uint32_t row_lane) {
-    if (live) {
-        const char* Wb = reinterpret_cast<const char*>(a.W);
-        for (int j = j0; j < j1; j += 8) {
-            const int n = j1 - j;
-            float w[8], al[8];
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                const int2 v = flat[j + (g < n ? g : n - 1)];
-                al[g] = __int_as_float(v.y);
-                w[g] = *reinterpret_cast<const float*>(Wb + ((uint32_t)v.x + row_lane));
-            }
-#pragma unroll
-            for (int g = 0; g < 8; ++g)
-                if (g < n) acc = __builtin_fmaf(w[g], al[g], acc);
-        }
-    }
-    return acc;
-}
-
-template <bool COUNT>
-__global__ __launch_bounds__(256) void k_integrate_wave(WaveArgs a) {
-    extern __shared__ int lds_all[];
-    const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
-    const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
-    if (unit >= a.n_units) return;  // uniform per wave
-
-    int* L = lds_all + wave * a.lds_wave_ints;
-    WaveLds s;
-    s.kcol = L;
-    s.krow = s.kcol + a.nk_max;
-    s.kcum = s.krow + a.nk_max;
-    s.otab = s.kcum + a.nk_max + 1;
-    s.dtab = s.otab + a.nk_max * (a.D + 1);
-    s.bst = s.dtab + a.nk_max * a.D;
-    s.flat = reinterpret_cast<int2*>(L + a.lds_flat_off);
-
-    const int cb = (int)(unit % a.n_cblk);
-    const int64_t pix = unit / a.n_cblk;
-    const int c = cb * 64 + lane;
-    const bool lane_ok = c < a.C_out;
-    const uint32_t row_lane = (uint32_t)(lane_ok ? c : 0) * 4u;
-    const int rowbytes = a.C_out * 4;
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
+    if (pix >= a.n_pix) return;  // uniform per wave
+    int* dtab = dtab_all[wave];
+    int* kinfo = kinfo_all[wave];
 
     int img, h_out = 0, w_out = 0;
     if (a.is_fc) {
@@ -143,14 +73,13 @@ __global__ __launch_bounds__(256) void k_integrate_wave(WaveArgs a) {
         h_out = (int)(q % a.H_out);
         img = (int)(q / a.H_out);
     }
-
-    // in-bounds receptive columns in (kh, kw) order
+    // in-bounds receptive columns, compacted in (kh, kw) order
     int nk;
     if (a.is_fc) {
         nk = 1;
         if (lane == 0) {
-            s.kcol[0] = img;
-            s.krow[0] = 0;
+            kinfo[0] = img;
+            kinfo[KMAX] = 0;
         }
     } else {
         bool v = false;
@@ -165,114 +94,335 @@ __global__ __launch_bounds__(256) void k_integrate_wave(WaveArgs a) {
         nk = __popcll(m);
         if (v) {
             const int slot = __popcll(m & lanemask_lt());
-            s.kcol[slot] = col;
-            s.krow[slot] = lane * a.C_in * rowbytes;
+            kinfo[slot] = col;
+            kinfo[KMAX + slot] = lane * a.C_in * a.rowbytes;
         }
     }
     wave_sync();
+    int colk[KMAX], krow[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        colk[k] = (k < nk) ? uniform(kinfo[k]) : 0;
+        krow[k] = (k < nk) ? uniform(kinfo[KMAX + k]) : 0;
+    }
 
-    float carry = lane_ok ? a.bias[c] : 0.0f;
-    float res = kInfTime;
-    bool live = lane_ok;
-    unsigned long long cnt_proc = 0, cnt_bin = 0;
-    const int T = a.T, D = a.D;
-    const int NC = (T + D - 1) / D;
-    const int osb = T + 1;   // offsets per column in the bin layout
-    const int os = D + 1;
-    bool done = false;
-
-    for (int tau = 0; tau < NC && !done; ++tau) {
-        const int t0 = tau * D;
-        const int nb = (T - t0) < D ? (T - t0) : D;
-        // closed-form merge table: for event i of column k in bin t0+d,
-        // merged position = dtab[k][d] + i (relative to the chunk start)
-        int S = 0;
-        for (int k = 0; k < nk; ++k) {
-            const int col = uniform(s.kcol[k]);
-            if (lane < nb) S += a.off[(int64_t)col * osb + t0 + lane];
+    int2* out = a.list + pix * a.cap;
+    int32_t* bs = a.bstart + pix * (int64_t)(a.T + 1);
+    const int osb = a.T + 1;
+    int base = 0;  // merged position of the current block's first event
+    for (int t0 = 0; t0 < a.T; t0 += kBlockBins) {
+        const int nb = (a.T - t0) < kBlockBins ? (a.T - t0) : kBlockBins;
+        int o[KMAX], on[KMAX];
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            o[k] = 0;
+            on[k] = 0;
+            if (k < nk && lane < nb) {
+                const int32_t* ob = a.off + (int64_t)colk[k] * osb + t0 + lane;
+                o[k] = ob[0];
+                on[k] = ob[1];
+            }
         }
+        int S = 0;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) S += o[k];
         const int C0 = uniform(S);
         int A = 0, P = 0;
-        for (int k = 0; k < nk; ++k) {
-            const int col = uniform(s.kcol[k]);
-            int o = 0, on = 0;
-            if (lane < nb) {
-                const int32_t* ob = a.off + (int64_t)col * osb + t0 + lane;
-                o = ob[0];
-                on = ob[1];
+        int st[KMAX], kc[KMAX];  // per column: first event of the block, run start in f order
+        int run = 0;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            st[k] = 0;
+            kc[k] = run;
+            if (k < nk) {
+                P += o[k];
+                if (lane < nb) dtab[k * kBlockBins + lane] = A + (S - P) - C0;
+                A += on[k];
+                st[k] = __builtin_amdgcn_readlane(o[k], 0);
+                run += __builtin_amdgcn_readlane(on[k], nb - 1) - st[k];
             }
-            P += o;
-            if (lane < nb) {
-                s.dtab[k * D + lane] = A + (S - P) - C0;
-                s.otab[k * os + lane] = o;
-            }
-            if (lane == nb - 1) s.otab[k * os + nb] = on;
-            A += on;
         }
-        if (lane < nb) s.bst[lane] = S - C0;
-        if (lane == nb - 1) s.bst[nb] = A - C0;
+        if (lane < nb) bs[t0 + lane] = base + S - C0;
+        const int total = run;  // events of the block
         wave_sync();
-        const uint64_t live_start = __ballot(live);
+        for (int f0 = 0; f0 < total; f0 += 64) {
+            const int f = f0 + lane;
+            if (f < total) {
+                int k = 0, kb = 0, s0 = st[0], col = colk[0], kr = krow[0];
+#pragma unroll
+                for (int kk = 1; kk < KMAX; ++kk)
+                    if (kk < nk && f >= kc[kk]) {
+                        k = kk;
+                        kb = kc[kk];
+                        s0 = st[kk];
+                        col = colk[kk];
+                        kr = krow[kk];
+                    }
+                const int i = s0 + (f - kb);
+                const vd_event e = a.ev[(int64_t)col * a.C_in + i];
+                const int pos = dtab[k * kBlockBins + (int)(e.key >> 24) - t0] + i;
+                out[base + pos] = make_int2(kr + (int)(e.key & 0xFFFFFFu) * a.rowbytes,
+                                            __float_as_int(e.alpha));
+            }
+        }
+        base += total;
+        wave_sync();
+    }
+    if (lane == 0) bs[a.T] = base;
+    // zeroed tail: the stream kernel reads whole groups of 8 entries
+    if (lane < kListPad) out[base + lane] = make_int2(0, 0);
+}
 
-        int d = 0;
-        while (d < nb && !done) {
-            const int sd = uniform(s.bst[d]);
-            int d1 = d + 1;
-            while (d1 < nb && uniform(s.bst[d1 + 1]) - sd <= a.pmax) ++d1;
-            const int n_range = uniform(s.bst[d1]) - sd;
-            if (n_range <= a.pmax) {
-                fill_flat(a, s, nk, t0, d, d1, 0, n_range, true, rowbytes);
-                for (int dd = d; dd < d1; ++dd) {
-                    const int j0 = uniform(s.bst[dd]) - sd, j1 = uniform(s.bst[dd + 1]) - sd;
-                    const float acc = stream_events(a, s.flat, j0, j1, 0.0f, live, row_lane);
-                    if (COUNT) {
-                        cnt_bin += (unsigned long long)(j1 - j0) * __popcll(__ballot(live));
-                        cnt_proc += (unsigned long long)(j1 - j0) * __popcll(live_start);
-                    }
-                    carry = carry + acc;
-                    const int t = t0 + dd;
-                    const float th = a.theta[t];
-                    if (t >= a.t_min && th >= 1e-5f && live && carry >= th) {
-                        res = (float)t;
-                        live = false;
-                    }
-                    if (!COUNT && __ballot(live) == 0) {
-                        done = true;
-                        break;
-                    }
+// ---------------------------------------------------------------------------
+// k_stream: one wave64 per (output pixel, 64-wide c_out block); lanes are
+// c_out.  The merged list is read through the scalar cache 8 events at a time
+// (one s_load_dwordx16), each event costs one buffer_load (the weight row's
+// byte offset goes in soffset, so no per-lane address arithmetic) and one fma
+// with alpha as a scalar operand.  Gathers are batched across bin boundaries;
+// bins are closed between fmas, in order, so every bin's fma chain is the
+// reference's.  Lanes that fired stop fetching; the wave leaves when its
+// ballot of live lanes is empty.
+struct StreamArgs {
+    float* out;
+    const int2* list;
+    const int32_t* bstart;
+    const float* W;
+    const float* bias;
+    const float* theta;
+    unsigned long long* counters;
+    int64_t n_pix;
+    int64_t cap;
+    int T, D, t_min, C_out, n_cblk;
+    int w_bytes;
+};
+
+// Block -> (c_out block, group of 4 output pixels).  Workgroups are dealt to
+// the 8 XCDs round-robin, so when C_out spans a multiple of 8 blocks of 64,
+// XCD x only ever integrates c_out blocks x, x+8, ...: its L2 then holds
+// 1/8 of the layer's weights (the 3x3x512x512 planes are 9.4 MB, an XCD's L2
+// is 4 MB).  With 1, 2 or 4 blocks, b % n_cblk already pins XCD x to block
+// x % n_cblk.
+__device__ __forceinline__ void map_block(int n_cblk, int& cb, int64_t& pg) {
+    const int64_t b = blockIdx.x;
+    if ((n_cblk & 7) == 0) {
+        const int per = n_cblk >> 3;
+        const int64_t q = b >> 3;
+        cb = (int)(b & 7) + 8 * (int)(q % per);
+        pg = q / per;
+    } else {
+        cb = (int)(b % n_cblk);
+        pg = b / n_cblk;
+    }
+}
+
+struct Group8 {
+    int2 v[8];
+};
+
+// VEC consecutive c_out per lane (1, or 4 with dwordx4 gathers: a 64-lane
+// dword gather and a dwordx4 gather cost the same texture-unit time, so four
+// c_out per lane quadruple the bytes per gather).  A c_out block is 64*VEC.
+template <int VEC>
+struct Vf {
+    float v[VEC];
+};
+
+template <int VEC>
+__device__ __forceinline__ Vf<VEC> gather(const __amdgpu_buffer_rsrc_t r, int voff, int row) {
+    Vf<VEC> o;
+    if constexpr (VEC == 1) {
+        o.v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, row, 0));
+    } else {
+        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, row, 0);
+        o.v[0] = __uint_as_float(x.x);
+        o.v[1] = __uint_as_float(x.y);
+        o.v[2] = __uint_as_float(x.z);
+        o.v[3] = __uint_as_float(x.w);
+    }
+    return o;
+}
+
+// Weight gathers from global memory through a buffer resource (VEC
+// consecutive c_out per lane).
+template <int VEC>
+struct GlobalGather {
+    __amdgpu_buffer_rsrc_t r;
+    int voff;
+    __device__ __forceinline__ Vf<VEC> operator()(int row) const { return gather<VEC>(r, voff, row); }
+};
+
+
+// Integrates one output pixel for one c_out block (lane = VEC c_out) from its
+// merged event list and writes the first-spike times.
+template <bool COUNT, int VEC, class G>
+__device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
+                                             const int2* __restrict__ list,
+                                             const int32_t* __restrict__ bstart,
+                                             const float* __restrict__ theta, int64_t pix, int cb,
+                                             const G& gather_w, unsigned long long& cnt_proc,
+                                             unsigned long long& cnt_bin) {
+    const int lane = lane_id();
+    const int c0 = (cb * 64 + lane) * VEC;  // first c_out of this lane
+    bool ok[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) ok[v] = c0 + v < a.C_out;
+    const int2* __restrict__ L = list + pix * a.cap;
+    const int32_t* __restrict__ BS = bstart + pix * (int64_t)(a.T + 1);
+
+    float carry[VEC], res[VEC];
+    bool alive[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+        carry[v] = ok[v] ? a.bias[c0 + v] : 0.0f;
+        res[v] = kInfTime;
+        alive[v] = ok[v];
+    }
+    bool live = ok[0];  // any neuron of the lane still integrating
+    int live_chunk_n = 0;
+    if (COUNT) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(alive[v]));
+    }
+    const int T = a.T, D = a.D;
+    bool done = false;
+    int j = 0;  // next merged event
+
+    for (int t0 = 0; t0 < T && !done; t0 += kBlockBins) {
+        const int nb = (T - t0) < kBlockBins ? (T - t0) : kBlockBins;
+        // lane d keeps bin t0+d's merged start and threshold
+        const int v_bs = lane < nb ? BS[t0 + lane] : 0;
+        const float v_th = lane < nb ? theta[t0 + lane] : 0.0f;
+        const int blk_end = BS[t0 + nb];
+        asm volatile("" ::"v"(v_bs), "v"(v_th));  // complete these loads before streaming
+
+#define VD_BIN_START(b) ((b) < nb ? __builtin_amdgcn_readlane(v_bs, (b)) : blk_end)
+#define VD_FINALIZE(b, acc_)                                                            \
+    do {                                                                                \
+        const int t_ = t0 + (b);                                                        \
+        if (COUNT) {                                                                    \
+            const int n_ = VD_BIN_START((b) + 1) - VD_BIN_START(b);                     \
+            int nl_ = 0;                                                                \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) nl_ += __popcll(__ballot(alive[v])); \
+            cnt_bin += (unsigned long long)n_ * nl_;                                    \
+            cnt_proc += (unsigned long long)n_ * live_chunk_n;                          \
+        }                                                                               \
+        const float th_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), (b))); \
+        const bool can_ = t_ >= a.t_min && th_ >= 1e-5f;                                \
+        _Pragma("unroll") for (int v = 0; v < VEC; ++v) {                               \
+            carry[v] = carry[v] + (acc_)[v];                                            \
+            if (can_ && alive[v] && carry[v] >= th_) {                                  \
+                res[v] = (float)t_;                                                     \
+                alive[v] = false;                                                       \
+            }                                                                           \
+        }                                                                               \
+        live = alive[0];                                                                \
+        _Pragma("unroll") for (int v = 1; v < VEC; ++v) live = live || alive[v];        \
+        const bool chunk_end_ = ((t_ + 1) % D) == 0;                                    \
+        if (COUNT && chunk_end_) {                                                      \
+            live_chunk_n = 0;                                                           \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(alive[v])); \
+        }                                                                               \
+        if (__ballot(live) == 0 && (!COUNT || chunk_end_)) done = true;                 \
+    } while (0)
+
+        int bcur = 0;                    // open bin of this block
+        int bend = VD_BIN_START(1);      // merged end of the open bin
+        float acc[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+        while (j < blk_end) {
+            const int n = (blk_end - j) < 8 ? (blk_end - j) : 8;
+            // one 64-byte scalar load of 8 (row, alpha) pairs; the list is
+            // zero-padded past its end
+            const Group8 grp = *reinterpret_cast<const Group8*>(L + j);
+            const int2* e = grp.v;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(e[g].x), "s"(e[g].y));
+            Vf<VEC> w[8];
+#pragma unroll
+            for (int g = 0; g < 8; ++g)
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) w[g].v[v] = 0.0f;
+            if (live) {
+#pragma unroll
+                for (int g = 0; g < 8; ++g) w[g] = gather_w(e[g].x);
+            }
+            if (bend >= j + n) {
+                // the whole group belongs to the open bin
+                if (n == 8) {
+#pragma unroll
+                    for (int g = 0; g < 8; ++g)
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v)
+                            acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
+                } else {
+#pragma unroll
+                    for (int g = 0; g < 8; ++g)
+                        if (g < n)
+#pragma unroll
+                            for (int v = 0; v < VEC; ++v)
+                                acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
                 }
             } else {
-                // one bin larger than the merged list: stream it in windows
-                float acc = 0.0f;
-                for (int lo = 0; lo < n_range; lo += a.pmax) {
-                    const int hi = (n_range - lo) < a.pmax ? n_range : lo + a.pmax;
-                    fill_flat(a, s, nk, t0, d, d + 1, lo, hi, false, rowbytes);
-                    acc = stream_events(a, s.flat, 0, hi - lo, acc, live, row_lane);
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    if (g >= n) break;
+                    while (bend <= j + g) {
+                        VD_FINALIZE(bcur, acc);
+                        if (done) goto stream_done;
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+                        ++bcur;
+                        bend = VD_BIN_START(bcur + 1);
+                    }
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v)
+                        acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
                 }
-                if (COUNT) {
-                    cnt_bin += (unsigned long long)n_range * __popcll(__ballot(live));
-                    cnt_proc += (unsigned long long)n_range * __popcll(live_start);
-                }
-                carry = carry + acc;
-                const int t = t0 + d;
-                const float th = a.theta[t];
-                if (t >= a.t_min && th >= 1e-5f && live && carry >= th) {
-                    res = (float)t;
-                    live = false;
-                }
-                if (!COUNT && __ballot(live) == 0) done = true;
-                d1 = d + 1;
             }
-            d = d1;
+            j += n;
         }
-        if (COUNT && __ballot(live) == 0) done = true;
+        // close the block's remaining bins (the open one and trailing empty ones)
+        while (bcur < nb) {
+            VD_FINALIZE(bcur, acc);
+            if (done) break;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+            ++bcur;
+        }
+#undef VD_FINALIZE
+#undef VD_BIN_START
     }
-    if (lane_ok) a.out[pix * a.C_out + c] = res;
-    if (COUNT && lane == 0) {
+stream_done:
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+        if (ok[v]) out[pix * a.C_out + c0 + v] = res[v];
+}
+
+template <bool COUNT, int VEC>
+__global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict__ out,
+                                                const int2* __restrict__ list,
+                                                const int32_t* __restrict__ bstart,
+                                                const float* __restrict__ theta) {
+    const int wave = uniform(threadIdx.x >> 6);
+    int cb;
+    int64_t pg;
+    map_block(a.n_cblk, cb, pg);
+    const int64_t pix = pg * 4 + wave;
+    if (pix >= a.n_pix) return;  // uniform per wave
+    const int c0 = (cb * 64 + lane_id()) * VEC;
+    GlobalGather<VEC> g;
+    g.r = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
+    unsigned long long cnt_proc = 0, cnt_bin = 0;
+    stream_pixel<COUNT, VEC>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
+    if (COUNT && lane_id() == 0) {
         atomicAdd(&a.counters[0], cnt_proc);
         atomicAdd(&a.counters[1], cnt_bin);
     }
 }
+
 
 // ---------------------------------------------------------------------------
 struct GenArgs {
@@ -506,61 +656,91 @@ int launch_integrate_generic_bins(vdttfs_ctx* ctx, float* out, const vd_event* e
     return counters ? launch_generic_d<true, true>(ctx, g) : launch_generic_d<true, false>(ctx, g);
 }
 
+int merged_list_cap(const IntegShape& sh) {
+    return (sh.is_fc ? 1 : sh.K_h * sh.K_w) * sh.C_in + kListPad;
+}
+
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
-                          const float* W, const float* bias, const float* theta, int t_min,
-                          const IntegShape& sh, unsigned long long* counters) {
+                          int2* list, int64_t list_cap, int32_t* bstart, const float* W,
+                          const float* bias, const float* theta, int t_min, const IntegShape& sh,
+                          unsigned long long* counters) {
     const int T = ctx->c.T, D = ctx->c.delta;
     const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
     const int64_t wbytes = (int64_t)nk_max * sh.C_in * sh.C_out * 4;
-    const bool wave_ok = sh.C_out >= 32 && D <= 64 && nk_max <= 64 && wbytes < INT64_C(0x7fffffff) &&
+    const bool wave_ok = sh.C_out >= 32 && nk_max <= 25 && wbytes < INT64_C(0x7fffffff) &&
                          sh.C_in < (1 << 24);
     if (!wave_ok)
         return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
-    WaveArgs a{};
+    const int64_t n_pix = (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
+    const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
+    if (!list || !bstart || list_cap < cap)
+        return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
+    MergeArgs m{};
+    m.list = list;
+    m.bstart = bstart;
+    m.ev = ev;
+    m.off = off;
+    m.n_pix = n_pix;
+    m.cap = cap;
+    m.T = T;
+    m.H_in = sh.H_in;
+    m.W_in = sh.W_in;
+    m.C_in = sh.C_in;
+    m.H_out = sh.H_out;
+    m.W_out = sh.W_out;
+    m.K_h = sh.K_h;
+    m.K_w = sh.K_w;
+    m.pad = sh.pad;
+    m.is_fc = sh.is_fc;
+    m.rowbytes = sh.C_out * 4;
+    const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
+    if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    if (nk_max == 1)
+        hipLaunchKernelGGL(k_merge<1>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    else if (nk_max <= 9)
+        hipLaunchKernelGGL(k_merge<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    else
+        hipLaunchKernelGGL(k_merge<25>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    VD_HIP(hipGetLastError());
+
+    StreamArgs a{};
     a.out = out;
-    a.ev = ev;
-    a.off = off;
+    a.list = list;
+    a.bstart = bstart;
     a.W = W;
     a.bias = bias;
     a.theta = theta;
     a.counters = counters;
+    a.n_pix = n_pix;
+    a.cap = cap;
     a.T = T;
     a.D = D;
     a.t_min = t_min;
-    a.H_in = sh.H_in;
-    a.W_in = sh.W_in;
-    a.C_in = sh.C_in;
-    a.H_out = sh.H_out;
-    a.W_out = sh.W_out;
     a.C_out = sh.C_out;
-    a.K_h = sh.K_h;
-    a.K_w = sh.K_w;
-    a.pad = sh.pad;
-    a.is_fc = sh.is_fc;
-    a.n_cblk = (sh.C_out + 63) / 64;
-    a.nk_max = nk_max;
-    a.pmax = 256;
-    const int64_t n_pix = (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
-    a.n_units = n_pix * a.n_cblk;
-    int ints = nk_max * 2 + (nk_max + 1) + nk_max * (D + 1) + nk_max * D + (D + 1);
-    ints = (ints + 1) & ~1;  // 8-byte align the merged list
-    a.lds_flat_off = ints;
-    a.lds_wave_ints = ints + 2 * a.pmax;
+    // 4 c_out per lane once a wave's 64 lanes hold >= 128 c_out
+    const int vec = (sh.C_out >= 128 && sh.C_out % 4 == 0) ? 4 : 1;
+    a.n_cblk = (sh.C_out + 64 * vec - 1) / (64 * vec);
+    a.w_bytes = (int)wbytes;
     const int waves = 4;
-    const size_t lds = (size_t)a.lds_wave_ints * 4 * waves;
-    if (lds > 64 * 1024) {
-        // large Delta x receptive field: the per-neuron kernel has no LDS need
-            return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
-    }
-    const int64_t blocks = (a.n_units + waves - 1) / waves;
+    const int64_t n_pg = (n_pix + waves - 1) / waves;
+    const int64_t blocks = n_pg * a.n_cblk;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-    if (counters)
-        hipLaunchKernelGGL(k_integrate_wave<true>, dim3((unsigned)blocks), dim3(64 * waves), lds,
-                           ctx->stream, a);
-    else
-        hipLaunchKernelGGL(k_integrate_wave<false>, dim3((unsigned)blocks), dim3(64 * waves), lds,
-                           ctx->stream, a);
+#define VD_LAUNCH_STREAM(C, V)                                                              \
+    hipLaunchKernelGGL((k_stream<C, V>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
+                       a, out, (const int2*)list, (const int32_t*)bstart, theta)
+    if (vec == 4) {
+        if (counters)
+            VD_LAUNCH_STREAM(true, 4);
+        else
+            VD_LAUNCH_STREAM(false, 4);
+    } else {
+        if (counters)
+            VD_LAUNCH_STREAM(true, 1);
+        else
+            VD_LAUNCH_STREAM(false, 1);
+    }
+#undef VD_LAUNCH_STREAM
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }

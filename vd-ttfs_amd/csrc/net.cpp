@@ -26,6 +26,7 @@ struct NetLayer {
     int64_t out_elems = 0;
     int64_t cols = 0;  // bucket columns (CONV/FC)
     int cin_col = 0;   // elements per column
+    int64_t list_cap = 0;  // merged-list entries per output pixel
     int t_min = 0;
 };
 
@@ -47,6 +48,8 @@ struct vdttfs_net {
     float* enc = nullptr;
     vd_event* ev = nullptr;
     int32_t* off = nullptr;
+    int2* list = nullptr;
+    int32_t* bstart = nullptr;
     bool timing = false;
     std::vector<hipEvent_t> pool;
     size_t pool_used = 0;
@@ -162,8 +165,9 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
                 net->pending.push_back(tb);
                 ti.a = tb.b;
             }
-            VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, l.W, l.bias, l.theta, l.t_min,
-                                         s, count ? ctx->d_counters : nullptr));
+            VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
+                                         net->bstart, l.W, l.bias, l.theta, l.t_min, s,
+                                         count ? ctx->d_counters : nullptr));
             if (net->timing && !count) {
                 VD_TRY(mark(net, &ti.b));
                 ti.kind = 0;
@@ -209,6 +213,8 @@ void release(vdttfs_net* net) {
     if (net->enc) (void)hipFree(net->enc);
     if (net->ev) (void)hipFree(net->ev);
     if (net->off) (void)hipFree(net->off);
+    if (net->list) (void)hipFree(net->list);
+    if (net->bstart) (void)hipFree(net->bstart);
     for (hipEvent_t e : net->pool) (void)hipEventDestroy(e);
     delete net;
 }
@@ -235,7 +241,7 @@ int create_impl(vdttfs_net* net, const vdttfs_layer_desc* layers, int n) {
     vdttfs_ctx* ctx = net->ctx;
     const vdttfs_consts& c = ctx->c;
     VD_TRY(dalloc((void**)&net->enc, (size_t)net->B * net->img_elems * 4));
-    int64_t max_elems = 1, max_cols = 1;
+    int64_t max_elems = 1, max_cols = 1, max_list = 1, max_bstart = 1;
     float tc_i = net->tc_in, td_i = net->td_in;
     std::vector<float> ha(c.T + 1), ht(c.T);
     net->L.resize(n);
@@ -278,10 +284,16 @@ int create_impl(vdttfs_net* net, const vdttfs_layer_desc* layers, int n) {
         VD_TRY(check_integ_shape(ctx, s));
         if (l.cols * l.cin_col > max_elems) max_elems = l.cols * l.cin_col;
         if (l.cols > max_cols) max_cols = l.cols;
+        l.list_cap = merged_list_cap(s);
+        const int64_t n_pix = (int64_t)net->B * (fc ? 1 : (int64_t)d.H_out * d.W_out);
+        if (n_pix * l.list_cap > max_list) max_list = n_pix * l.list_cap;
+        if (n_pix * (c.T + 1) > max_bstart) max_bstart = n_pix * (c.T + 1);
     }
     for (int i = 0; i < n; ++i) net->L[i].d.kernel = net->L[i].d.bias = nullptr;
     VD_TRY(dalloc((void**)&net->ev, (size_t)max_elems * sizeof(vd_event)));
     VD_TRY(dalloc((void**)&net->off, (size_t)max_cols * (c.T + 1) * 4));
+    VD_TRY(dalloc((void**)&net->list, (size_t)max_list * sizeof(int2)));
+    VD_TRY(dalloc((void**)&net->bstart, (size_t)max_bstart * 4));
     VD_HIP(hipDeviceSynchronize());
     return VDTTFS_OK;
 }
