@@ -9,6 +9,13 @@ integrator's roofline position and a same-host CPU baseline of the
 reference algorithm (oracle/, timed on a bounded sample).
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+  python bench.py --copy-calibration   # known-size copy for FETCH/WRITE_SIZE scaling
+
+roofline.traffic is the integrator's HBM bytes per launch measured with
+rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs and written to
+profiles/integrator_vgg16_b256_traffic.md (by python -m
+vdttfs.rocprof_summary traffic); it is reported only when that file's
+workload line matches the configuration being run, else null.
 """
 from __future__ import annotations
 
@@ -27,6 +34,8 @@ import numpy as np  # noqa: E402
 
 METRIC = "images/sec/GPU for VGG-16 TTFS bs=256; integrator % of HBM peak"
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "integrator_vgg16_b256_traffic.md")
+COPY_FLOATS = 1 << 28  # 1 GiB read + 1 GiB written per calibration dispatch
 
 
 def log(msg: str) -> None:
@@ -51,6 +60,46 @@ def algorithmic_bytes(w, eproc, n_ev, n_cols, B):
     return total, per_layer
 
 
+def workload_key(B, consts) -> str:
+    return f"vgg16 B={B} T={consts.T} delta={consts.delta} tfs={consts.tfs:g}"
+
+
+def measured_traffic(key: str):
+    """(bytes per step, launches per step) from the committed counter summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            text = f.read()
+    except OSError:
+        return None
+    wl = per_step = launches = None
+    for line in text.splitlines():
+        line = line.strip().strip("`")
+        if line.startswith("WORKLOAD="):
+            wl = line[len("WORKLOAD="):].strip()
+        elif line.startswith("TRAFFIC_PER_STEP_BYTES="):
+            kv = dict(t.split("=", 1) for t in line.split())
+            per_step = float(kv["TRAFFIC_PER_STEP_BYTES"])
+            launches = int(kv["LAUNCHES_PER_STEP"])
+    if wl != key or per_step is None:
+        return None
+    return per_step, launches
+
+
+def copy_calibration() -> int:
+    """One elementwise kernel over 2^28 fp32 per dispatch (1 GiB in, 1 GiB out):
+    the known-size reference that FETCH_SIZE / WRITE_SIZE are scaled by."""
+    import torch
+
+    x = torch.empty(COPY_FLOATS, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": COPY_FLOATS * 4,
+                      "copy_calibration_bytes_written": COPY_FLOATS * 4, "dispatches": 3}), flush=True)
+    return 0
+
+
 def cpu_baseline(w, img, gpu_pred, threads_all):
     import oracle
 
@@ -62,10 +111,12 @@ def cpu_baseline(w, img, gpu_pred, threads_all):
                                w.td_in, oracle.READ_ARGMAX, same_pad=True, nthreads=thr)
         return time.perf_counter() - t0, r
 
-    n1 = 4
+    # bounded sample, ~10-20 s of CPU work in all: 16 images on 1 thread and
+    # the whole batch on every thread the box grants
+    n1 = min(16, len(gpu_pred))
     run(1, 1)  # warm-up (page-in, OpenMP pool)
     dt1, r1 = run(n1, 1)
-    nall = 64
+    nall = len(gpu_pred)
     dta, ra = run(nall, threads_all)
     match = bool(np.array_equal(ra["pred"], gpu_pred[:nall]) and np.array_equal(r1["pred"], gpu_pred[:n1]))
     return {
@@ -73,7 +124,7 @@ def cpu_baseline(w, img, gpu_pred, threads_all):
         "unit": "images/s",
         "cores": threads_all,
         "kind": "port",
-        "sample": f"first {nall} images of the batch, whole network, {threads_all} OpenMP threads "
+        "sample": f"{nall} images (the whole batch), whole network, {threads_all} OpenMP threads "
                   f"({dta:.2f} s); 1 thread on the first {n1} images: {n1 / dt1:.3f} images/s",
         "single_thread_value": n1 / dt1,
         "pred_match_gpu": match,
@@ -88,11 +139,15 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--delta", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the known-size copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (every image "
               f"is independent, so N GPUs would each run this same per-GPU batch)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
 
     import vdttfs
     from vdttfs import models
@@ -129,6 +184,8 @@ def main() -> int:
     integ_ms_step = integ_ms / args.steps
     launches_per_step = integ_n / args.steps
     achieved = b_int / (integ_ms_step * 1e-3) / 1e9
+    key = workload_key(B, w.consts)
+    tr = measured_traffic(key)
     dense = 0
     for l in w.layers:
         if l.kind == 0:
@@ -149,6 +206,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: seeded splitmix64 U[0,1) images, Kaiming-normal weights (random init)",
         "config": {"workload": "VGG-16 TTFS-SNN, config 3 (3x32x32, 13 conv + FC 512-512-10)",
+                   "key": key,
                    "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
                    "seed": w.seed, "parallelism": "none (one GPU)"},
         "roofline": {
@@ -157,9 +215,13 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "k_integrate_wave (all conv/FC integrator launches of a step)",
+            "traffic": (tr[0] / tr[1]) if tr else None,
+            "kernel": "integrator = k_merge + k_stream per integrating layer; a launch is one layer's "
+                      "pair, achieved = algorithmic bytes of a step / integrator time of a step",
             "algorithmic_bytes_per_step": b_int,
+            "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
+            "traffic_per_step": tr[0] if tr else None,
+            "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if tr else None,
             "integrator_ms_per_step": integ_ms_step,
             "integrator_launches_per_step": launches_per_step,
         },

@@ -1,0 +1,165 @@
+"""Summaries of rocprofv3 CSV output for the VGG-16 benchmark.
+
+Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
+(``NAME_kernel_stats.csv``, ``NAME_kernel_trace.csv``,
+``NAME_counter_collection.csv``) and prints short markdown tables:
+
+  python -m vdttfs.rocprof_summary stats   DIR NAME            # --kernel-trace --stats
+  python -m vdttfs.rocprof_summary layers  DIR NAME            # one forward, per layer
+  python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME
+
+``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
+benchmark, and the same two counters over ``bench.py --copy-calibration``
+(an elementwise copy of a known number of bytes).  Each counter is scaled by
+known_bytes / counted_bytes of the copy, then summed over the integrator
+dispatches (k_merge + k_stream, or the generic integrator) of one
+non-counting forward.  The last line is machine-readable and is what
+bench.py reports as ``roofline.traffic``.
+"""
+from __future__ import annotations
+
+import collections
+import csv
+import os
+import re
+import sys
+
+INTEGRATOR = ("k_merge", "k_stream", "k_integrate_generic")
+COPY_BYTES_DEFAULT = 1 << 30  # bench.py --copy-calibration moves 2^28 floats each way
+
+
+def short_name(n: str) -> str:
+    m = re.search(r"(k_\w+(<[\w, ]+>)?)", n)
+    if m:
+        return m.group(1)
+    return n.split("(")[0][-48:]
+
+
+def _csv(d: str, name: str, kind: str):
+    p = os.path.join(d, f"{name}_{kind}.csv")
+    with open(p, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def stats(d: str, name: str) -> str:
+    rows = _csv(d, name, "kernel_stats")
+    out = ["| kernel | calls | avg us | total ms | % |", "|---|---:|---:|---:|---:|"]
+    for r in rows:
+        out.append("| %s | %s | %.1f | %.3f | %s |" % (
+            short_name(r["Name"]), r["Calls"], float(r["AverageNs"]) / 1e3,
+            float(r["TotalDurationNs"]) / 1e6, r["Percentage"]))
+    return "\n".join(out)
+
+
+def _forwards(rows, key_start="Start_Timestamp"):
+    """Split dispatches (sorted by start) into forwards; each starts with an encoder."""
+    rows = sorted(rows, key=lambda r: int(r[key_start]))
+    fw, cur = [], None
+    for r in rows:
+        n = short_name(r["Kernel_Name"])
+        if n.startswith("k_encode"):
+            cur = []
+            fw.append(cur)
+        if cur is not None:
+            cur.append(r)
+    return fw
+
+
+_COUNTING = re.compile(r"^(k_stream<true|k_integrate_generic<\w+, \d+, true>)")
+
+
+def _is_counting(forward) -> bool:
+    """A forward run with the E_proc counters on (net.count), not a timed one."""
+    return any(_COUNTING.match(short_name(r["Kernel_Name"])) for r in forward)
+
+
+def layers(d: str, name: str) -> str:
+    fw = [f for f in _forwards(_csv(d, name, "kernel_trace")) if not _is_counting(f)]
+    if not fw:
+        return "no forward found"
+    f = fw[-1]
+    out = ["| # | kernel | grid | us |", "|---:|---|---:|---:|"]
+    tot = integ = 0.0
+    for i, r in enumerate(f):
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        n = short_name(r["Kernel_Name"])
+        tot += us
+        if n.startswith(INTEGRATOR):
+            integ += us
+        out.append("| %d | %s | %s | %.1f |" % (i, n, r["Grid_Size_X"], us))
+    out.append("")
+    out.append("kernel time of the last non-counting forward: %.1f us, of which integrator "
+               "(k_merge + k_stream) %.1f us" % (tot, integ))
+    return "\n".join(out)
+
+
+def _per_dispatch(d: str, name: str, counter: str):
+    """{dispatch id: (kernel name, KiB)} for one counter, forward-grouped."""
+    rows = [r for r in _csv(d, name, "counter_collection") if r["Counter_Name"] == counter]
+    agg = collections.OrderedDict()
+    for r in rows:  # one row per dispatch (and per dimension, summed here)
+        k = int(r["Dispatch_Id"])
+        if k not in agg:
+            agg[k] = dict(r)
+            agg[k]["_v"] = 0.0
+        agg[k]["_v"] += float(r["Counter_Value"])
+    return list(agg.values())
+
+
+def _copy_factor(d: str, name: str, counter: str, known: int) -> float:
+    disp = _per_dispatch(d, name, counter)
+    big = max(disp, key=lambda r: r["_v"])
+    return known / (big["_v"] * 1024.0)
+
+
+def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str,
+            copy_bytes: int = COPY_BYTES_DEFAULT) -> str:
+    ff = _copy_factor(cfdir, name, "FETCH_SIZE", copy_bytes)
+    wf = _copy_factor(cwdir, name, "WRITE_SIZE", copy_bytes)
+    lines = [f"copy calibration ({copy_bytes} B read + {copy_bytes} B written per dispatch): "
+             f"FETCH_SIZE scale {ff:.4f}, WRITE_SIZE scale {wf:.4f}", ""]
+    res = {}
+    for counter, d, scale in (("FETCH_SIZE", fdir, ff), ("WRITE_SIZE", wdir, wf)):
+        disp = _per_dispatch(d, name, counter)
+        fw = [f for f in _forwards(disp, key_start="Dispatch_Id") if not _is_counting(f)]
+        f = fw[-1]
+        per = [(short_name(r["Kernel_Name"]), r["_v"] * 1024.0 * scale) for r in f]
+        res[counter] = per
+    lines.append("| # | kernel | FETCH bytes | WRITE bytes |")
+    lines.append("|---:|---|---:|---:|")
+    tf = tw = 0.0
+    n_integ = 0
+    for i, ((n, fb), (_, wb)) in enumerate(zip(res["FETCH_SIZE"], res["WRITE_SIZE"])):
+        lines.append("| %d | %s | %.4g | %.4g |" % (i, n, fb, wb))
+        if n.startswith(INTEGRATOR):
+            tf += fb
+            tw += wb
+            if not n.startswith("k_merge"):
+                n_integ += 1
+    lines.append("")
+    lines.append(f"integrator (k_merge + k_stream) per forward: FETCH {tf:.6g} B, WRITE {tw:.6g} B, "
+                 f"{n_integ} integrating layers")
+    lines.append(f"TRAFFIC_PER_STEP_BYTES={tf + tw:.0f} LAUNCHES_PER_STEP={n_integ} "
+                 f"FETCH_SCALE={ff:.5f} WRITE_SCALE={wf:.5f}")
+    return "\n".join(lines)
+
+
+def main(argv) -> int:
+    if len(argv) < 2:
+        print(__doc__)
+        return 2
+    cmd = argv[1]
+    if cmd == "stats":
+        print(stats(argv[2], argv[3]))
+    elif cmd == "layers":
+        print(layers(argv[2], argv[3]))
+    elif cmd == "traffic":
+        print(traffic(*argv[2:7]))
+    else:
+        print(__doc__)
+        return 2
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv))
