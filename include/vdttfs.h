@@ -194,6 +194,7 @@ int vdttfs_free_weights(vdttfs_ctx* ctx, vdttfs_dev_layer* layers, int num_layer
 #define VDTTFS_ENCODE_LOG    1
 #define VDTTFS_READOUT_ARGMIN 0
 #define VDTTFS_READOUT_ARGMAX 1
+#define VDTTFS_READOUT_ARGMIN_FIRST 2  /* T3V:291-298: argmin seeded with class 0 */
 
 typedef struct vdttfs_layer_desc {
     int32_t kind;
@@ -229,11 +230,92 @@ int vdttfs_net_set_timing(vdttfs_net* net, int enable);
 int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
                            double* bucket_ms, int64_t* bucket_launches);
 
+/* ---- CuLIF set: task 3 (T3V = task3_dvsgesture/vdttfs_cuda/
+ *      snn_inference_timesorted.cu) ------------------------------------ */
+/* The current-based LIF neuron of T3V:58-62: per step I = I*decay + in
+ * (one fma), V += I, fire at the first step with V >= th.  The context's
+ * T is T_TOTAL and delta is CHUNK_SIZE; delta must divide T (the reference
+ * chunk loop has no t < T guard).  Maps are NCHW and weights OIHW / [out][in]
+ * as in the reference; bucket lists are the reference layout with
+ * OS = T/delta + 1 offsets per site. */
+
+/* conv1_raw_early (T3V:30-65): 3x3, pad 1, over a dense event tensor
+ * d_data [N][C_in][H][W][T]; d_out [N][C_out][H][W] first-spike steps. */
+int vdttfs_culif_conv1_raw(vdttfs_ctx* ctx, const float* d_data, float* d_out,
+                           const float* d_weight, int N, int C_in, int C_out, int H, int W,
+                           float decay, float th);
+/* k_bucketize_conv (T3V:70-90): site = (n, y, x) of an NCHW map. */
+int vdttfs_culif_bucketize_conv(vdttfs_ctx* ctx, const float* d_in, int N, int C, int H, int W,
+                                int32_t* d_out_cin, float* d_out_tin, int32_t* d_out_off);
+/* k_bucketize_fc (T3V:93-106): one site per sample over F features. */
+int vdttfs_culif_bucketize_fc(vdttfs_ctx* ctx, const float* d_in, int N, int F,
+                              int32_t* d_out_cin, float* d_out_tin, int32_t* d_out_off);
+/* conv_bucketed_early (T3V:109-143): 3x3, pad 1, H x W kept. */
+int vdttfs_culif_conv(vdttfs_ctx* ctx, const int32_t* d_bcin, const float* d_btin,
+                      const int32_t* d_boff, float* d_out, const float* d_weight, int N, int C_in,
+                      int C_out, int H, int W, float decay, float th);
+/* pool_chunk_early (T3V:146-168): 2x2 spiking pool. */
+int vdttfs_culif_pool(vdttfs_ctx* ctx, const float* d_in, float* d_out, int N, int C, int H_in,
+                      int W_in, float decay, float th);
+/* fc1_bucketed_recurrent (T3V:171-200): d_w [out_f][in_f], d_w_rec
+ * [out_f][out_f]; out_f <= 1024. */
+int vdttfs_culif_fc_recurrent(vdttfs_ctx* ctx, const int32_t* d_bcin, const float* d_btin,
+                              const int32_t* d_boff, float* d_out, const float* d_w,
+                              const float* d_w_rec, int N, int in_f, int out_f, float decay,
+                              float th);
+/* fc2_bucketed_early (T3V:203-225): d_w [out_f][in_f]. */
+int vdttfs_culif_fc(vdttfs_ctx* ctx, const int32_t* d_bcin, const float* d_btin,
+                    const int32_t* d_boff, float* d_out, const float* d_w, int N, int in_f,
+                    int out_f, float decay, float th);
+/* Readout T3V:291-298 (argmin seeded with class 0). */
+int vdttfs_readout_argmin_first(vdttfs_ctx* ctx, const float* d_out, int B, int C,
+                                int32_t* d_pred);
+
+/* CuLIF network engine: the T3V main() layer sequence (T3V:276-289).  The
+ * first layer is RAW_CONV over the dense event tensor; conv maps stay NHWC
+ * inside the engine (weights are re-laid out at creation), FC inputs are
+ * flattened in the reference's NCHW order. */
+#define VDTTFS_CULIF_RAW_CONV 0
+#define VDTTFS_CULIF_CONV     1
+#define VDTTFS_CULIF_POOL     2
+#define VDTTFS_CULIF_FC_REC   3
+#define VDTTFS_CULIF_FC       4
+
+typedef struct vdttfs_culif_layer {
+    int32_t kind;
+    int32_t C_in, H_in, W_in, C_out;  /* FC: C_in = input features, H_in = W_in = 1 */
+    const float* weight;              /* host: conv OIHW [C_out][C_in][3][3], FC [out][in]; pool NULL */
+    const float* weight_rec;          /* host: FC_REC [out][out], else NULL */
+    float decay, th;
+} vdttfs_culif_layer;
+
+typedef struct vdttfs_culif_net vdttfs_culif_net;
+
+int vdttfs_culif_net_create(vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n_layers,
+                            int B, vdttfs_culif_net** out);
+int vdttfs_culif_net_destroy(vdttfs_culif_net* net);
+/* d_data [B][C_in][H][W][T] -> per-layer maps -> d_pred (nullable, B int32,
+ * T3V:291-298), stream-ordered. */
+int vdttfs_culif_net_forward(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred);
+/* Layer i's output after a forward; *nhwc = 1 when the map is NHWC
+ * (engine conv / pool layers), 0 when NCHW or FC [B][C]. */
+int vdttfs_culif_net_layer_output(vdttfs_culif_net* net, int layer, const float** d_out,
+                                  int64_t* elems, int32_t* nhwc);
+
 /* ---- synthetic workloads (counter-mode splitmix64; host) --------------- */
 /* u = (z>>40) * 2^-24 with z = mix(seed + 0x9E3779B97F4A7C15*(stream*2^40+i+1)). */
 int vdttfs_synth_uniform(uint64_t seed, uint64_t stream, float* out, int64_t n);
 /* Box-Muller in fp64, scaled by sigma, rounded to fp32. */
 int vdttfs_synth_normal(uint64_t seed, uint64_t stream, float* out, int64_t n, double sigma);
+/* Config 4 event tensor out[N][C][H][W][T] in {0,1}: per sample a Gaussian
+ * blob of `sigma` px whose centre starts uniform in the middle half of the
+ * field and moves linearly at a per-axis velocity uniform in [-vmax, vmax]
+ * px/step; p(c,y,x,t) = min(1, scale*exp(-d^2/(2 sigma^2))) with scale set
+ * per sample so the mean of p over (y,x,t) is `density`; every element is
+ * Bernoulli(p) from stream 2000+n.  scales (nullable, N doubles) receives the
+ * per-sample scale. */
+int vdttfs_synth_dvs(uint64_t seed, int N, int C, int H, int W, int T, double density,
+                     double sigma, double vmax, float* out, double* scales);
 
 #ifdef __cplusplus
 }

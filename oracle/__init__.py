@@ -225,3 +225,99 @@ def net_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td_in,
         raise RuntimeError(f"orc_net_forward failed: {rc}")
     return {"final": final, "pred": pred, "eproc": np.array(list(ep), np.uint64),
             "ebin": np.array(list(eb), np.uint64), "outs": outs}
+
+
+# ---- CuLIF set (T3V:30-225) -------------------------------------------------
+def _ci(*xs):
+    return [C.c_int(int(x)) for x in xs]
+
+
+def culif_conv1_raw(data, weight, N, C_in, C_out, H, W, T, delta, decay, th, nthreads=0):
+    data, weight = f32(data), f32(weight)
+    out = np.empty(N * C_out * H * W, np.float32)
+    lib().orc_culif_conv1_raw(_p(data), _p(out), _p(weight), *_ci(N, C_in, C_out, H, W, T, delta),
+                              C.c_float(decay), C.c_float(th), C.c_int(nthreads))
+    return out
+
+
+def culif_bucketize_nchw(x, N, Cc, H, W, T, delta, nthreads=0):
+    x = f32(x)
+    OS = T // delta + 1
+    cin = np.zeros(N * H * W * Cc, np.int32)
+    tin = np.zeros(N * H * W * Cc, np.float32)
+    off = np.zeros(N * H * W * OS, np.int32)
+    lib().orc_culif_bucketize_nchw(_p(x), *_ci(N, Cc, H, W, T, delta), _p(cin), _p(tin), _p(off),
+                                   C.c_int(nthreads))
+    return cin, tin, off
+
+
+def culif_bucketize_fc(x, N, F, T, delta, nthreads=0):
+    x = f32(x)
+    OS = T // delta + 1
+    cin = np.zeros(N * F, np.int32)
+    tin = np.zeros(N * F, np.float32)
+    off = np.zeros(N * OS, np.int32)
+    lib().orc_culif_bucketize_fc(_p(x), *_ci(N, F, T, delta), _p(cin), _p(tin), _p(off),
+                                 C.c_int(nthreads))
+    return cin, tin, off
+
+
+def culif_conv(cin, tin, off, weight, N, C_in, C_out, H, W, T, delta, decay, th, nthreads=0):
+    cin, tin, off, weight = i32(cin), f32(tin), i32(off), f32(weight)
+    out = np.empty(N * C_out * H * W, np.float32)
+    lib().orc_culif_conv(_p(cin), _p(tin), _p(off), _p(out), _p(weight),
+                         *_ci(N, C_in, C_out, H, W, T, delta), C.c_float(decay), C.c_float(th),
+                         C.c_int(nthreads))
+    return out
+
+
+def culif_pool(x, N, Cc, H_in, W_in, T, delta, decay, th, nthreads=0):
+    x = f32(x)
+    out = np.empty(N * Cc * (H_in // 2) * (W_in // 2), np.float32)
+    lib().orc_culif_pool(_p(x), _p(out), *_ci(N, Cc, H_in, W_in, T, delta), C.c_float(decay),
+                         C.c_float(th), C.c_int(nthreads))
+    return out
+
+
+def culif_fc_recurrent(cin, tin, off, w, w_rec, N, in_f, out_f, T, delta, decay, th, nthreads=0):
+    cin, tin, off, w, w_rec = i32(cin), f32(tin), i32(off), f32(w), f32(w_rec)
+    out = np.empty(N * out_f, np.float32)
+    lib().orc_culif_fc_recurrent(_p(cin), _p(tin), _p(off), _p(out), _p(w), _p(w_rec),
+                                 *_ci(N, in_f, out_f, T, delta), C.c_float(decay), C.c_float(th),
+                                 C.c_int(nthreads))
+    return out
+
+
+def culif_fc(cin, tin, off, w, N, in_f, out_f, T, delta, decay, th, nthreads=0):
+    cin, tin, off, w = i32(cin), f32(tin), i32(off), f32(w)
+    out = np.empty(N * out_f, np.float32)
+    lib().orc_culif_fc(_p(cin), _p(tin), _p(off), _p(out), _p(w), *_ci(N, in_f, out_f, T, delta),
+                       C.c_float(decay), C.c_float(th), C.c_int(nthreads))
+    return out
+
+
+def culif_net_forward(layers, data, N, T, delta, nthreads=0):
+    """The T3V main() sequence (T3V:276-298) over the oracle's kernels.
+    layers: vdttfs.CulifLayerSpec-like (kind 0 raw conv, 1 conv, 2 pool,
+    3 recurrent FC, 4 FC).  Returns (per-layer NCHW outputs, predictions)."""
+    outs = []
+    cur = None
+    for l in layers:
+        if l.kind == 0:
+            cur = culif_conv1_raw(data, l.weight, N, l.C_in, l.C_out, l.H_in, l.W_in, T, delta,
+                                  l.decay, l.th, nthreads)
+        elif l.kind == 1:
+            b = culif_bucketize_nchw(cur, N, l.C_in, l.H_in, l.W_in, T, delta, nthreads)
+            cur = culif_conv(*b, l.weight, N, l.C_in, l.C_out, l.H_in, l.W_in, T, delta, l.decay,
+                             l.th, nthreads)
+        elif l.kind == 2:
+            cur = culif_pool(cur, N, l.C_in, l.H_in, l.W_in, T, delta, l.decay, l.th, nthreads)
+        elif l.kind == 3:
+            b = culif_bucketize_fc(cur, N, l.C_in, T, delta, nthreads)
+            cur = culif_fc_recurrent(*b, l.weight, l.weight_rec, N, l.C_in, l.C_out, T, delta,
+                                     l.decay, l.th, nthreads)
+        else:
+            b = culif_bucketize_fc(cur, N, l.C_in, T, delta, nthreads)
+            cur = culif_fc(*b, l.weight, N, l.C_in, l.C_out, T, delta, l.decay, l.th, nthreads)
+        outs.append(cur)
+    return outs, readout(cur, N, layers[-1].C_out, READ_T3)

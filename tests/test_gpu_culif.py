@@ -1,0 +1,177 @@
+"""CuLIF (T3V, config 4) on the GPU: each drop-in kernel against the oracle on
+the reference layouts, bit for bit; the engine network layer by layer; and,
+at the full config-4 size, the first samples against the oracle plus
+bit-identical outputs across chunk widths."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import vdttfs
+from vdttfs import models
+
+pytestmark = pytest.mark.gpu
+INF = np.float32(9999.0)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def spike_map(rng, n, T, p=0.5):
+    t = rng.integers(0, T, size=n).astype(np.float32)
+    s = np.where(rng.random(n) < p, t, INF).astype(np.float32)
+    s[:6] = [T + 3, np.nan, 2.75, -0.5, -1.5, T - 1]  # dropped, dropped, 2, 0, dropped, last
+    return s
+
+
+@pytest.mark.parametrize("T,delta,C_out", [(64, 32, 70), (48, 16, 64), (32, 32, 5)])
+def test_conv1_raw(gpu_ctx_factory, T, delta, C_out):
+    say(f"culif conv1_raw T={T} delta={delta} C_out={C_out}")
+    ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
+    rng = np.random.default_rng(31)
+    N, C_in, H, W = 2, 2, 9, 7
+    data = (rng.random((N, C_in, H, W, T)) < 0.05).astype(np.float32)
+    w = (rng.standard_normal((C_out, C_in, 3, 3)) * 0.6).astype(np.float32)
+    exp = oracle.culif_conv1_raw(data, w, N, C_in, C_out, H, W, T, delta, 0.5, 1.0)
+    d_out = ctx.empty(exp.size)
+    ctx.culif_conv1_raw(ctx.to_device(data), d_out, ctx.to_device(w), N, C_in, C_out, H, W, 0.5, 1.0)
+    got = d_out.download()
+    assert np.any(exp < INF) and np.any(exp == INF)
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_bucketize_conv_and_fc(gpu_ctx_factory):
+    say("culif bucketize conv/fc")
+    T, delta = 64, 16
+    ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
+    rng = np.random.default_rng(32)
+    for (N, Cc, H, W) in [(2, 64, 5, 6), (1, 3, 7, 1), (3, 130, 2, 2)]:
+        x = spike_map(rng, N * Cc * H * W, T)
+        cin, tin, off = oracle.culif_bucketize_nchw(x, N, Cc, H, W, T, delta)
+        d_c, d_t, d_o = ctx.empty(cin.size, np.int32), ctx.empty(tin.size), ctx.empty(off.size, np.int32)
+        ctx.culif_bucketize_conv(ctx.to_device(x), N, Cc, H, W, d_c, d_t, d_o)
+        go = d_o.download()
+        np.testing.assert_array_equal(go, off)
+        gc, gt = d_c.download(), d_t.download()
+        OS = T // delta + 1
+        for s in range(N * H * W):  # only each site's first off[NC] entries are defined
+            n = off[s * OS + OS - 1]
+            np.testing.assert_array_equal(gc[s * Cc:s * Cc + n], cin[s * Cc:s * Cc + n])
+            np.testing.assert_array_equal(gt[s * Cc:s * Cc + n], tin[s * Cc:s * Cc + n])
+    N, F = 5, 1000
+    x = spike_map(rng, N * F, T)
+    cin, tin, off = oracle.culif_bucketize_fc(x, N, F, T, delta)
+    d_c, d_t, d_o = ctx.empty(cin.size, np.int32), ctx.empty(tin.size), ctx.empty(off.size, np.int32)
+    ctx.culif_bucketize_fc(ctx.to_device(x), N, F, d_c, d_t, d_o)
+    np.testing.assert_array_equal(d_o.download(), off)
+    OS = T // delta + 1
+    gc, gt = d_c.download(), d_t.download()
+    for n in range(N):
+        k = off[n * OS + OS - 1]
+        np.testing.assert_array_equal(gc[n * F:n * F + k], cin[n * F:n * F + k])
+        np.testing.assert_array_equal(gt[n * F:n * F + k], tin[n * F:n * F + k])
+
+
+@pytest.mark.parametrize("delta", [8, 32])
+def test_conv_pool_fc_fcrec_dropin(gpu_ctx_factory, delta):
+    say(f"culif conv / pool / fc / fc_recurrent drop-in delta={delta}")
+    T = 64
+    ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
+    rng = np.random.default_rng(33)
+    # conv_bucketed_early
+    N, C_in, C_out, H, W = 2, 24, 20, 6, 5
+    x = spike_map(rng, N * C_in * H * W, T, p=0.4)
+    w = (rng.standard_normal((C_out, C_in, 3, 3)) * 0.5).astype(np.float32)
+    b = oracle.culif_bucketize_nchw(x, N, C_in, H, W, T, delta)
+    exp = oracle.culif_conv(*b, w, N, C_in, C_out, H, W, T, delta, 0.5, 1.0)
+    db = [ctx.to_device(a) for a in b]
+    d_out = ctx.empty(exp.size)
+    ctx.culif_conv(*db, d_out, ctx.to_device(w), N, C_in, C_out, H, W, 0.5, 1.0)
+    assert np.any(exp < INF)
+    np.testing.assert_array_equal(d_out.download(), exp)
+    # pool_chunk_early
+    xp = spike_map(rng, 3 * 7 * 8 * 6, T, p=0.3)
+    exp = oracle.culif_pool(xp, 3, 7, 8, 6, T, delta, 0.5, 1.0)
+    d_p = ctx.empty(exp.size)
+    ctx.culif_pool(ctx.to_device(xp), d_p, 3, 7, 8, 6, 0.5, 1.0)
+    assert np.any(exp < INF) and np.any(exp == INF)
+    np.testing.assert_array_equal(d_p.download(), exp)
+    # fc2_bucketed_early and fc1_bucketed_recurrent
+    for (N, F, O) in [(3, 300, 11), (2, 513, 128), (2, 70, 70)]:
+        xf = spike_map(rng, N * F, T, p=0.5)
+        bf = oracle.culif_bucketize_fc(xf, N, F, T, delta)
+        dbf = [ctx.to_device(a) for a in bf]
+        wf = (rng.standard_normal((O, F)) * (2.0 / np.sqrt(F))).astype(np.float32)
+        exp = oracle.culif_fc(*bf, wf, N, F, O, T, delta, 0.5, 1.0)
+        d_f = ctx.empty(exp.size)
+        ctx.culif_fc(*dbf, d_f, ctx.to_device(wf), N, F, O, 0.5, 1.0)
+        np.testing.assert_array_equal(d_f.download(), exp)
+        wr = (rng.standard_normal((O, O)) * 0.3).astype(np.float32)
+        exp = oracle.culif_fc_recurrent(*bf, wf, wr, N, F, O, T, delta, 0.5, 1.0)
+        d_r = ctx.empty(exp.size)
+        ctx.culif_fc_recurrent(*dbf, d_r, ctx.to_device(wf), ctx.to_device(wr), N, F, O, 0.5, 1.0)
+        assert np.any(exp < INF)
+        np.testing.assert_array_equal(d_r.download(), exp)
+    # readout T3V:291-298 (class 0 when nothing fires)
+    rows = np.array([[INF, INF, INF], [5, 3, 3], [2, 9, 1], [INF, 7, INF]], np.float32)
+    d_pr = ctx.empty(4, np.int32)
+    ctx.readout_argmin_first(ctx.to_device(rows), 4, 3, d_pr)
+    np.testing.assert_array_equal(d_pr.download(), oracle.readout(rows, 4, 3, oracle.READ_T3))
+    assert d_pr.download().tolist() == [0, 1, 2, 1]
+
+
+def run_engine(ctx, w, B, ev):
+    net = vdttfs.CulifNet(ctx, w.layers, B)
+    try:
+        d_ev = ctx.to_device(ev)
+        d_pred = ctx.empty(B, np.int32)
+        net.forward(d_ev, d_pred)
+        ctx.synchronize()
+        outs = [net.layer_output(i) for i in range(len(w.layers))]
+        pred = d_pred.download()
+        d_ev.free()
+        d_pred.free()
+    finally:
+        net.close()
+    return outs, pred
+
+
+def test_culif_engine_small(gpu_ctx_factory):
+    say("culif engine 2x32x32 B=3 vs oracle, every layer")
+    w = models.culif7(H=32, W=32)
+    B = 3
+    ev = models.dvs_events(w, B)
+    ctx = gpu_ctx_factory(w.consts)
+    outs, pred = run_engine(ctx, w, B, ev)
+    ref, rpred = oracle.culif_net_forward(w.layers, ev, B, w.consts.T, w.consts.delta)
+    for i, (g, o) in enumerate(zip(outs, ref)):
+        o = o.reshape(g.shape)
+        assert np.any(o < INF), f"layer {i} silent"
+        assert np.array_equal(g, o), f"layer {i} differs at {np.flatnonzero(g != o)[:8]}"
+    np.testing.assert_array_equal(pred, rpred)
+
+
+def test_culif_config4_full(gpu_ctx_factory):
+    """Config 4 at full size (2x128x128, T=64, B=64): samples 0-1 equal the
+    oracle at every layer; Delta in {16, 64} gives bit-identical maps."""
+    w = models.culif7()
+    B = 64
+    ev = models.dvs_events(w, B)
+    say("culif config 4 B=64 delta=32")
+    outs, pred = run_engine(gpu_ctx_factory(w.consts), w, B, ev)
+    k = 2
+    ref, rpred = oracle.culif_net_forward(w.layers, ev[:k], k, w.consts.T, w.consts.delta)
+    for i, (g, o) in enumerate(zip(outs, ref)):
+        o = o.reshape((k,) + g.shape[1:])
+        assert np.array_equal(g[:k], o), f"layer {i} differs"
+    np.testing.assert_array_equal(pred[:k], rpred)
+    assert len(set(pred.tolist())) > 1
+    for d in (16, 64):
+        say(f"culif config 4 B=64 delta={d}")
+        outs_d, pred_d = run_engine(gpu_ctx_factory(vdttfs.task3_consts(T=64, delta=d)), w, B, ev)
+        for i, (a, b) in enumerate(zip(outs_d, outs)):
+            assert np.array_equal(a, b), f"layer {i} differs at delta={d}"
+        np.testing.assert_array_equal(pred_d, pred)

@@ -78,6 +78,11 @@ int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const 
                          int W_in, int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
                          int is_fc);
 
+// CuLIF neuron constants (T3V:24-27 per layer; one decay and threshold).
+struct CulifNeuron {
+    float decay, th;
+};
+
 struct IntegShape {
     int B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
 };
@@ -86,15 +91,40 @@ int merged_list_cap(const IntegShape& s);
 // Engine integrator over the bin layout: merge per pixel, then stream.
 // list/bstart: merged-list scratch of n_pix*list_cap entries and
 // n_pix*(T+1) bin starts.  counters: nullable; [0] += eproc, [1] += ebin.
+// culif: nullable; selects the CuLIF neuron (bias, theta and t_min unused).
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
                           int2* list, int64_t list_cap, int32_t* bstart, const float* W,
                           const float* bias, const float* theta, int t_min, const IntegShape& s,
-                          unsigned long long* counters);
+                          unsigned long long* counters, const CulifNeuron* culif = nullptr);
 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
 int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,
                    const float* alpha, int B, int C_in, int C_out);
-int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int argmax);
+// mode: 0 argmin (T1V), 1 argmax (T2V), 2 argmin seeded with class 0 (T3V)
+int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int mode);
+
+// ---- CuLIF (T3V) ----
+int check_culif_consts(const vdttfs_ctx* ctx);
+int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
+                           int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th);
+// Reference layout; site s = (n, hw), element c at (n*C + c)*HW + hw (FC: HW = 1).
+int launch_culif_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_sites, int C, int HW,
+                           int32_t* cin, float* tin, int32_t* off);
+int launch_culif_generic(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, const int32_t* off,
+                         float* out, const float* W, int N, int C_in, int C_out, int H, int Wd,
+                         int is_fc, float decay, float th);
+int launch_culif_pool(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H_in, int W_in,
+                      int nhwc_in, int nhwc_out, float decay, float th);
+// Drop-in (cur == NULL): reference buckets, W [out][in], Wrec [i][j].
+// Engine (cur != NULL): feed-forward input per step cur[N][T][out_f] from
+// launch_bin_currents, Wrec transposed to [j][i]; cin/tin/off/W unused.
+int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, const int32_t* off,
+                        const float* cur, float* out, const float* W, const float* Wrec, int N,
+                        int in_f, int out_f, float decay, float th);
+// cur[n][t][o] = sum over bin t's events (ascending input j) of W_t[j][o].
+int launch_bin_currents(vdttfs_ctx* ctx, const vd_event* ev, const int32_t* off, const float* W_t,
+                        float* cur, int N, int in_f, int out_f);
+int launch_nhwc_to_nchw(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H, int W);
 
 // shape validation shared by the entry points
 int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s);

@@ -1,0 +1,618 @@
+// CuLIF kernels (T3V, config 4): the current-based LIF neuron
+//   I = fma(I, decay, in_t);  V = V + I;  fire at the first t with V >= th
+// over one arrival-ordered pass per layer.  The reference processes Delta-wide
+// chunks and stops at the chunk that fires; with Delta | T this equals the
+// per-step recurrence above, so every kernel here steps bins in time order
+// and leaves at the first crossing (results are Delta-invariant).
+//
+//  k_culif_conv1_raw   conv1_raw_early (T3V:30-65): one wave64 per output
+//                      pixel and 64-wide c_out block; the pixel's dense input
+//                      vectors are wave-uniform and read through the scalar
+//                      cache, weights are per lane.  Output layout by strides
+//                      (NCHW for the drop-in, NHWC for the engine).
+//  k_culif_bucketize   k_bucketize_conv / k_bucketize_fc (T3V:70-106) in the
+//                      reference layout: one thread per site, counters in LDS.
+//  k_culif_generic     conv_bucketed_early / fc2_bucketed_early (T3V:109-143,
+//                      203-225) over the reference layout, one thread per
+//                      neuron (the drop-in path and the engine's small FC).
+//  k_culif_pool        pool_chunk_early (T3V:146-168), layouts by strides.
+//  k_culif_fc_rec      fc1_bucketed_recurrent (T3V:171-200): one block per
+//                      sample; fired-last-step neurons as a bitmask in LDS.
+//  k_nhwc_to_nchw      flattening order for an FC layer after a spatial map.
+#include "common.h"
+#include "wave.h"
+
+namespace vdttfs {
+namespace {
+
+constexpr int kRawChunk = 32;  // steps per register chunk in conv1_raw (any T)
+
+// ---------------------------------------------------------------------------
+struct RawArgs {
+    const float* data;  // [N][C_in][H][W][T]
+    float* out;
+    const float* W;     // OIHW [C_out][C_in][3][3]
+    int64_t n_pix;      // N*H*W
+    int C_in, C_out, H, Wd, T, n_cblk;
+    int64_t sN, sC, sY, sX;  // output strides
+    float decay, th;
+};
+
+template <bool FULL>
+__device__ __forceinline__ void raw_chunk(const RawArgs& a, int64_t n, int y, int x, int c, bool ok,
+                                          int t0, float (&in)[kRawChunk]) {
+#pragma unroll
+    for (int t = 0; t < kRawChunk; ++t) in[t] = 0.0f;
+    // T3V:39-55: c_in, ky, kx (out-of-bounds taps skipped), then time
+    for (int ci = 0; ci < a.C_in; ++ci)
+        for (int ky = 0; ky < 3; ++ky) {
+            const int iy = y + ky - 1;
+            if (iy < 0 || iy >= a.H) continue;
+            for (int kx = 0; kx < 3; ++kx) {
+                const int ix = x + kx - 1;
+                if (ix < 0 || ix >= a.Wd) continue;
+                const float w = ok ? a.W[(((int64_t)c * a.C_in + ci) * 3 + ky) * 3 + kx] : 0.0f;
+                const float* __restrict__ dv =
+                    a.data + ((((n * a.C_in + ci) * a.H + iy) * a.Wd + ix) * (int64_t)a.T + t0);
+                if (FULL) {
+#pragma unroll
+                    for (int t = 0; t < kRawChunk; ++t) in[t] = __builtin_fmaf(w, dv[t], in[t]);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < kRawChunk; ++t)
+                        if (t0 + t < a.T) in[t] = __builtin_fmaf(w, dv[t], in[t]);
+                }
+            }
+        }
+}
+
+__global__ __launch_bounds__(256) void k_culif_conv1_raw(RawArgs a) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t b = blockIdx.x;
+    const int cb = (int)(b % a.n_cblk);
+    const int64_t pix0 = (b / a.n_cblk) * 4 + wave;
+    if (pix0 >= a.n_pix) return;  // uniform per wave
+    // wave-uniform pixel: the input vectors below are scalar loads
+    const int64_t pix = ((int64_t)uniform((int)(pix0 >> 32)) << 32) | (uint32_t)uniform((int)pix0);
+    const int x = (int)(pix % a.Wd);
+    const int y = (int)((pix / a.Wd) % a.H);
+    const int64_t n = pix / ((int64_t)a.Wd * a.H);
+    const int c = cb * 64 + lane_id();
+    const bool ok = c < a.C_out;
+    float I = 0.0f, V = 0.0f, res = kInfTime;
+    bool alive = ok;
+    for (int t0 = 0; t0 < a.T; t0 += kRawChunk) {
+        float in[kRawChunk];
+        if (t0 + kRawChunk <= a.T)
+            raw_chunk<true>(a, n, y, x, c, ok, t0, in);
+        else
+            raw_chunk<false>(a, n, y, x, c, ok, t0, in);
+#pragma unroll
+        for (int t = 0; t < kRawChunk; ++t) {
+            if (t0 + t < a.T) {
+                I = __builtin_fmaf(I, a.decay, in[t]);
+                V = V + I;
+                if (alive && V >= a.th) {
+                    res = (float)(t0 + t);
+                    alive = false;
+                }
+            }
+        }
+        if (__ballot(alive) == 0) break;
+    }
+    if (ok) a.out[n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+}
+
+// ---------------------------------------------------------------------------
+// Reference-layout bucketize (T3V:70-106).  Site s = (n, hw): element c at
+// (n*C + c)*HW + hw; an FC input is HW = 1, C = F.  tb = (int)t, kept if
+// 0 <= tb < T; chunks of D; events in ascending c within a chunk.
+constexpr int kCBktThreads = 64;
+constexpr int kCBktMaxChunks = 64;
+
+struct CBktArgs {
+    const float* in;
+    int32_t* cin;
+    float* tin;
+    int32_t* off;
+    int64_t n_sites;
+    int C, HW, T, D, NC;
+};
+
+__device__ __forceinline__ int culif_bin(float tf, int T) {
+    if (!(tf < kInfTime)) return -1;
+    const int tb = (int)tf;
+    return (tb >= 0 && tb < T) ? tb : -1;
+}
+
+__global__ __launch_bounds__(kCBktThreads) void k_culif_bucketize(CBktArgs a) {
+    __shared__ int cnt[kCBktMaxChunks * kCBktThreads];  // [chunk][lane]
+    const int lane = threadIdx.x;
+    const int64_t s = (int64_t)blockIdx.x * kCBktThreads + lane;
+    if (s >= a.n_sites) return;  // no barriers below
+    int* my = cnt + lane;
+    for (int k = 0; k < a.NC; ++k) my[k * kCBktThreads] = 0;
+    const int64_t base = (s / a.HW) * (int64_t)a.C * a.HW + s % a.HW;
+    for (int c = 0; c < a.C; ++c) {
+        const int tb = culif_bin(a.in[base + (int64_t)c * a.HW], a.T);
+        if (tb >= 0) my[(tb / a.D) * kCBktThreads] += 1;
+    }
+    const int OS = a.NC + 1;
+    int run = 0;
+    for (int k = 0; k < a.NC; ++k) {
+        a.off[s * OS + k] = run;
+        const int v = my[k * kCBktThreads];
+        my[k * kCBktThreads] = run;
+        run += v;
+    }
+    a.off[s * OS + a.NC] = run;
+    int32_t* dc = a.cin + s * a.C;
+    float* dt = a.tin + s * a.C;
+    for (int c = 0; c < a.C; ++c) {
+        const float tf = a.in[base + (int64_t)c * a.HW];
+        const int tb = culif_bin(tf, a.T);
+        if (tb >= 0) {
+            const int p = my[(tb / a.D) * kCBktThreads]++;
+            dc[p] = c;
+            dt[p] = tf;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+struct CGenArgs {
+    const int32_t* cin;
+    const float* tin;
+    const int32_t* off;
+    float* out;
+    const float* W;   // conv OIHW [C_out][C_in][3][3]; fc [out][in]
+    int64_t total;
+    int C_in, C_out, H, Wd, T, D, NC;
+    float decay, th;
+};
+
+// One thread per neuron; in_val[] of a chunk in private memory.
+template <bool FC, int DMAX>
+__global__ __launch_bounds__(256) void k_culif_generic(CGenArgs a) {
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n;
+        int c_out, y = 0, x = 0;
+        if (FC) {
+            n = idx / a.C_out;
+            c_out = (int)(idx % a.C_out);
+        } else {  // NCHW, x fastest (T3V:112-114)
+            const int64_t hw = (int64_t)a.H * a.Wd;
+            n = idx / (a.C_out * hw);
+            const int64_t rem = idx % (a.C_out * hw);
+            c_out = (int)(rem / hw);
+            y = (int)((rem / a.Wd) % a.H);
+            x = (int)(rem % a.Wd);
+        }
+        const int OS = a.NC + 1;
+        float I = 0.0f, V = 0.0f, res = kInfTime;
+        for (int ch = 0; ch < a.NC && res == kInfTime; ++ch) {
+            const int base_t = ch * a.D;
+            float in_val[DMAX];
+            for (int t = 0; t < a.D; ++t) in_val[t] = 0.0f;
+            const int ntap = FC ? 1 : 9;
+            for (int k = 0; k < ntap; ++k) {
+                int64_t site;
+                int64_t wk;
+                if (FC) {
+                    site = n;
+                    wk = (int64_t)c_out * a.C_in;  // + j
+                } else {
+                    const int ky = k / 3, kx = k % 3;
+                    const int iy = y + ky - 1, ix = x + kx - 1;
+                    if (iy < 0 || iy >= a.H || ix < 0 || ix >= a.Wd) continue;
+                    site = (n * a.H + iy) * a.Wd + ix;
+                    wk = (int64_t)c_out * a.C_in * 9 + ky * 3 + kx;  // + cin*9
+                }
+                // offsets and indices are the caller's: keep every access in bounds
+                const int s = max(a.off[site * OS + ch], 0), e = min(a.off[site * OS + ch + 1], a.C_in);
+                const int32_t* sc = a.cin + site * a.C_in;
+                const float* st = a.tin + site * a.C_in;
+                for (int p = s; p < e; ++p) {
+                    const int j = sc[p];
+                    const int dt = (int)st[p] - base_t;
+                    if ((unsigned)dt < (unsigned)a.D && (unsigned)j < (unsigned)a.C_in)
+                        in_val[dt] = in_val[dt] + a.W[wk + (int64_t)j * (FC ? 1 : 9)];
+                }
+            }
+            for (int t = 0; t < a.D; ++t) {
+                I = __builtin_fmaf(I, a.decay, in_val[t]);
+                V = V + I;
+                if (V >= a.th) {
+                    res = (float)(base_t + t);
+                    break;
+                }
+            }
+        }
+        a.out[idx] = res;
+    }
+}
+
+// ---------------------------------------------------------------------------
+struct CPoolArgs {
+    const float* in;
+    float* out;
+    int64_t total;
+    int C, H_in, W_in, T;
+    int nhwc;                       // flat output order: 1 = NHWC, 0 = NCHW
+    int64_t iN, iC, iY, iX;         // input strides
+    int64_t oN, oC, oY, oX;         // output strides
+    float decay, th;
+};
+
+// T3V:146-168.  in_t = 1.0 when one of the 4 inputs has floor(tf) == t
+// (the reference sets in_val[(int)tf - chunk] for chunk <= tf < chunk+D).
+__global__ __launch_bounds__(256) void k_culif_pool(CPoolArgs a) {
+    const int H_out = a.H_in / 2, W_out = a.W_in / 2;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n;
+        int c, yo, xo;
+        if (a.nhwc) {
+            c = (int)(idx % a.C);
+            xo = (int)((idx / a.C) % W_out);
+            yo = (int)((idx / a.C / W_out) % H_out);
+            n = idx / ((int64_t)a.C * W_out * H_out);
+        } else {
+            xo = (int)(idx % W_out);
+            yo = (int)((idx / W_out) % H_out);
+            c = (int)((idx / W_out / H_out) % a.C);
+            n = idx / ((int64_t)a.C * W_out * H_out);
+        }
+        int tf[4];
+        bool any = false;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float v = a.in[n * a.iN + c * a.iC + (int64_t)(yo * 2 + (k >> 1)) * a.iY +
+                                 (int64_t)(xo * 2 + (k & 1)) * a.iX];
+            // arrival step, or -1: only 0 <= tf < T can ever set in_t
+            tf[k] = (v >= 0.0f && v < (float)a.T) ? (int)v : -1;
+            any = any || tf[k] >= 0;
+        }
+        float res = kInfTime;
+        if (!any) {
+            // no input: I and V stay +0
+            res = (0.0f >= a.th) ? 0.0f : kInfTime;
+        } else {
+            float I = 0.0f, V = 0.0f;
+            for (int t = 0; t < a.T; ++t) {
+                const float in = (tf[0] == t || tf[1] == t || tf[2] == t || tf[3] == t) ? 1.0f : 0.0f;
+                I = __builtin_fmaf(I, a.decay, in);
+                V = V + I;
+                if (V >= a.th) {
+                    res = (float)t;
+                    break;
+                }
+            }
+        }
+        a.out[n * a.oN + c * a.oC + (int64_t)yo * a.oY + (int64_t)xo * a.oX] = res;
+    }
+}
+
+// ---------------------------------------------------------------------------
+struct CRecArgs {
+    const int32_t* cin;  // drop-in: reference buckets
+    const float* tin;
+    const int32_t* off;
+    const float* cur;    // engine: feed-forward input per step [N][T][out_f]
+    float* out;
+    const float* W;      // drop-in: [out][in]
+    const float* Wrec;   // drop-in [i][j]; engine [j][i]
+    int in_f, out_f, out_pad, T, D, NC;
+    float decay, th;
+};
+
+// T3V:171-200: block per sample, thread i = neuron i.  The feed-forward
+// input of step t is either accumulated per chunk in LDS from the reference
+// buckets (drop-in, in bucket order) or read from k_bin_currents' output
+// (engine).  Every step then adds the recurrent input of the neurons that
+// fired on the previous step (ascending j), between two barriers as the
+// reference does.
+template <bool CURRENTS>
+__global__ __launch_bounds__(1024) void k_culif_fc_rec(CRecArgs a) {
+    extern __shared__ float in_ff[];              // drop-in: [D][out_pad]
+    __shared__ unsigned long long fmask[16];      // fired on the previous step
+    const int n = blockIdx.x;
+    const int i = threadIdx.x;
+    const bool ok = i < a.out_f;
+    const int nwords = a.out_pad >> 6;
+    if (i < 16) fmask[i] = 0ull;
+    float I = 0.0f, V = 0.0f, my_fire = kInfTime;
+    bool has_fired = false;
+    const int OS = a.NC + 1;
+    for (int ch = 0; ch < a.NC; ++ch) {
+        const int base_t = ch * a.D;
+        if (!CURRENTS) {
+            const int32_t* sc = a.cin + (int64_t)n * a.in_f;
+            const float* st = a.tin + (int64_t)n * a.in_f;
+            for (int t = 0; t < a.D; ++t) in_ff[t * a.out_pad + i] = 0.0f;
+            const int s = max(a.off[(int64_t)n * OS + ch], 0);
+            const int e = min(a.off[(int64_t)n * OS + ch + 1], a.in_f);
+            for (int p = s; p < e; ++p) {
+                const int j = sc[p];
+                const int dt = (int)st[p] - base_t;
+                if (ok && (unsigned)dt < (unsigned)a.D && (unsigned)j < (unsigned)a.in_f)
+                    in_ff[dt * a.out_pad + i] = in_ff[dt * a.out_pad + i] + a.W[(int64_t)i * a.in_f + j];
+            }
+        }
+        for (int t = 0; t < a.D; ++t) {
+            __syncthreads();
+            float in_rec = 0.0f;
+            for (int wd = 0; wd < nwords; ++wd) {
+                unsigned long long m = fmask[wd];
+                while (m) {
+                    const int j = wd * 64 + __builtin_ctzll(m);
+                    m &= m - 1;
+                    if (ok)
+                        in_rec = in_rec + (CURRENTS ? a.Wrec[(int64_t)j * a.out_f + i]
+                                                    : a.Wrec[(int64_t)i * a.out_f + j]);
+                }
+            }
+            float ff = 0.0f;
+            if (CURRENTS)
+                ff = ok ? a.cur[((int64_t)n * a.T + base_t + t) * a.out_f + i] : 0.0f;
+            else
+                ff = in_ff[t * a.out_pad + i];
+            I = __builtin_fmaf(I, a.decay, ff) + in_rec;
+            V = V + I;
+            bool fire_now = false;
+            if (ok && V >= a.th && !has_fired) {
+                fire_now = true;
+                has_fired = true;
+                my_fire = (float)(base_t + t);
+                V = -10000.0f;
+            }
+            __syncthreads();
+            const unsigned long long b = __ballot(fire_now);
+            if ((i & 63) == 0) fmask[i >> 6] = b;
+        }
+    }
+    if (ok) a.out[(int64_t)n * a.out_f + i] = my_fire;
+}
+
+// Engine feed-forward currents of an FC layer: one wave per (sample, arrival
+// bin, 64 outputs); lanes are outputs.  cur[n][t][o] = sum over the bin's
+// events, in ascending input index, of W[j][o] (the weights transposed to
+// [in][out], so each event is one coalesced row segment).  Bins are
+// independent, so the T bins of a sample run in parallel while each bin's
+// sum keeps the reference's order.
+__global__ __launch_bounds__(256) void k_bin_currents(const vd_event* __restrict__ ev,
+                                                      const int32_t* __restrict__ off,
+                                                      const float* __restrict__ W,
+                                                      float* __restrict__ cur, int N, int T,
+                                                      int in_f, int out_f, int n_oblk) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t, oblk)
+    if (u >= (int64_t)N * T * n_oblk) return;
+    const int ob = (int)(u % n_oblk);
+    const int t = (int)((u / n_oblk) % T);
+    const int64_t n = u / ((int64_t)n_oblk * T);
+    const int o = ob * 64 + lane_id();
+    const bool ok = o < out_f;
+    const int oo = ok ? o : 0;
+    const int32_t* BO = off + n * (T + 1);
+    const int s = BO[t], e = BO[t + 1];
+    const vd_event* E = ev + n * (int64_t)in_f;
+    float acc = 0.0f;
+    int p = s;
+    for (; p + 8 <= e; p += 8) {
+        float w[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) w[g] = W[(int64_t)(E[p + g].key & 0xFFFFFFu) * out_f + oo];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) acc = acc + w[g];
+    }
+    for (; p < e; ++p) acc = acc + W[(int64_t)(E[p].key & 0xFFFFFFu) * out_f + oo];
+    if (ok) cur[(n * T + t) * out_f + o] = acc;
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_nhwc_to_nchw(const float* __restrict__ in,
+                                                      float* __restrict__ out, int64_t total, int C,
+                                                      int H, int W) {
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int x = (int)(idx % W);
+        const int y = (int)((idx / W) % H);
+        const int c = (int)((idx / ((int64_t)W * H)) % C);
+        const int64_t n = idx / ((int64_t)W * H * C);
+        out[idx] = in[((n * H + y) * W + x) * C + c];
+    }
+}
+
+unsigned flat_grid(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    if (b > (1 << 20)) b = 1 << 20;
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+int check_culif_consts(const vdttfs_ctx* ctx) {
+    if (ctx->c.T % ctx->c.delta != 0)
+        return set_error(VDTTFS_E_UNSUPPORTED,
+                         "CuLIF layers need delta to divide T (the reference chunk loop has no t < T guard)");
+    return VDTTFS_OK;
+}
+
+int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
+                           int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th) {
+    VD_TRY(check_culif_consts(ctx));
+    if (N <= 0 || C_in <= 0 || C_out <= 0 || H <= 0 || Wd <= 0)
+        return set_error(VDTTFS_E_INVALID, "culif_conv1_raw: non-positive shape");
+    RawArgs a{};
+    a.data = data;
+    a.out = out;
+    a.W = W;
+    a.n_pix = (int64_t)N * H * Wd;
+    a.C_in = C_in;
+    a.C_out = C_out;
+    a.H = H;
+    a.Wd = Wd;
+    a.T = ctx->c.T;
+    a.n_cblk = (C_out + 63) / 64;
+    if (nhwc_out) {
+        a.sX = C_out;
+        a.sY = (int64_t)Wd * C_out;
+        a.sN = (int64_t)H * Wd * C_out;
+        a.sC = 1;
+    } else {
+        a.sX = 1;
+        a.sY = Wd;
+        a.sC = (int64_t)H * Wd;
+        a.sN = (int64_t)C_out * H * Wd;
+    }
+    a.decay = decay;
+    a.th = th;
+    const int64_t blocks = ((a.n_pix + 3) / 4) * a.n_cblk;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_raw: grid too large");
+    hipLaunchKernelGGL(k_culif_conv1_raw, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_culif_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_sites, int C, int HW,
+                           int32_t* cin, float* tin, int32_t* off) {
+    VD_TRY(check_culif_consts(ctx));
+    const int NC = ctx->c.T / ctx->c.delta;
+    if (NC > kCBktMaxChunks)
+        return set_error(VDTTFS_E_UNSUPPORTED, "culif bucketize: T/delta = %d chunks > %d", NC,
+                         kCBktMaxChunks);
+    if (n_sites <= 0 || C <= 0 || HW <= 0) return set_error(VDTTFS_E_INVALID, "culif bucketize: bad shape");
+    CBktArgs a{in, cin, tin, off, n_sites, C, HW, ctx->c.T, ctx->c.delta, NC};
+    const int64_t blocks = (n_sites + kCBktThreads - 1) / kCBktThreads;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif bucketize: grid too large");
+    hipLaunchKernelGGL(k_culif_bucketize, dim3((unsigned)blocks), dim3(kCBktThreads), 0, ctx->stream, a);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_culif_generic(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, const int32_t* off,
+                         float* out, const float* W, int N, int C_in, int C_out, int H, int Wd,
+                         int is_fc, float decay, float th) {
+    VD_TRY(check_culif_consts(ctx));
+    CGenArgs a{};
+    a.cin = cin;
+    a.tin = tin;
+    a.off = off;
+    a.out = out;
+    a.W = W;
+    a.C_in = C_in;
+    a.C_out = C_out;
+    a.H = is_fc ? 1 : H;
+    a.Wd = is_fc ? 1 : Wd;
+    a.T = ctx->c.T;
+    a.D = ctx->c.delta;
+    a.NC = a.T / a.D;
+    a.decay = decay;
+    a.th = th;
+    a.total = (int64_t)N * C_out * a.H * a.Wd;
+    if (a.total <= 0) return set_error(VDTTFS_E_INVALID, "culif integrate: bad shape");
+    const unsigned g = flat_grid(a.total);
+#define VD_CG(FC, DM) hipLaunchKernelGGL((k_culif_generic<FC, DM>), dim3(g), dim3(256), 0, ctx->stream, a)
+    if (a.D <= 32) {
+        if (is_fc) VD_CG(true, 32); else VD_CG(false, 32);
+    } else if (a.D <= 64) {
+        if (is_fc) VD_CG(true, 64); else VD_CG(false, 64);
+    } else {
+        if (is_fc) VD_CG(true, 256); else VD_CG(false, 256);
+    }
+#undef VD_CG
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_culif_pool(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H_in, int W_in,
+                      int nhwc_in, int nhwc_out, float decay, float th) {
+    VD_TRY(check_culif_consts(ctx));
+    if (N <= 0 || C <= 0 || H_in < 2 || W_in < 2)
+        return set_error(VDTTFS_E_INVALID, "culif_pool: bad shape");
+    const int H_out = H_in / 2, W_out = W_in / 2;
+    CPoolArgs a{};
+    a.in = in;
+    a.out = out;
+    a.total = (int64_t)N * C * H_out * W_out;
+    a.C = C;
+    a.H_in = H_in;
+    a.W_in = W_in;
+    a.T = ctx->c.T;
+    a.nhwc = nhwc_out;
+    if (nhwc_in) {
+        a.iC = 1; a.iX = C; a.iY = (int64_t)W_in * C; a.iN = (int64_t)H_in * W_in * C;
+    } else {
+        a.iX = 1; a.iY = W_in; a.iC = (int64_t)H_in * W_in; a.iN = (int64_t)C * H_in * W_in;
+    }
+    if (nhwc_out) {
+        a.oC = 1; a.oX = C; a.oY = (int64_t)W_out * C; a.oN = (int64_t)H_out * W_out * C;
+    } else {
+        a.oX = 1; a.oY = W_out; a.oC = (int64_t)H_out * W_out; a.oN = (int64_t)C * H_out * W_out;
+    }
+    a.decay = decay;
+    a.th = th;
+    hipLaunchKernelGGL(k_culif_pool, dim3(flat_grid(a.total)), dim3(256), 0, ctx->stream, a);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, const int32_t* off,
+                        const float* cur, float* out, const float* W, const float* Wrec, int N,
+                        int in_f, int out_f, float decay, float th) {
+    VD_TRY(check_culif_consts(ctx));
+    if (N <= 0 || in_f <= 0 || out_f <= 0 || out_f > 1024)
+        return set_error(VDTTFS_E_UNSUPPORTED, "culif_fc_recurrent: needs 1 <= out_f <= 1024");
+    CRecArgs a{};
+    a.cin = cin;
+    a.tin = tin;
+    a.off = off;
+    a.cur = cur;
+    a.out = out;
+    a.W = W;
+    a.Wrec = Wrec;
+    a.in_f = in_f;
+    a.out_f = out_f;
+    a.out_pad = (out_f + 63) / 64 * 64;
+    a.T = ctx->c.T;
+    a.D = ctx->c.delta;
+    a.NC = a.T / a.D;
+    a.decay = decay;
+    a.th = th;
+    if (cur) {
+        hipLaunchKernelGGL(k_culif_fc_rec<true>, dim3(N), dim3(a.out_pad), 0, ctx->stream, a);
+    } else {
+        const size_t lds = (size_t)a.D * a.out_pad * sizeof(float);
+        if (lds > 64 * 1024)
+            return set_error(VDTTFS_E_UNSUPPORTED, "culif_fc_recurrent: delta*out_f*4 = %zu B > 64 KB", lds);
+        hipLaunchKernelGGL(k_culif_fc_rec<false>, dim3(N), dim3(a.out_pad), lds, ctx->stream, a);
+    }
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_bin_currents(vdttfs_ctx* ctx, const vd_event* ev, const int32_t* off, const float* W_t,
+                        float* cur, int N, int in_f, int out_f) {
+    if (in_f >= (1 << 24)) return set_error(VDTTFS_E_UNSUPPORTED, "bin currents: in_f >= 2^24");
+    const int T = ctx->c.T;
+    const int n_oblk = (out_f + 63) / 64;
+    const int64_t waves = (int64_t)N * T * n_oblk;
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "bin currents: grid too large");
+    hipLaunchKernelGGL(k_bin_currents, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, ev, off, W_t,
+                       cur, N, T, in_f, out_f, n_oblk);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+int launch_nhwc_to_nchw(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H, int W) {
+    const int64_t total = (int64_t)N * C * H * W;
+    hipLaunchKernelGGL(k_nhwc_to_nchw, dim3(flat_grid(total)), dim3(256), 0, ctx->stream, in, out,
+                       total, C, H, W);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+}  // namespace vdttfs

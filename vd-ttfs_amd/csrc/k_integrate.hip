@@ -194,6 +194,7 @@ struct StreamArgs {
     int64_t cap;
     int T, D, t_min, C_out, n_cblk;
     int w_bytes;
+    float decay, th;  // CuLIF neuron (T3V:62-63): I = I*decay + in; V += I; fire at V >= th
 };
 
 // Block -> (c_out block, group of 4 output pixels).  Workgroups are dealt to
@@ -254,8 +255,12 @@ struct GlobalGather {
 
 
 // Integrates one output pixel for one c_out block (lane = VEC c_out) from its
-// merged event list and writes the first-spike times.
-template <bool COUNT, int VEC, class G>
+// merged event list and writes the first-spike times.  CULIF selects the
+// neuron that closes each bin: the LUT-threshold neuron of T1V/T2V (carry +=
+// delta_t, fire at carry >= theta[t] >= 1e-5, t >= t_min) or the CuLIF neuron
+// of T3V (I = fma(I, decay, in_t); V += I; fire at V >= th).  CuLIF events
+// carry alpha = 1, so fma(w, 1, acc) is exactly the reference's acc + w.
+template <bool COUNT, int VEC, bool CULIF, class G>
 __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
                                              const int2* __restrict__ list,
                                              const int32_t* __restrict__ bstart,
@@ -270,11 +275,12 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
     const int2* __restrict__ L = list + pix * a.cap;
     const int32_t* __restrict__ BS = bstart + pix * (int64_t)(a.T + 1);
 
-    float carry[VEC], res[VEC];
+    float carry[VEC], cur[VEC], res[VEC];  // carry: membrane (V for CuLIF); cur: CuLIF current I
     bool alive[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-        carry[v] = ok[v] ? a.bias[c0 + v] : 0.0f;
+        carry[v] = (ok[v] && !CULIF) ? a.bias[c0 + v] : 0.0f;
+        cur[v] = 0.0f;
         res[v] = kInfTime;
         alive[v] = ok[v];
     }
@@ -292,7 +298,7 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         const int nb = (T - t0) < kBlockBins ? (T - t0) : kBlockBins;
         // lane d keeps bin t0+d's merged start and threshold
         const int v_bs = lane < nb ? BS[t0 + lane] : 0;
-        const float v_th = lane < nb ? theta[t0 + lane] : 0.0f;
+        const float v_th = (!CULIF && lane < nb) ? theta[t0 + lane] : 0.0f;
         const int blk_end = BS[t0 + nb];
         asm volatile("" ::"v"(v_bs), "v"(v_th));  // complete these loads before streaming
 
@@ -307,13 +313,24 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
             cnt_bin += (unsigned long long)n_ * nl_;                                    \
             cnt_proc += (unsigned long long)n_ * live_chunk_n;                          \
         }                                                                               \
-        const float th_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), (b))); \
-        const bool can_ = t_ >= a.t_min && th_ >= 1e-5f;                                \
-        _Pragma("unroll") for (int v = 0; v < VEC; ++v) {                               \
-            carry[v] = carry[v] + (acc_)[v];                                            \
-            if (can_ && alive[v] && carry[v] >= th_) {                                  \
-                res[v] = (float)t_;                                                     \
-                alive[v] = false;                                                       \
+        if (CULIF) {                                                                    \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) {                           \
+                cur[v] = __builtin_fmaf(cur[v], a.decay, (acc_)[v]);                    \
+                carry[v] = carry[v] + cur[v];                                           \
+                if (alive[v] && carry[v] >= a.th) {                                     \
+                    res[v] = (float)t_;                                                 \
+                    alive[v] = false;                                                   \
+                }                                                                       \
+            }                                                                           \
+        } else {                                                                        \
+            const float th_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), (b))); \
+            const bool can_ = t_ >= a.t_min && th_ >= 1e-5f;                            \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) {                           \
+                carry[v] = carry[v] + (acc_)[v];                                        \
+                if (can_ && alive[v] && carry[v] >= th_) {                              \
+                    res[v] = (float)t_;                                                 \
+                    alive[v] = false;                                                   \
+                }                                                                       \
             }                                                                           \
         }                                                                               \
         live = alive[0];                                                                \
@@ -400,7 +417,7 @@ stream_done:
         if (ok[v]) out[pix * a.C_out + c0 + v] = res[v];
 }
 
-template <bool COUNT, int VEC>
+template <bool COUNT, int VEC, bool CULIF>
 __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict__ out,
                                                 const int2* __restrict__ list,
                                                 const int32_t* __restrict__ bstart,
@@ -416,7 +433,7 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     g.r = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
     g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
     unsigned long long cnt_proc = 0, cnt_bin = 0;
-    stream_pixel<COUNT, VEC>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
+    stream_pixel<COUNT, VEC, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
     if (COUNT && lane_id() == 0) {
         atomicAdd(&a.counters[0], cnt_proc);
         atomicAdd(&a.counters[1], cnt_bin);
@@ -663,14 +680,18 @@ int merged_list_cap(const IntegShape& sh) {
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
                           int2* list, int64_t list_cap, int32_t* bstart, const float* W,
                           const float* bias, const float* theta, int t_min, const IntegShape& sh,
-                          unsigned long long* counters) {
+                          unsigned long long* counters, const CulifNeuron* culif) {
     const int T = ctx->c.T, D = ctx->c.delta;
     const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
     const int64_t wbytes = (int64_t)nk_max * sh.C_in * sh.C_out * 4;
     const bool wave_ok = sh.C_out >= 32 && nk_max <= 25 && wbytes < INT64_C(0x7fffffff) &&
                          sh.C_in < (1 << 24);
-    if (!wave_ok)
+    if (!wave_ok) {
+        if (culif)
+            return set_error(VDTTFS_E_UNSUPPORTED,
+                             "CuLIF engine layers need C_out >= 32, <= 25 taps and < 2 GB of weights");
         return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
+    }
     const int64_t n_pix = (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
     if (!list || !bstart || list_cap < cap)
@@ -717,6 +738,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     a.D = D;
     a.t_min = t_min;
     a.C_out = sh.C_out;
+    a.decay = culif ? culif->decay : 0.0f;
+    a.th = culif ? culif->th : 0.0f;
     // 4 c_out per lane once a wave's 64 lanes hold >= 128 c_out
     const int vec = (sh.C_out >= 128 && sh.C_out % 4 == 0) ? 4 : 1;
     a.n_cblk = (sh.C_out + 64 * vec - 1) / (64 * vec);
@@ -726,20 +749,28 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     const int64_t blocks = n_pg * a.n_cblk;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-#define VD_LAUNCH_STREAM(C, V)                                                              \
-    hipLaunchKernelGGL((k_stream<C, V>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
+#define VD_LAUNCH_STREAM(C, V, L)                                                               \
+    hipLaunchKernelGGL((k_stream<C, V, L>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
                        a, out, (const int2*)list, (const int32_t*)bstart, theta)
-    if (vec == 4) {
+#define VD_LAUNCH_STREAM_V(C, L)    \
+    do {                            \
+        if (vec == 4)               \
+            VD_LAUNCH_STREAM(C, 4, L); \
+        else                        \
+            VD_LAUNCH_STREAM(C, 1, L); \
+    } while (0)
+    if (culif) {
         if (counters)
-            VD_LAUNCH_STREAM(true, 4);
+            VD_LAUNCH_STREAM_V(true, true);
         else
-            VD_LAUNCH_STREAM(false, 4);
+            VD_LAUNCH_STREAM_V(false, true);
     } else {
         if (counters)
-            VD_LAUNCH_STREAM(true, 1);
+            VD_LAUNCH_STREAM_V(true, false);
         else
-            VD_LAUNCH_STREAM(false, 1);
+            VD_LAUNCH_STREAM_V(false, false);
     }
+#undef VD_LAUNCH_STREAM_V
 #undef VD_LAUNCH_STREAM
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;

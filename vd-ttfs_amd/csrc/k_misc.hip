@@ -96,12 +96,15 @@ __global__ void k_fc_vmem(const float* __restrict__ in, float* __restrict__ out,
 
 // T1V:312-319 (argmin from INF, strict <, -1 if nothing fired) and
 // T2V:389-396 (argmax from -1e9, strict >).
+// mode 0: argmin from INF, pred -1 if nothing fired (T1V:312-319);
+// 1: argmax from -1e9 (T2V:389-396); 2: argmin seeded with class 0
+// (T3V:291-298).  Strict comparisons: the first extremum wins.
 __global__ void k_readout(const float* __restrict__ out, int B, int C, int32_t* __restrict__ pred,
-                          int argmax) {
+                          int mode) {
     for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < B; b += gridDim.x * blockDim.x) {
         const float* row = out + (int64_t)b * C;
         int p = -1;
-        if (argmax) {
+        if (mode == 1) {
             float m = -1e9f;
             for (int i = 0; i < C; ++i)
                 if (row[i] > m) {
@@ -110,7 +113,13 @@ __global__ void k_readout(const float* __restrict__ out, int B, int C, int32_t* 
                 }
         } else {
             float m = kInfTime;
-            for (int i = 0; i < C; ++i)
+            int i0 = 0;
+            if (mode == 2) {
+                p = 0;
+                m = row[0];
+                i0 = 1;
+            }
+            for (int i = i0; i < C; ++i)
                 if (row[i] < m) {
                     m = row[i];
                     p = i;
@@ -157,10 +166,11 @@ int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W,
     return VDTTFS_OK;
 }
 
-int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int argmax) {
+int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pred, int mode) {
     if (B <= 0) return VDTTFS_OK;
+    if (C <= 0 || mode < 0 || mode > 2) return set_error(VDTTFS_E_INVALID, "readout: bad C or mode");
     hipLaunchKernelGGL(k_readout, dim3(grid_for(B)), dim3(kThreads), 0, ctx->stream, out, B, C, pred,
-                       argmax);
+                       mode);
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }

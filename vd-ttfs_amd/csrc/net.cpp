@@ -194,7 +194,7 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
     if (d_pred) {
         const vdttfs_layer_desc& last = net->L.back().d;
         VD_TRY(launch_readout(ctx, cur, net->B, last.H_out * last.W_out * last.C_out, d_pred,
-                              net->readout == VDTTFS_READOUT_ARGMAX));
+                              net->readout));
     }
     return VDTTFS_OK;
 }
@@ -311,7 +311,8 @@ int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_la
     *out = nullptr;
     if (encode_mode != VDTTFS_ENCODE_LINEAR && encode_mode != VDTTFS_ENCODE_LOG)
         return set_error(VDTTFS_E_INVALID, "net_create: encode mode %d", encode_mode);
-    if (readout != VDTTFS_READOUT_ARGMIN && readout != VDTTFS_READOUT_ARGMAX)
+    if (readout != VDTTFS_READOUT_ARGMIN && readout != VDTTFS_READOUT_ARGMAX &&
+        readout != VDTTFS_READOUT_ARGMIN_FIRST)
         return set_error(VDTTFS_E_INVALID, "net_create: readout %d", readout);
     VD_TRY(validate(ctx->c, layers, n_layers, img_elems));
     vdttfs_net* net = new (std::nothrow) vdttfs_net();

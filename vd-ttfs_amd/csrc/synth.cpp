@@ -4,6 +4,7 @@
 // in fp64.  Host-only; the same arrays feed the GPU engine and the CPU
 // baseline, so results never depend on where a number was drawn.
 #include <cmath>
+#include <vector>
 
 #include "common.h"
 
@@ -47,6 +48,40 @@ int vdttfs_synth_normal(uint64_t seed, uint64_t stream, float* out, int64_t n, d
         const double r = std::sqrt(-2.0 * std::log(u1));
         out[i] = (float)(sigma * r * std::cos(two_pi * u2));
         if (i + 1 < n) out[i + 1] = (float)(sigma * r * std::sin(two_pi * u2));
+    }
+    return VDTTFS_OK;
+}
+
+int vdttfs_synth_dvs(uint64_t seed, int N, int C, int H, int W, int T, double density, double sigma,
+                     double vmax, float* out, double* scales) {
+    if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || T <= 0 || !out || !(sigma > 0.0) || !(density > 0.0))
+        return set_error(VDTTFS_E_INVALID, "synth_dvs: bad args");
+    const int64_t per = (int64_t)C * H * W * T;
+    if (per >= (INT64_C(1) << 40)) return set_error(VDTTFS_E_INVALID, "synth_dvs: sample too large");
+    std::vector<double> g((size_t)H * W * T);
+    for (int n = 0; n < N; ++n) {
+        auto u = [&](int k) { return (double)(draw(seed, 3000 + (uint64_t)n, (uint64_t)k) >> 40) * 0x1.0p-24; };
+        const double cx0 = W * (0.25 + 0.5 * u(0)), cy0 = H * (0.25 + 0.5 * u(1));
+        const double vx = vmax * (2.0 * u(2) - 1.0), vy = vmax * (2.0 * u(3) - 1.0);
+        double sum = 0.0;
+        for (int y = 0; y < H; ++y)
+            for (int x = 0; x < W; ++x)
+                for (int t = 0; t < T; ++t) {
+                    const double dx = x - (cx0 + vx * t), dy = y - (cy0 + vy * t);
+                    const double v = std::exp(-(dx * dx + dy * dy) / (2.0 * sigma * sigma));
+                    g[((size_t)y * W + x) * T + t] = v;
+                    sum += v;
+                }
+        const double scale = sum > 0.0 ? density * (double)H * W * T / sum : 0.0;
+        if (scales) scales[n] = scale;
+        float* o = out + (int64_t)n * per;
+        for (int c = 0; c < C; ++c)
+            for (int64_t k = 0; k < (int64_t)H * W * T; ++k) {
+                const double p = std::fmin(1.0, scale * g[(size_t)k]);
+                const int64_t idx = (int64_t)c * H * W * T + k;
+                const double r = (double)(draw(seed, 2000 + (uint64_t)n, (uint64_t)idx) >> 40) * 0x1.0p-24;
+                o[idx] = r < p ? 1.0f : 0.0f;
+            }
     }
     return VDTTFS_OK;
 }

@@ -25,7 +25,8 @@ INF_TIME = 9999.0
 
 LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM = 0, 1, 2, 3
 ENCODE_LINEAR, ENCODE_LOG = 0, 1
-READOUT_ARGMIN, READOUT_ARGMAX = 0, 1
+READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
+CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
 
 
 class VdttfsError(RuntimeError):
@@ -100,6 +101,20 @@ class LayerDesc(C.Structure):
     ]
 
 
+class CulifLayer(C.Structure):
+    _fields_ = [
+        ("kind", C.c_int32),
+        ("C_in", C.c_int32),
+        ("H_in", C.c_int32),
+        ("W_in", C.c_int32),
+        ("C_out", C.c_int32),
+        ("weight", C.POINTER(C.c_float)),
+        ("weight_rec", C.POINTER(C.c_float)),
+        ("decay", C.c_float),
+        ("th", C.c_float),
+    ]
+
+
 _vp = C.c_void_p
 _i = C.c_int
 _i64 = C.c_int64
@@ -153,6 +168,21 @@ SIGNATURES = {
                                C.POINTER(C.c_double), C.POINTER(_i64)],
     "vdttfs_synth_uniform": [C.c_uint64, C.c_uint64, _vp, _i64],
     "vdttfs_synth_normal": [C.c_uint64, C.c_uint64, _vp, _i64, C.c_double],
+    "vdttfs_synth_dvs": [C.c_uint64, _i, _i, _i, _i, _i, C.c_double, C.c_double, C.c_double, _vp,
+                         _vp],
+    "vdttfs_culif_conv1_raw": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f],
+    "vdttfs_culif_bucketize_conv": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "vdttfs_culif_bucketize_fc": [_vp, _vp, _i, _i, _vp, _vp, _vp],
+    "vdttfs_culif_conv": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f],
+    "vdttfs_culif_pool": [_vp, _vp, _vp, _i, _i, _i, _i, _f, _f],
+    "vdttfs_culif_fc_recurrent": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f],
+    "vdttfs_culif_fc": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f],
+    "vdttfs_readout_argmin_first": [_vp, _vp, _i, _i, _vp],
+    "vdttfs_culif_net_create": [_vp, C.POINTER(CulifLayer), _i, _i, C.POINTER(_vp)],
+    "vdttfs_culif_net_destroy": [_vp],
+    "vdttfs_culif_net_forward": [_vp, _vp, _vp],
+    "vdttfs_culif_net_layer_output": [_vp, _i, C.POINTER(_vp), C.POINTER(_i64),
+                                      C.POINTER(C.c_int32)],
 }
 
 _RESTYPES = {"vdttfs_last_error": C.c_char_p, "vdttfs_version": C.c_char_p}

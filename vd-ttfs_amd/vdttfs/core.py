@@ -14,9 +14,10 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import (Consts, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
+from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
                    LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG,
-                   READOUT_ARGMIN, READOUT_ARGMAX)
+                   READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
+                   CULIF_FC_REC, CULIF_FC)
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -55,6 +56,11 @@ def task1_consts(T=80, delta=16) -> TaskConsts:
 
 def task2_consts(T=80, delta=8, tfs=40.0) -> TaskConsts:
     return TaskConsts(T=T, tfs=tfs, delta=delta, vth=1.0, alpha_by_time=True, conv_same_pad=True)
+
+
+# Task 3 (CuLIF, T3V:17-21): T_TOTAL and CHUNK_SIZE; no fire start, no LUTs
+def task3_consts(T=160, delta=32) -> TaskConsts:
+    return TaskConsts(T=T, tfs=0.0, delta=delta, vth=1.0, alpha_by_time=False, conv_same_pad=True)
 
 
 def build_luts_host(consts: TaskConsts, tc_integ, td_integ, tc_fire, td_fire):
@@ -195,6 +201,37 @@ class Context:
                                              H_out, W_out, C_out, K_h, K_w, td, d_kernel.ptr,
                                              d_bias.ptr, d_alpha.ptr, d_theta.ptr, B, int(is_fc)))
 
+    # CuLIF set (T3V:30-225), reference layouts
+    def culif_conv1_raw(self, d_data, d_out, d_weight, N, C_in, C_out, H, W, decay, th):
+        check(lib().vdttfs_culif_conv1_raw(self.handle, d_data.ptr, d_out.ptr, d_weight.ptr, N, C_in,
+                                           C_out, H, W, decay, th))
+
+    def culif_bucketize_conv(self, d_in, N, Cc, H, W, d_cin, d_tin, d_off):
+        check(lib().vdttfs_culif_bucketize_conv(self.handle, d_in.ptr, N, Cc, H, W, d_cin.ptr,
+                                                d_tin.ptr, d_off.ptr))
+
+    def culif_bucketize_fc(self, d_in, N, F, d_cin, d_tin, d_off):
+        check(lib().vdttfs_culif_bucketize_fc(self.handle, d_in.ptr, N, F, d_cin.ptr, d_tin.ptr,
+                                              d_off.ptr))
+
+    def culif_conv(self, d_cin, d_tin, d_off, d_out, d_weight, N, C_in, C_out, H, W, decay, th):
+        check(lib().vdttfs_culif_conv(self.handle, d_cin.ptr, d_tin.ptr, d_off.ptr, d_out.ptr,
+                                      d_weight.ptr, N, C_in, C_out, H, W, decay, th))
+
+    def culif_pool(self, d_in, d_out, N, Cc, H_in, W_in, decay, th):
+        check(lib().vdttfs_culif_pool(self.handle, d_in.ptr, d_out.ptr, N, Cc, H_in, W_in, decay, th))
+
+    def culif_fc_recurrent(self, d_cin, d_tin, d_off, d_out, d_w, d_w_rec, N, in_f, out_f, decay, th):
+        check(lib().vdttfs_culif_fc_recurrent(self.handle, d_cin.ptr, d_tin.ptr, d_off.ptr, d_out.ptr,
+                                              d_w.ptr, d_w_rec.ptr, N, in_f, out_f, decay, th))
+
+    def culif_fc(self, d_cin, d_tin, d_off, d_out, d_w, N, in_f, out_f, decay, th):
+        check(lib().vdttfs_culif_fc(self.handle, d_cin.ptr, d_tin.ptr, d_off.ptr, d_out.ptr, d_w.ptr,
+                                    N, in_f, out_f, decay, th))
+
+    def readout_argmin_first(self, d_out, B, Cc, d_pred):
+        check(lib().vdttfs_readout_argmin_first(self.handle, d_out.ptr, B, Cc, d_pred.ptr))
+
     def launch_pool(self, d_in, d_out, H_in, W_in, Cc, B):
         check(lib().vdttfs_launch_pool_sync(self.handle, d_in.ptr, d_out.ptr, H_in, W_in, Cc, B))
 
@@ -281,3 +318,74 @@ class Net:
         check(lib().vdttfs_net_read_timing(self.handle, C.byref(im), C.byref(il), C.byref(bm),
                                            C.byref(bl)))
         return im.value, il.value, bm.value, bl.value
+
+
+@dataclass
+class CulifLayerSpec:
+    """One layer of the CuLIF engine (vdttfs_culif_layer): conv weights OIHW
+    [C_out][C_in][3][3], FC weights [out][in], FC_REC also [out][out]."""
+    kind: int
+    C_in: int
+    H_in: int
+    W_in: int
+    C_out: int
+    weight: np.ndarray | None = None
+    weight_rec: np.ndarray | None = None
+    decay: float = 0.5
+    th: float = 1.0
+
+    @property
+    def out_shape(self):
+        if self.kind in (CULIF_FC, CULIF_FC_REC):
+            return (self.C_out, 1, 1)
+        if self.kind == CULIF_POOL:
+            return (self.C_out, self.H_in // 2, self.W_in // 2)
+        return (self.C_out, self.H_in, self.W_in)
+
+    def to_c(self) -> CulifLayer:
+        fp = C.POINTER(C.c_float)
+        w = self.weight.ctypes.data_as(fp) if self.weight is not None else fp()
+        r = self.weight_rec.ctypes.data_as(fp) if self.weight_rec is not None else fp()
+        return CulifLayer(self.kind, self.C_in, self.H_in, self.W_in, self.C_out, w, r, self.decay,
+                          self.th)
+
+
+class CulifNet:
+    """The CuLIF engine: dense events -> layers -> readout (T3V:276-298)."""
+
+    def __init__(self, ctx: Context, layers: list[CulifLayerSpec], B: int):
+        self.ctx = ctx
+        self.layers = layers
+        self.B = B
+        for l in layers:
+            if l.weight is not None:
+                l.weight = np.ascontiguousarray(l.weight, np.float32)
+            if l.weight_rec is not None:
+                l.weight_rec = np.ascontiguousarray(l.weight_rec, np.float32)
+        arr = (CulifLayer * len(layers))(*[l.to_c() for l in layers])
+        h = C.c_void_p()
+        check(lib().vdttfs_culif_net_create(ctx.handle, arr, len(layers), B, C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle is not None:
+            lib().vdttfs_culif_net_destroy(self.handle)
+            self.handle = None
+
+    def forward(self, d_data: DeviceArray, d_pred: DeviceArray | None = None):
+        check(lib().vdttfs_culif_net_forward(self.handle, d_data.ptr, d_pred.ptr if d_pred else None))
+
+    def layer_output(self, i: int, layout: str = "nchw") -> np.ndarray:
+        """Layer i's output as [B][C][H][W] (layout "nchw") whatever the engine
+        keeps internally."""
+        p = C.c_void_p()
+        n = C.c_int64()
+        nhwc = C.c_int32()
+        check(lib().vdttfs_culif_net_layer_output(self.handle, i, C.byref(p), C.byref(n),
+                                                  C.byref(nhwc)))
+        h = np.empty(n.value, np.float32)
+        check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), p, h.nbytes))
+        Cc, H, W = self.layers[i].out_shape
+        if nhwc.value:
+            h = h.reshape(self.B, H, W, Cc).transpose(0, 3, 1, 2)
+        return np.ascontiguousarray(h.reshape(self.B, Cc, H, W)) if layout == "nchw" else h

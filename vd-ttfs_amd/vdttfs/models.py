@@ -6,6 +6,7 @@ batch does not depend on the batch size.
 
   config 1/2  LeNet-5 TTFS-SNN, T=64, Delta=16, Task-1 semantics (T1V)
   config 3    VGG-16 TTFS-SNN,  T=64, Delta=8, TFS=32, Task-2 semantics (T2V)
+  config 4    7-layer CuLIF SNN on a synthetic 2x128x128 event stream (T3V)
   config 5    one FC 4096->4096 layer, spike density / window / Delta sweep
 
 Weights are Kaiming-normal (sigma = sqrt(2/fan_in), fan_in = K_h*K_w*C_in),
@@ -21,8 +22,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from ._lib import check, lib
-from .core import (LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, READOUT_ARGMAX, READOUT_ARGMIN,
-                   Layer, TaskConsts)
+from .core import (CULIF_CONV, CULIF_FC, CULIF_FC_REC, CULIF_POOL, CULIF_RAW_CONV, LAYER_CONV,
+                   LAYER_FC, LAYER_POOL, LAYER_VMEM, READOUT_ARGMAX, READOUT_ARGMIN, CulifLayerSpec,
+                   Layer, TaskConsts, task3_consts)
 
 STREAM_IMG = 1
 STREAM_IMG_VALUE = 2
@@ -165,3 +167,58 @@ def fc_sweep_spikes(seed: int, B: int, cin: int, density: float, T: int = 64) ->
     act = uniform(seed, STREAM_IMG, n) < np.float32(density)
     t = np.floor(uniform(seed, STREAM_IMG_VALUE, n) * np.float32(T)).astype(np.float32)
     return np.where(act, t, np.float32(9999.0)).astype(np.float32).reshape(B, cin)
+
+
+# ---- config 4: CuLIF on a synthetic event stream (T3V) ----------------------
+@dataclass
+class CulifWorkload:
+    name: str
+    consts: TaskConsts
+    layers: list              # CulifLayerSpec
+    in_shape: tuple           # (C, H, W) of one sample; events are [C][H][W][T]
+    n_classes: int
+    seed: int
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def n_params(self) -> int:
+        return int(sum((0 if l.weight is None else l.weight.size) +
+                       (0 if l.weight_rec is None else l.weight_rec.size) for l in self.layers))
+
+
+def culif7(seed: int = 4, T: int = 64, delta: int = 32, H: int = 128, W: int = 128,
+           n_classes: int = 11, decay: float = 0.5, th: float = 1.0) -> CulifWorkload:
+    """Config 4, T3V's topology (T3V:276-289) at 2xHxW input:
+    conv 2->64 (raw events) -> conv 64->128 -> pool -> conv 128->128 -> pool
+    -> recurrent FC 128*(H/4)*(W/4) -> 128 -> FC 128 -> n_classes.
+    One decay and threshold for every layer; Kaiming-normal OIHW / [out][in]
+    weights (recurrent weights fan_in 128)."""
+    consts = task3_consts(T=T, delta=delta)
+    h2, w2 = H // 4, W // 4
+    F = 128 * h2 * w2
+    L = [
+        CulifLayerSpec(CULIF_RAW_CONV, 2, H, W, 64, kaiming(seed, 0, (64, 2, 3, 3), 2 * 9), None, decay, th),
+        CulifLayerSpec(CULIF_CONV, 64, H, W, 128, kaiming(seed, 1, (128, 64, 3, 3), 64 * 9), None, decay, th),
+        CulifLayerSpec(CULIF_POOL, 128, H, W, 128, None, None, decay, th),
+        CulifLayerSpec(CULIF_CONV, 128, H // 2, W // 2, 128, kaiming(seed, 2, (128, 128, 3, 3), 128 * 9),
+                       None, decay, th),
+        CulifLayerSpec(CULIF_POOL, 128, H // 2, W // 2, 128, None, None, decay, th),
+        CulifLayerSpec(CULIF_FC_REC, F, 1, 1, 128, kaiming(seed, 3, (128, F), F),
+                       kaiming(seed, 4, (128, 128), 128), decay, th),
+        CulifLayerSpec(CULIF_FC, 128, 1, 1, n_classes, kaiming(seed, 5, (n_classes, 128), 128), None,
+                       decay, th),
+    ]
+    return CulifWorkload("culif7-dvs", consts, L, (2, H, W), n_classes, seed,
+                         meta={"decay": decay, "th": th, "density": 0.03, "sigma_px": 12.0,
+                               "vmax_px_per_step": 0.5})
+
+
+def dvs_events(w: CulifWorkload, B: int) -> np.ndarray:
+    """[B][C][H][W][T] in {0,1}: a Gaussian blob (sigma 12 px) moving linearly
+    at up to 0.5 px/step per axis, Bernoulli events with mean density 0.03."""
+    Cc, H, W = w.in_shape
+    T = w.consts.T
+    out = np.empty((B, Cc, H, W, T), np.float32)
+    check(lib().vdttfs_synth_dvs(w.seed, B, Cc, H, W, T, w.meta["density"], w.meta["sigma_px"],
+                                 w.meta["vmax_px_per_step"], C.c_void_p(out.ctypes.data), None))
+    return out
