@@ -11,6 +11,13 @@ reference algorithm (oracle/, timed on a bounded sample).
   python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
   python bench.py --copy-calibration   # known-size copy for FETCH/WRITE_SIZE scaling
 
+The other synthetic workloads print one line each in the same format
+(parity cases of the same engine, not the headline):
+
+  python bench.py --workload lenet5     # config 2: LeNet-5, B=1024 (config 1 = its B=1 CPU leg)
+  python bench.py --workload culif7     # config 4: 7-layer CuLIF on 2x128x128 events, B=64
+  python bench.py --workload fc-sweep   # config 5: FC 4096x4096, B=512, density/T'/delta sweep
+
 roofline.traffic is the integrator's HBM bytes per launch measured with
 rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs and written to
 profiles/integrator_vgg16_b256_traffic.md (by python -m
@@ -100,23 +107,25 @@ def copy_calibration() -> int:
     return 0
 
 
-def cpu_baseline(w, img, gpu_pred, threads_all):
+def cpu_baseline(w, img, gpu_pred, threads_all, n1=16, nall=None):
     import oracle
+    import vdttfs
 
     c = oracle.Consts.from_task(w.consts)
+    rmode = oracle.READ_ARGMAX if w.readout == vdttfs.READOUT_ARGMAX else oracle.READ_ARGMIN
 
     def run(n, thr):
         t0 = time.perf_counter()
         r = oracle.net_forward(c, w.layers, n, img[:n], w.img_elems, oracle.ENC_LINEAR, w.tc_in,
-                               w.td_in, oracle.READ_ARGMAX, same_pad=True, nthreads=thr)
+                               w.td_in, rmode, same_pad=bool(w.consts.conv_same_pad), nthreads=thr)
         return time.perf_counter() - t0, r
 
-    # bounded sample, ~10-20 s of CPU work in all: 16 images on 1 thread and
+    # bounded sample, ~10-20 s of CPU work in all: n1 images on 1 thread and
     # the whole batch on every thread the box grants
-    n1 = min(16, len(gpu_pred))
+    n1 = min(n1, len(gpu_pred))
     run(1, 1)  # warm-up (page-in, OpenMP pool)
     dt1, r1 = run(n1, 1)
-    nall = len(gpu_pred)
+    nall = len(gpu_pred) if nall is None else min(nall, len(gpu_pred))
     dta, ra = run(nall, threads_all)
     match = bool(np.array_equal(ra["pred"], gpu_pred[:nall]) and np.array_equal(r1["pred"], gpu_pred[:n1]))
     return {
@@ -124,11 +133,199 @@ def cpu_baseline(w, img, gpu_pred, threads_all):
         "unit": "images/s",
         "cores": threads_all,
         "kind": "port",
-        "sample": f"{nall} images (the whole batch), whole network, {threads_all} OpenMP threads "
+        "sample": f"{nall} images of the batch, whole network, {threads_all} OpenMP threads "
                   f"({dta:.2f} s); 1 thread on the first {n1} images: {n1 / dt1:.3f} images/s",
         "single_thread_value": n1 / dt1,
         "pred_match_gpu": match,
     }
+
+
+def threads_all() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
+def bench_culif(args) -> int:
+    """Config 4: 7-layer CuLIF SNN on a synthetic 2x128x128 event stream."""
+    import vdttfs
+    from vdttfs import models
+
+    B = args.batch or 64
+    w = models.culif7(delta=args.delta or 32)
+    T, D = w.consts.T, w.consts.delta
+    ev = models.dvs_events(w, B)
+    ctx = vdttfs.Context(w.consts, 0)
+    net = vdttfs.CulifNet(ctx, w.layers, B)
+    d_ev = ctx.to_device(ev)
+    d_pred = ctx.empty(B, np.int32)
+    log(f"bench: {w.name} B={B} T={T} delta={D} params={w.n_params}")
+    for _ in range(args.warmup):
+        net.forward(d_ev, d_pred)
+    ctx.synchronize()
+    net.read_timing()
+    net.set_timing(True)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        net.forward(d_ev, d_pred)
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    net.set_timing(False)
+    ms_layers, _ = net.read_timing()
+    ms_layers = ms_layers / args.steps
+    gpu_pred = d_pred.download()
+    eproc, ebin, n_ev, n_cols = net.count(d_ev)
+    OS = T // D + 1
+    conv = [i for i, l in enumerate(w.layers) if l.kind == vdttfs.CULIF_CONV]
+    b_conv = 0
+    for i in conv:
+        l = w.layers[i]
+        n_out = B * l.H_in * l.W_in * l.C_out
+        # fused form: the dense input map is read by bucketize, the rest is B_int
+        b_conv += (4 * int(eproc[i]) + 8 * int(n_ev[i]) + 4 * OS * int(n_cols[i]) + 4 * l.C_out
+                   + 4 * n_out + 4 * int(n_cols[i]) * l.C_in)
+    conv_ms = float(sum(ms_layers[i] for i in conv))
+    achieved = b_conv / (conv_ms * 1e-3) / 1e9
+    l0 = w.layers[0]
+    raw_bytes = B * l0.C_in * l0.H_in * l0.W_in * T * 4 + B * l0.C_out * l0.H_in * l0.W_in * 4
+    ms_step = elapsed * 1000.0 / args.steps
+    out = {
+        "metric": f"samples/sec/GPU for CuLIF-7 DVS bs={B}; conv integrator % of HBM peak",
+        "value": B / (ms_step * 1e-3),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: moving Gaussian blob events (sigma 12 px, density 0.03), Kaiming-normal "
+                "weights (random init)",
+        "config": {"workload": "CuLIF-7 SNN, config 4 (2x128x128 events, conv 64/128/128, "
+                               "recurrent FC 131072-128, FC 128-11)",
+                   "batch": B, "T": T, "delta": D, "decay": w.meta["decay"], "th": w.meta["th"],
+                   "seed": w.seed, "parallelism": "none (one GPU)"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "conv layers (bucketize + k_merge + k_stream<CuLIF>); achieved = fused "
+                      "algorithmic bytes of the conv layers / their HIP-event time",
+            "algorithmic_bytes_per_step": b_conv,
+            "conv_ms_per_step": conv_ms,
+        },
+        "layers_ms": [round(float(x), 4) for x in ms_layers],
+        "conv1_raw_dense_GBps": raw_bytes / (float(ms_layers[0]) * 1e-3) / 1e9,
+        "eproc_per_sample": float(eproc.sum()) / B,
+        "ebin_per_sample": float(ebin.sum()) / B,
+    }
+    if not args.no_cpu:
+        import oracle
+
+        thr = threads_all()
+
+        def run(n, t):
+            t0 = time.perf_counter()
+            _, pred = oracle.culif_net_forward(w.layers, ev[:n], n, T, D, t)
+            return time.perf_counter() - t0, pred
+
+        run(1, thr)  # warm-up
+        dt1, p1 = run(1, 1)
+        nall = min(8, B)
+        dta, pa = run(nall, thr)
+        out["cpu_baseline"] = {
+            "value": nall / dta, "unit": "samples/s", "cores": thr, "kind": "port",
+            "sample": f"{nall} samples, whole network, {thr} OpenMP threads ({dta:.2f} s); "
+                      f"1 thread on 1 sample: {1.0 / dt1:.3f} samples/s",
+            "single_thread_value": 1.0 / dt1,
+            "pred_match_gpu": bool(np.array_equal(pa, gpu_pred[:nall]) and p1[0] == gpu_pred[0]),
+        }
+        out["x_cpu_all_cores"] = out["value"] / out["cpu_baseline"]["value"]
+    d_ev.free()
+    d_pred.free()
+    net.close()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_fc_sweep(args) -> int:
+    """Config 5: one FC 4096->4096 layer at B=512 over spike density, the
+    truncated window T' and delta.  Every point times one whole layer call
+    (bucketize + merge + stream) with HIP events on the library's stream."""
+    import vdttfs
+    from vdttfs import models
+
+    B = args.batch or 512
+    cin = cout = 4096
+    layer = models.fc_sweep_layer()
+    dens = (0.01, 0.05, 0.2, 0.5)
+    spikes = {d: models.fc_sweep_spikes(5, B, cin, d) for d in dens}
+    reps = max(1, min(args.steps, 10))
+    rows = []
+    for Tp in (16, 32, 64):
+        for D in (8, 16, 32):
+            tc = vdttfs.TaskConsts(T=Tp, tfs=0.0, delta=D, alpha_by_time=False)
+            ctx = vdttfs.Context(tc, 0)
+            alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+            d_W, d_b = ctx.to_device(layer.kernel), ctx.to_device(layer.bias)
+            d_a, d_t = ctx.to_device(alpha), ctx.to_device(theta)
+            d_out = ctx.empty(B * cout)
+            OS = tc.num_chunks + 1
+            for d in dens:
+                sp = spikes[d]
+                d_in = ctx.to_device(sp)
+                call = lambda cnt=False: ctx.layer_forward(d_out, d_in, d_W, d_b, d_a, d_t, 0, B, 1, 1,  # noqa: E731
+                                                           cin, 1, 1, cout, 1, 1, True, count=cnt)
+                call()
+                ctx.synchronize()
+                ctx.timer_begin()
+                for _ in range(reps):
+                    call()
+                ms = ctx.timer_end() / reps
+                eproc, ebin = call(True)
+                n_ev = int(np.count_nonzero(sp < Tp))
+                b_int = 4 * eproc + 8 * n_ev + 4 * OS * B + 4 * cout + 4 * B * cout
+                b_fused = b_int + 4 * B * cin
+                gbs = b_fused / (ms * 1e-3) / 1e9
+                rows.append({"density": d, "retained_density": n_ev / (B * cin), "T_window": Tp,
+                             "delta": D, "ms": ms, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
+                             "eproc": int(eproc), "ebin": int(ebin),
+                             "skip_rate": 1.0 - eproc / max(1, n_ev * cout),
+                             "skip_rate_per_bin": 1.0 - ebin / max(1, n_ev * cout)})
+                d_in.free()
+            for x in (d_W, d_b, d_a, d_t, d_out):
+                x.free()
+            ctx.close()
+    head = next(r for r in rows if r["density"] == 0.05 and r["T_window"] == 64 and r["delta"] == 16)
+    out = {
+        "metric": f"integrator GB/s, FC 4096x4096 bs={B} (config 5 sweep; value at density 5%, T'=64, delta=16)",
+        "value": head["achieved_GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": reps,
+        "warmup": 1,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: per (image, input) active with the given density, time uniform in "
+                "[0,64); Gaussian N(0, 2/4096) weights",
+        "config": {"workload": "FC 4096x4096 integrator sweep, config 5", "batch": B,
+                   "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "achieved": head["achieved_GBps"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": head["frac"], "traffic": None,
+                     "kernel": "one layer call = bucketize + k_merge + k_stream; fused algorithmic "
+                               "bytes B_int + 4*N_cols*C_in"},
+        "sweep": rows,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -136,8 +333,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=256)
-    ap.add_argument("--delta", type=int, default=8)
+    ap.add_argument("--workload", default="vgg16", choices=["vgg16", "lenet5", "culif7", "fc-sweep"])
+    ap.add_argument("--batch", type=int, default=None,
+                    help="default: 256 (vgg16), 1024 (lenet5), 64 (culif7), 512 (fc-sweep)")
+    ap.add_argument("--delta", type=int, default=None,
+                    help="default: 8 (vgg16), 16 (lenet5), 32 (culif7)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size copy used to scale FETCH_SIZE/WRITE_SIZE")
@@ -148,18 +348,34 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.workload == "culif7":
+        return bench_culif(args)
+    if args.workload == "fc-sweep":
+        return bench_fc_sweep(args)
+    return bench_ttfs(args)
 
+
+def bench_ttfs(args) -> int:
+    """Configs 3 (VGG-16, the headline) and 2 (LeNet-5)."""
     import vdttfs
     from vdttfs import models
 
-    B = args.batch
-    w = models.vgg16(delta=args.delta)
+    vgg = args.workload == "vgg16"
+    B = args.batch or (256 if vgg else 1024)
+    if vgg:
+        w = models.vgg16(delta=args.delta or 8)
+        metric = METRIC
+        workload = "VGG-16 TTFS-SNN, config 3 (3x32x32, 13 conv + FC 512-512-10)"
+    else:
+        w = models.lenet5(delta=args.delta or 16)
+        metric = f"images/sec/GPU for LeNet-5 TTFS bs={B}; integrator % of HBM peak"
+        workload = "LeNet-5 TTFS-SNN, config 2 (1x28x28, conv 6/16 + FC 256-120-84-10)"
     img = models.images_for(w, B)
     ctx = vdttfs.Context(w.consts, 0)
     net = vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
     d_img = ctx.to_device(img)
     d_pred = ctx.empty(B, np.int32)
-    log(f"bench: VGG-16 TTFS B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
+    log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
         f"params={w.n_params}")
 
     for _ in range(args.warmup):
@@ -184,7 +400,7 @@ def main() -> int:
     integ_ms_step = integ_ms / args.steps
     launches_per_step = integ_n / args.steps
     achieved = b_int / (integ_ms_step * 1e-3) / 1e9
-    key = workload_key(B, w.consts)
+    key = workload_key(B, w.consts) if vgg else f"{w.name} B={B} T={w.consts.T} delta={w.consts.delta}"
     tr = measured_traffic(key)
     dense = 0
     for l in w.layers:
@@ -193,7 +409,7 @@ def main() -> int:
         elif l.kind == 1:
             dense += B * l.C_out * l.H_in * l.W_in * l.C_in
     out = {
-        "metric": METRIC,
+        "metric": metric,
         "value": B / (ms_step * 1e-3),
         "unit": "images/s",
         "n_gpus": 1,
@@ -205,7 +421,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded splitmix64 U[0,1) images, Kaiming-normal weights (random init)",
-        "config": {"workload": "VGG-16 TTFS-SNN, config 3 (3x32x32, 13 conv + FC 512-512-10)",
+        "config": {"workload": workload,
                    "key": key,
                    "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
                    "seed": w.seed, "parallelism": "none (one GPU)"},
@@ -216,8 +432,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": (tr[0] / tr[1]) if tr else None,
-            "kernel": "integrator = k_merge + k_stream per integrating layer; a launch is one layer's "
-                      "pair, achieved = algorithmic bytes of a step / integrator time of a step",
+            "kernel": "integrator = k_merge + k_stream per integrating layer (k_integrate_generic "
+                      "for layers under 32 outputs); a launch is one layer's integrate, achieved = "
+                      "algorithmic bytes of a step / integrator time of a step",
             "algorithmic_bytes_per_step": b_int,
             "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
             "traffic_per_step": tr[0] if tr else None,
@@ -233,7 +450,7 @@ def main() -> int:
     }
     if not args.no_cpu:
         thr = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-        cb = cpu_baseline(w, img, gpu_pred, thr)
+        cb = cpu_baseline(w, img, gpu_pred, thr, n1=16 if vgg else 256)
         out["cpu_baseline"] = cb
         out["x_cpu_all_cores"] = out["value"] / cb["value"]
     net.close()

@@ -68,6 +68,12 @@ int vdttfs_get_consts(const vdttfs_ctx* ctx, vdttfs_consts* out);
 /* NC = ceil(T/delta) and OFF_STRIDE = NC+1 (T1V:18-19, T2V:17-18). */
 int vdttfs_num_chunks(const vdttfs_ctx* ctx);
 int vdttfs_synchronize(vdttfs_ctx* ctx);
+/* HIP-event timer on the context's stream (no reference counterpart; the
+ * reference times its batch with cudaEventRecord around main()'s layer
+ * loop, T2V:339-388).  begin records a start event; end records a stop
+ * event, waits for it and returns the milliseconds in between. */
+int vdttfs_timer_begin(vdttfs_ctx* ctx);
+int vdttfs_timer_end(vdttfs_ctx* ctx, double* ms);
 int vdttfs_device_count(int* out);
 
 /* ---- device memory plumbing (cudaMalloc/cudaMemcpy in the reference) -- */
@@ -301,6 +307,18 @@ int vdttfs_culif_net_forward(vdttfs_culif_net* net, const float* d_data, int32_t
  * (engine conv / pool layers), 0 when NCHW or FC [B][C]. */
 int vdttfs_culif_net_layer_output(vdttfs_culif_net* net, int layer, const float** d_out,
                                   int64_t* elems, int32_t* nhwc);
+/* Per-layer event timing: when enabled, forward() brackets every layer with
+ * HIP events on the context stream; read_timing synchronises and writes the
+ * summed milliseconds per layer (ms[n_layers]) and the number of timed
+ * forwards since the last read. */
+int vdttfs_culif_net_set_timing(vdttfs_culif_net* net, int enable);
+int vdttfs_culif_net_read_timing(vdttfs_culif_net* net, double* ms, int64_t* forwards);
+/* One instrumented forward (T3M-style counts): for every CONV layer the
+ * integrated-synapse count under the reference's chunk-granular early exit
+ * (eproc) and under the per-bin exit executed (ebin), the retained input
+ * events (n_ev) and bucket columns (n_cols); 0 for other layers. */
+int vdttfs_culif_net_count(vdttfs_culif_net* net, const float* d_data, uint64_t* eproc,
+                           uint64_t* ebin, uint64_t* n_ev, uint64_t* n_cols);
 
 /* ---- synthetic workloads (counter-mode splitmix64; host) --------------- */
 /* u = (z>>40) * 2^-24 with z = mix(seed + 0x9E3779B97F4A7C15*(stream*2^40+i+1)). */

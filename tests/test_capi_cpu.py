@@ -48,7 +48,7 @@ def test_no_gpu_create_fails_cleanly():
 def test_bad_consts_rejected():
     L = vdttfs.lib()
     for bad in (_lib.Consts(0, 0, 1, 1, 0, 0), _lib.Consts(64, 0, 0, 1, 0, 0),
-                _lib.Consts(64, 0, 65, 1, 0, 0), _lib.Consts(300, 0, 8, 1, 0, 0)):
+                _lib.Consts(64, 0, 257, 1, 0, 0), _lib.Consts(300, 0, 8, 1, 0, 0)):
         a = np.empty(400, np.float32)
         rc = L.vdttfs_build_luts_host(C.byref(bad), 16, 0, 16, 0, C.c_void_p(a.ctypes.data),
                                       C.c_void_p(a.ctypes.data))

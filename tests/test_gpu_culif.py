@@ -27,12 +27,16 @@ def spike_map(rng, n, T, p=0.5):
     return s
 
 
-@pytest.mark.parametrize("T,delta,C_out", [(64, 32, 70), (48, 16, 64), (32, 32, 5)])
-def test_conv1_raw(gpu_ctx_factory, T, delta, C_out):
-    say(f"culif conv1_raw T={T} delta={delta} C_out={C_out}")
+# C_in <= 4 runs the LDS-tiled kernel (16-pixel row tiles, ragged here);
+# larger C_in the per-pixel scalar-load kernel
+@pytest.mark.parametrize("T,delta,C_out,C_in,W", [(64, 32, 70, 2, 37), (48, 16, 64, 2, 7),
+                                                  (32, 32, 5, 1, 16), (64, 32, 64, 5, 11),
+                                                  (80, 16, 33, 6, 5)])
+def test_conv1_raw(gpu_ctx_factory, T, delta, C_out, C_in, W):
+    say(f"culif conv1_raw T={T} delta={delta} C_out={C_out} C_in={C_in} W={W}")
     ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
     rng = np.random.default_rng(31)
-    N, C_in, H, W = 2, 2, 9, 7
+    N, H = 2, 9
     data = (rng.random((N, C_in, H, W, T)) < 0.05).astype(np.float32)
     w = (rng.standard_normal((C_out, C_in, 3, 3)) * 0.6).astype(np.float32)
     exp = oracle.culif_conv1_raw(data, w, N, C_in, C_out, H, W, T, delta, 0.5, 1.0)

@@ -116,7 +116,7 @@ def test_fc_sweep_config5(gpu_ctx_factory, density):
     sp = models.fc_sweep_spikes(5, B, cin, density)
     for Tp in (16, 64):
         outs = []
-        for delta in (8, 16):
+        for delta in (8, 16, 32):  # delta > T' is one chunk cut at T' (T1V:152-153)
             tc = vdttfs.TaskConsts(T=Tp, tfs=0.0, delta=delta, alpha_by_time=False)
             ctx = gpu_ctx_factory(tc)
             alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
@@ -129,6 +129,7 @@ def test_fc_sweep_config5(gpu_ctx_factory, density):
             for d in (d_out, d_in, d_W, d_b, d_a, d_t):
                 d.free()
         np.testing.assert_array_equal(outs[0], outs[1])
+        np.testing.assert_array_equal(outs[0], outs[2])
         c = oracle.Consts(Tp, 0.0, 8, False)
         nb = 64
         cin_, tin_, off_ = oracle.bucketize(c, sp[:nb], nb, cin)

@@ -101,8 +101,10 @@ static int check_consts(const vdttfs_consts* c) {
     if (!c) return set_error(VDTTFS_E_INVALID, "null constants");
     if (c->T < 1 || c->T > 255)
         return set_error(VDTTFS_E_INVALID, "TIME_WINDOW %d outside [1,255]", c->T);
-    if (c->delta < 1 || c->delta > c->T)
-        return set_error(VDTTFS_E_INVALID, "CHUNK %d outside [1,T=%d]", c->delta, c->T);
+    // CHUNK may exceed TIME_WINDOW: the chunk loop's t < T guard then ends
+    // the single chunk early (T1V:151-153)
+    if (c->delta < 1 || c->delta > 256)
+        return set_error(VDTTFS_E_INVALID, "CHUNK %d outside [1,256]", c->delta);
     if (!std::isfinite(c->tfs) || !std::isfinite(c->vth))
         return set_error(VDTTFS_E_INVALID, "TIME_FIRE_START / VTH_INIT must be finite");
     return VDTTFS_OK;
@@ -161,8 +163,37 @@ int vdttfs_destroy(vdttfs_ctx* ctx) {
                     ctx->bin_off, ctx->mrg_list, ctx->mrg_bstart, ctx->d_counters};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    if (ctx->timer_ready) {
+        (void)hipEventDestroy(ctx->timer[0]);
+        (void)hipEventDestroy(ctx->timer[1]);
+    }
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
+    return VDTTFS_OK;
+}
+
+int vdttfs_timer_begin(vdttfs_ctx* ctx) {
+    VD_TRY(check_ctx(ctx));
+    if (!ctx->timer_ready) {
+        VD_HIP(hipEventCreate(&ctx->timer[0]));
+        if (hipEventCreate(&ctx->timer[1]) != hipSuccess) {
+            (void)hipEventDestroy(ctx->timer[0]);
+            return set_error(VDTTFS_E_HIP, "timer: event creation failed");
+        }
+        ctx->timer_ready = true;
+    }
+    VD_HIP(hipEventRecord(ctx->timer[0], ctx->stream));
+    return VDTTFS_OK;
+}
+
+int vdttfs_timer_end(vdttfs_ctx* ctx, double* ms) {
+    VD_TRY(check_ctx(ctx));
+    if (!ctx->timer_ready || !ms) return set_error(VDTTFS_E_INVALID, "timer_end without timer_begin");
+    VD_HIP(hipEventRecord(ctx->timer[1], ctx->stream));
+    VD_HIP(hipEventSynchronize(ctx->timer[1]));
+    float f = 0.0f;
+    VD_HIP(hipEventElapsedTime(&f, ctx->timer[0], ctx->timer[1]));
+    *ms = f;
     return VDTTFS_OK;
 }
 

@@ -36,6 +36,8 @@ struct vdttfs_ctx {
     void* mrg_bstart;
     size_t mrg_list_elems, mrg_bstart_elems;
     unsigned long long* d_counters;  // 4 x u64
+    hipEvent_t timer[2];             // vdttfs_timer_begin/end (created on first use)
+    bool timer_ready;
 };
 
 namespace vdttfs {
@@ -117,13 +119,14 @@ int launch_culif_pool(vdttfs_ctx* ctx, const float* in, float* out, int N, int C
                       int nhwc_in, int nhwc_out, float decay, float th);
 // Drop-in (cur == NULL): reference buckets, W [out][in], Wrec [i][j].
 // Engine (cur != NULL): feed-forward input per step cur[N][T][out_f] from
-// launch_bin_currents, Wrec transposed to [j][i]; cin/tin/off/W unused.
+// launch_fc_currents, Wrec transposed to [j][i]; cin/tin/off/W unused.
 int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, const int32_t* off,
                         const float* cur, float* out, const float* W, const float* Wrec, int N,
                         int in_f, int out_f, float decay, float th);
-// cur[n][t][o] = sum over bin t's events (ascending input j) of W_t[j][o].
-int launch_bin_currents(vdttfs_ctx* ctx, const vd_event* ev, const int32_t* off, const float* W_t,
-                        float* cur, int N, int in_f, int out_f);
+// cur[n][t][o] = sum over inputs j ascending arriving at step t of W_t[j][o],
+// from the dense input x[N][F] (T3V arrival rule).
+int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F,
+                       int out_f);
 int launch_nhwc_to_nchw(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H, int W);
 
 // shape validation shared by the entry points

@@ -9,8 +9,9 @@
 // reference's NCHW order, because the order of the per-step sums follows
 // the input index.  Conv layers run bucketize -> merge -> stream with the
 // CuLIF neuron and alpha = 1 (fma(w, 1, acc) is the reference's acc + w).
-// The recurrent FC layer's feed-forward sums are computed per (sample, bin)
-// in parallel (k_bin_currents) before the per-step recurrence.
+// The recurrent FC layer's feed-forward sums are computed per (sample, step)
+// in parallel from its dense input (k_fc_currents) before the per-step
+// recurrence.
 #include <cstring>
 #include <new>
 #include <vector>
@@ -62,13 +63,22 @@ struct vdttfs_culif_net {
     int32_t* roff = nullptr;
     float* flat = nullptr;     // NCHW flatten of a spatial map before an FC
     float* cur = nullptr;      // FC_REC feed-forward currents [B][T][out]
+    bool timing = false;
+    std::vector<hipEvent_t> pool;      // 2 per layer per timed forward
+    size_t pool_used = 0;
+    std::vector<int> pending_layer;    // layer of each recorded pair
+    int64_t forwards = 0;
 };
 
 namespace {
 
 void destroy_impl(vdttfs_culif_net* net) {
     if (!net) return;
-    if (net->ctx) (void)hipSetDevice(net->ctx->device);
+    if (net->ctx) {
+        (void)hipSetDevice(net->ctx->device);
+        (void)hipStreamSynchronize(net->ctx->stream);
+    }
+    for (hipEvent_t e : net->pool) (void)hipEventDestroy(e);
     for (CLayer& l : net->L)
         for (float* q : {l.W, l.Wrec, l.out})
             if (q) (void)hipFree(q);
@@ -112,8 +122,6 @@ int validate(const vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n) {
         }
         if (d.kind == VDTTFS_CULIF_FC_REC && (!d.weight_rec || d.C_out > 1024))
             return set_error(VDTTFS_E_INVALID, "culif net: FC_REC layer %d needs weight_rec and <= 1024 outputs", i);
-        if (d.kind == VDTTFS_CULIF_FC_REC && d.C_in >= (1 << 24))
-            return set_error(VDTTFS_E_UNSUPPORTED, "culif net: FC_REC layer %d has >= 2^24 inputs", i);
         if (d.kind == VDTTFS_CULIF_CONV && (d.C_out < 32 || d.C_in >= (1 << 24)))
             return set_error(VDTTFS_E_UNSUPPORTED, "culif net: conv layer %d needs C_out >= 32", i);
         if (fc) {
@@ -193,8 +201,6 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
                         r[(size_t)b * d.C_out + a] = d.weight_rec[(size_t)a * d.C_out + b];
                 VD_TRY(upload(&l.W, w));
                 VD_TRY(upload(&l.Wrec, r));
-                if ((int64_t)B * d.C_in > max_ev) max_ev = (int64_t)B * d.C_in;
-                if (B > max_cols) max_cols = B;
                 if ((int64_t)B * T * d.C_out > max_cur) max_cur = (int64_t)B * T * d.C_out;
                 if (spatial_in && (int64_t)B * d.C_in > max_flat) max_flat = (int64_t)B * d.C_in;
                 break;
@@ -224,15 +230,36 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
     return VDTTFS_OK;
 }
 
-int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred) {
+int mark(vdttfs_culif_net* net, hipEvent_t* e) {
+    if (net->pool_used == net->pool.size()) {
+        hipEvent_t ev;
+        VD_HIP(hipEventCreate(&ev));
+        net->pool.push_back(ev);
+    }
+    *e = net->pool[net->pool_used++];
+    VD_HIP(hipEventRecord(*e, net->ctx->stream));
+    return VDTTFS_OK;
+}
+
+// counts: nullable [4][n_layers] (eproc, ebin, n_ev, n_cols) for an
+// instrumented forward; counting and timing are exclusive.
+int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, uint64_t* const* counts) {
     vdttfs_ctx* ctx = net->ctx;
     const int B = net->B;
     const float* cur = nullptr;
     int cur_nhwc = 0, cH = 1, cW = 1, cC = 0;
+    const bool timed = net->timing && !counts;
     for (size_t i = 0; i < net->L.size(); ++i) {
         CLayer& l = net->L[i];
         const vdttfs_culif_layer& d = l.d;
         CulifNeuron nrn{d.decay, d.th};
+        hipEvent_t e0 = nullptr, e1 = nullptr;  // consecutive pool slots 2k, 2k+1
+        if (timed) VD_TRY(mark(net, &e0));
+        const bool count_here = counts && d.kind == VDTTFS_CULIF_CONV;
+        if (counts)
+            for (int k = 0; k < 4; ++k) counts[k][i] = 0;
+        if (count_here)
+            VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
         // an FC layer reads the previous map flattened in NCHW order
         const float* fc_in = cur;
         if ((d.kind == VDTTFS_CULIF_FC || d.kind == VDTTFS_CULIF_FC_REC) && cur_nhwc && (cH > 1 || cW > 1)) {
@@ -246,10 +273,21 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred) {
                 break;
             case VDTTFS_CULIF_CONV: {
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;
-                VD_TRY(launch_bucketize_bins(ctx, cur, cols, d.C_in, net->ones, net->ev, net->off, nullptr));
+                VD_TRY(launch_bucketize_bins(ctx, cur, cols, d.C_in, net->ones, net->ev, net->off,
+                                             count_here ? ctx->d_counters + 2 : nullptr));
                 IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3, 1, 0};
                 VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
-                                             net->bstart, l.W, nullptr, nullptr, 0, sh, nullptr, &nrn));
+                                             net->bstart, l.W, nullptr, nullptr, 0, sh,
+                                             count_here ? ctx->d_counters : nullptr, &nrn));
+                if (count_here) {
+                    unsigned long long h[4];
+                    VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
+                    VD_HIP(hipStreamSynchronize(ctx->stream));
+                    counts[0][i] = h[0];
+                    counts[1][i] = h[1];
+                    counts[2][i] = h[2];
+                    counts[3][i] = (uint64_t)cols;
+                }
                 break;
             }
             case VDTTFS_CULIF_POOL:
@@ -257,8 +295,7 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred) {
                                          d.th));
                 break;
             case VDTTFS_CULIF_FC_REC:
-                VD_TRY(launch_bucketize_bins(ctx, fc_in, B, d.C_in, net->ones, net->ev, net->off, nullptr));
-                VD_TRY(launch_bin_currents(ctx, net->ev, net->off, l.W, net->cur, B, d.C_in, d.C_out));
+                VD_TRY(launch_fc_currents(ctx, fc_in, l.W, net->cur, B, d.C_in, d.C_out));
                 VD_TRY(launch_culif_fc_rec(ctx, nullptr, nullptr, nullptr, net->cur, l.out, nullptr, l.Wrec, B,
                                            d.C_in, d.C_out, d.decay, d.th));
                 break;
@@ -267,6 +304,10 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred) {
                 VD_TRY(launch_culif_generic(ctx, net->rcin, net->rtin, net->roff, l.out, l.W, B, d.C_in,
                                             d.C_out, 1, 1, 1, d.decay, d.th));
                 break;
+        }
+        if (timed) {
+            VD_TRY(mark(net, &e1));
+            net->pending_layer.push_back((int)i);
         }
         cur = l.out;
         cur_nhwc = l.nhwc;
@@ -386,7 +427,52 @@ int vdttfs_culif_net_destroy(vdttfs_culif_net* net) {
 int vdttfs_culif_net_forward(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred) {
     if (!net || !d_data) return set_error(VDTTFS_E_INVALID, "culif_net_forward: null argument");
     VD_TRY(check_ctx(net->ctx));
-    return forward_impl(net, d_data, d_pred);
+    VD_TRY(forward_impl(net, d_data, d_pred, nullptr));
+    if (net->timing) net->forwards += 1;
+    return VDTTFS_OK;
+}
+
+int vdttfs_culif_net_set_timing(vdttfs_culif_net* net, int enable) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    net->timing = enable != 0;
+    return VDTTFS_OK;
+}
+
+int vdttfs_culif_net_read_timing(vdttfs_culif_net* net, double* ms, int64_t* forwards) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    VD_TRY(check_ctx(net->ctx));
+    VD_HIP(hipStreamSynchronize(net->ctx->stream));
+    std::vector<double> acc(net->L.size(), 0.0);
+    for (size_t k = 0; k < net->pending_layer.size(); ++k) {
+        float f = 0.0f;
+        VD_HIP(hipEventElapsedTime(&f, net->pool[2 * k], net->pool[2 * k + 1]));
+        acc[net->pending_layer[k]] += f;
+    }
+    if (ms)
+        for (size_t i = 0; i < acc.size(); ++i) ms[i] = acc[i];
+    if (forwards) *forwards = net->forwards;
+    net->pending_layer.clear();
+    net->pool_used = 0;
+    net->forwards = 0;
+    return VDTTFS_OK;
+}
+
+int vdttfs_culif_net_count(vdttfs_culif_net* net, const float* d_data, uint64_t* eproc, uint64_t* ebin,
+                           uint64_t* n_ev, uint64_t* n_cols) {
+    if (!net || !d_data) return set_error(VDTTFS_E_INVALID, "culif_net_count: null argument");
+    VD_TRY(check_ctx(net->ctx));
+    const size_t n = net->L.size();
+    std::vector<uint64_t> a(n), b(n), c(n), d(n);
+    uint64_t* counts[4] = {a.data(), b.data(), c.data(), d.data()};
+    VD_TRY(forward_impl(net, d_data, nullptr, counts));
+    VD_HIP(hipStreamSynchronize(net->ctx->stream));
+    for (size_t i = 0; i < n; ++i) {
+        if (eproc) eproc[i] = a[i];
+        if (ebin) ebin[i] = b[i];
+        if (n_ev) n_ev[i] = c[i];
+        if (n_cols) n_cols[i] = d[i];
+    }
+    return VDTTFS_OK;
 }
 
 int vdttfs_culif_net_layer_output(vdttfs_culif_net* net, int layer, const float** d_out, int64_t* elems,

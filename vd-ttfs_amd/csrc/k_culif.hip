@@ -18,6 +18,8 @@
 //  k_culif_pool        pool_chunk_early (T3V:146-168), layouts by strides.
 //  k_culif_fc_rec      fc1_bucketed_recurrent (T3V:171-200): one block per
 //                      sample; fired-last-step neurons as a bitmask in LDS.
+//  k_fc_currents       the engine's per-step feed-forward input of that layer,
+//                      computed per (sample, step group) from the dense input.
 //  k_nhwc_to_nchw      flattening order for an FC layer after a spatial map.
 #include "common.h"
 #include "wave.h"
@@ -101,6 +103,106 @@ __global__ __launch_bounds__(256) void k_culif_conv1_raw(RawArgs a) {
         if (__ballot(alive) == 0) break;
     }
     if (ok) a.out[n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+}
+
+// Tiled variant for few input channels (C_in <= kTileMaxCin): a block of 4
+// waves owns kTileX consecutive output pixels of one row and one 64-wide
+// c_out block.  Per 32-step chunk the block stages the 3 x (kTileX + 2)
+// input neighbourhood (C_in channels, 32 steps each: coalesced 128-byte
+// segments) in LDS; each wave then integrates its pixels with the time
+// vectors read as LDS broadcasts.  The per-step fma order is conv1_raw's
+// (c_in, ky, kx), out-of-bounds taps skipped.  The block stops once no lane
+// of any pixel is alive.
+constexpr int kTileX = 16;
+constexpr int kTileMaxCin = 4;
+constexpr int kTilePix = kTileX / 4;  // pixels per wave
+
+__global__ __launch_bounds__(256) void k_culif_conv1_tile(RawArgs a) {
+    __shared__ float4 tile4[kTileMaxCin * 3 * (kTileX + 2) * (kRawChunk / 4)];
+    float* tile = reinterpret_cast<float*>(tile4);
+    const int wave = uniform(threadIdx.x >> 6);
+    const int n_xt = (a.Wd + kTileX - 1) / kTileX;
+    int64_t b = blockIdx.x;
+    const int cb = (int)(b % a.n_cblk);
+    b /= a.n_cblk;
+    const int xt = (int)(b % n_xt);
+    b /= n_xt;
+    const int y = (int)(b % a.H);
+    const int64_t n = b / a.H;
+    const int x0 = xt * kTileX;
+    const int c = cb * 64 + lane_id();
+    const bool ok = c < a.C_out;
+    const int segs = a.C_in * 3 * (kTileX + 2);  // (ci, r, cx) time vectors
+    float I[kTilePix], V[kTilePix], res[kTilePix];
+    bool alive[kTilePix];
+#pragma unroll
+    for (int q = 0; q < kTilePix; ++q) {
+        const int x = x0 + wave + 4 * q;
+        I[q] = 0.0f;
+        V[q] = 0.0f;
+        res[q] = kInfTime;
+        alive[q] = ok && x < a.Wd;
+    }
+    for (int t0 = 0; t0 < a.T; t0 += kRawChunk) {
+        __syncthreads();  // previous chunk's readers are done
+        for (int idx = threadIdx.x; idx < segs * kRawChunk; idx += blockDim.x) {
+            const int t = idx % kRawChunk, sg = idx / kRawChunk;
+            const int cx = sg % (kTileX + 2), r = (sg / (kTileX + 2)) % 3, ci = sg / (3 * (kTileX + 2));
+            const int iy = y + r - 1, ix = x0 + cx - 1;
+            float v = 0.0f;
+            if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd && t0 + t < a.T)
+                v = a.data[(((n * a.C_in + ci) * a.H + iy) * a.Wd + ix) * (int64_t)a.T + t0 + t];
+            tile[idx] = v;
+        }
+        __syncthreads();
+        bool any = false;
+#pragma unroll
+        for (int q = 0; q < kTilePix; ++q) {
+            const int x = x0 + wave + 4 * q;
+            if (x >= a.Wd || __ballot(alive[q]) == 0) continue;  // uniform per wave
+            float in[kRawChunk];
+#pragma unroll
+            for (int t = 0; t < kRawChunk; ++t) in[t] = 0.0f;
+            for (int ci = 0; ci < a.C_in; ++ci)
+                for (int ky = 0; ky < 3; ++ky) {
+                    const int iy = y + ky - 1;
+                    if (iy < 0 || iy >= a.H) continue;
+                    for (int kx = 0; kx < 3; ++kx) {
+                        const int ix = x + kx - 1;
+                        if (ix < 0 || ix >= a.Wd) continue;
+                        const float w = ok ? a.W[(((int64_t)c * a.C_in + ci) * 3 + ky) * 3 + kx] : 0.0f;
+                        const float4* v4 = tile4 + ((ci * 3 + ky) * (kTileX + 2) + (ix - x0 + 1)) * (kRawChunk / 4);
+#pragma unroll
+                        for (int t4 = 0; t4 < kRawChunk / 4; ++t4) {
+                            const float4 v = v4[t4];
+                            in[4 * t4 + 0] = __builtin_fmaf(w, v.x, in[4 * t4 + 0]);
+                            in[4 * t4 + 1] = __builtin_fmaf(w, v.y, in[4 * t4 + 1]);
+                            in[4 * t4 + 2] = __builtin_fmaf(w, v.z, in[4 * t4 + 2]);
+                            in[4 * t4 + 3] = __builtin_fmaf(w, v.w, in[4 * t4 + 3]);
+                        }
+                    }
+                }
+#pragma unroll
+            for (int t = 0; t < kRawChunk; ++t) {
+                if (t0 + t < a.T) {
+                    I[q] = __builtin_fmaf(I[q], a.decay, in[t]);
+                    V[q] = V[q] + I[q];
+                    if (alive[q] && V[q] >= a.th) {
+                        res[q] = (float)(t0 + t);
+                        alive[q] = false;
+                    }
+                }
+            }
+            any = any || alive[q];
+        }
+        if (!__syncthreads_or(any)) break;
+    }
+#pragma unroll
+    for (int q = 0; q < kTilePix; ++q) {
+        const int x = x0 + wave + 4 * q;
+        if (ok && x < a.Wd)
+            a.out[n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res[q];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -375,40 +477,62 @@ __global__ __launch_bounds__(1024) void k_culif_fc_rec(CRecArgs a) {
     if (ok) a.out[(int64_t)n * a.out_f + i] = my_fire;
 }
 
-// Engine feed-forward currents of an FC layer: one wave per (sample, arrival
-// bin, 64 outputs); lanes are outputs.  cur[n][t][o] = sum over the bin's
-// events, in ascending input index, of W[j][o] (the weights transposed to
-// [in][out], so each event is one coalesced row segment).  Bins are
-// independent, so the T bins of a sample run in parallel while each bin's
-// sum keeps the reference's order.
-__global__ __launch_bounds__(256) void k_bin_currents(const vd_event* __restrict__ ev,
-                                                      const int32_t* __restrict__ off,
-                                                      const float* __restrict__ W,
-                                                      float* __restrict__ cur, int N, int T,
-                                                      int in_f, int out_f, int n_oblk) {
+// Engine feed-forward currents of an FC layer, straight from the dense input
+// x[N][F] (no bucketize): one wave per (sample, kFcBins arrival steps, 64
+// outputs); lanes are outputs.  The wave scans the sample's inputs in
+// ascending j, 64 at a time, ballots the inputs arriving at each of its
+// steps (T3V:78 rule) and adds their weight rows in that order, so
+//   cur[n][t][o] = sum over j ascending with step(x[n][j]) == t of W_t[j][o]
+// is summed exactly as the reference's bucket order sums it (W_t is the
+// [in][out] transpose: each term is one coalesced row segment).
+constexpr int kFcBins = 4;
+
+__global__ __launch_bounds__(256) void k_fc_currents(const float* __restrict__ x,
+                                                     const float* __restrict__ W,
+                                                     float* __restrict__ cur, int N, int T, int F,
+                                                     int out_f, int n_oblk, int n_tgrp) {
     const int wave = uniform(threadIdx.x >> 6);
-    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t, oblk)
-    if (u >= (int64_t)N * T * n_oblk) return;
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t group, oblk)
+    if (u >= (int64_t)N * n_tgrp * n_oblk) return;
     const int ob = (int)(u % n_oblk);
-    const int t = (int)((u / n_oblk) % T);
-    const int64_t n = u / ((int64_t)n_oblk * T);
-    const int o = ob * 64 + lane_id();
+    const int t0 = (int)((u / n_oblk) % n_tgrp) * kFcBins;
+    const int64_t n = u / ((int64_t)n_oblk * n_tgrp);
+    const int lane = lane_id();
+    const int o = ob * 64 + lane;
     const bool ok = o < out_f;
     const int oo = ok ? o : 0;
-    const int32_t* BO = off + n * (T + 1);
-    const int s = BO[t], e = BO[t + 1];
-    const vd_event* E = ev + n * (int64_t)in_f;
-    float acc = 0.0f;
-    int p = s;
-    for (; p + 8 <= e; p += 8) {
-        float w[8];
+    const float* __restrict__ X = x + n * (int64_t)F;
+    float acc[kFcBins];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) w[g] = W[(int64_t)(E[p + g].key & 0xFFFFFFu) * out_f + oo];
+    for (int k = 0; k < kFcBins; ++k) acc[k] = 0.0f;
+    for (int base = 0; base < F; base += 64) {
+        const int j = base + lane;
+        const int st = culif_bin(j < F ? X[j] : kInfTime, T);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) acc = acc + w[g];
+        for (int k = 0; k < kFcBins; ++k) {
+            uint64_t m = __ballot(st == t0 + k);
+            while (m) {
+                // up to 8 gathers in flight, added in ascending j
+                int js[8];
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    js[g] = m ? base + (int)__builtin_ctzll(m) : -1;
+                    m &= m - 1;
+                }
+                float w[8];
+#pragma unroll
+                for (int g = 0; g < 8; ++g) w[g] = js[g] >= 0 ? W[(int64_t)js[g] * out_f + oo] : 0.0f;
+#pragma unroll
+                for (int g = 0; g < 8; ++g)
+                    if (js[g] >= 0) acc[k] = acc[k] + w[g];
+            }
+        }
     }
-    for (; p < e; ++p) acc = acc + W[(int64_t)(E[p].key & 0xFFFFFFu) * out_f + oo];
-    if (ok) cur[(n * T + t) * out_f + o] = acc;
+    if (ok) {
+#pragma unroll
+        for (int k = 0; k < kFcBins; ++k)
+            if (t0 + k < T) cur[(n * T + t0 + k) * out_f + o] = acc[k];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -469,6 +593,13 @@ int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const
     }
     a.decay = decay;
     a.th = th;
+    if (C_in <= kTileMaxCin) {
+        const int64_t blocks = (int64_t)N * H * ((Wd + kTileX - 1) / kTileX) * a.n_cblk;
+        if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_raw: grid too large");
+        hipLaunchKernelGGL(k_culif_conv1_tile, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+        VD_HIP(hipGetLastError());
+        return VDTTFS_OK;
+    }
     const int64_t blocks = ((a.n_pix + 3) / 4) * a.n_cblk;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_raw: grid too large");
     hipLaunchKernelGGL(k_culif_conv1_raw, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
@@ -593,16 +724,16 @@ int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, c
     return VDTTFS_OK;
 }
 
-int launch_bin_currents(vdttfs_ctx* ctx, const vd_event* ev, const int32_t* off, const float* W_t,
-                        float* cur, int N, int in_f, int out_f) {
-    if (in_f >= (1 << 24)) return set_error(VDTTFS_E_UNSUPPORTED, "bin currents: in_f >= 2^24");
+int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F,
+                       int out_f) {
     const int T = ctx->c.T;
     const int n_oblk = (out_f + 63) / 64;
-    const int64_t waves = (int64_t)N * T * n_oblk;
+    const int n_tgrp = (T + kFcBins - 1) / kFcBins;
+    const int64_t waves = (int64_t)N * n_tgrp * n_oblk;
     const int64_t blocks = (waves + 3) / 4;
-    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "bin currents: grid too large");
-    hipLaunchKernelGGL(k_bin_currents, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, ev, off, W_t,
-                       cur, N, T, in_f, out_f, n_oblk);
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "fc currents: grid too large");
+    hipLaunchKernelGGL(k_fc_currents, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, x, W_t, cur, N,
+                       T, F, out_f, n_oblk, n_tgrp);
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }

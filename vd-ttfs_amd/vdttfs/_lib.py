@@ -183,6 +183,11 @@ SIGNATURES = {
     "vdttfs_culif_net_forward": [_vp, _vp, _vp],
     "vdttfs_culif_net_layer_output": [_vp, _i, C.POINTER(_vp), C.POINTER(_i64),
                                       C.POINTER(C.c_int32)],
+    "vdttfs_culif_net_set_timing": [_vp, _i],
+    "vdttfs_culif_net_read_timing": [_vp, C.POINTER(C.c_double), C.POINTER(_i64)],
+    "vdttfs_culif_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
+    "vdttfs_timer_begin": [_vp],
+    "vdttfs_timer_end": [_vp, C.POINTER(C.c_double)],
 }
 
 _RESTYPES = {"vdttfs_last_error": C.c_char_p, "vdttfs_version": C.c_char_p}

@@ -146,6 +146,16 @@ class Context:
         h = np.ascontiguousarray(host, dtype=dtype or host.dtype)
         return DeviceArray(self, h.shape, h.dtype).upload(h)
 
+    def timer_begin(self):
+        """Record a HIP event on the context stream (see timer_end)."""
+        check(lib().vdttfs_timer_begin(self.handle))
+
+    def timer_end(self) -> float:
+        """Milliseconds on the context stream since timer_begin (HIP events)."""
+        ms = C.c_double()
+        check(lib().vdttfs_timer_end(self.handle, C.byref(ms)))
+        return ms.value
+
     def synchronize(self):
         check(lib().vdttfs_synchronize(self.handle))
 
@@ -389,3 +399,21 @@ class CulifNet:
         if nhwc.value:
             h = h.reshape(self.B, H, W, Cc).transpose(0, 3, 1, 2)
         return np.ascontiguousarray(h.reshape(self.B, Cc, H, W)) if layout == "nchw" else h
+
+    def set_timing(self, on: bool):
+        check(lib().vdttfs_culif_net_set_timing(self.handle, int(on)))
+
+    def read_timing(self):
+        """(per-layer milliseconds summed over the timed forwards, forwards)."""
+        n = len(self.layers)
+        ms = (C.c_double * n)()
+        fw = C.c_int64()
+        check(lib().vdttfs_culif_net_read_timing(self.handle, ms, C.byref(fw)))
+        return np.array(list(ms)), fw.value
+
+    def count(self, d_data: DeviceArray):
+        """Per layer (eproc, ebin, n_ev, n_cols); nonzero for conv layers."""
+        n = len(self.layers)
+        arrs = [(C.c_uint64 * n)() for _ in range(4)]
+        check(lib().vdttfs_culif_net_count(self.handle, d_data.ptr, *arrs))
+        return [np.array(list(a), dtype=np.uint64) for a in arrs]
