@@ -95,6 +95,13 @@ LAYER_CASES = [
     ("t2-fc-512-512", 64, 32.0, 8, True, True, 20, 1, 1, 512, 512, 1),
     ("t1-fc-4096-96-delta32", 32, 0.0, 32, False, True, 9, 1, 1, 4096, 96, 1),
     ("t2-conv-T80", 80, 40.0, 8, True, False, 2, 6, 6, 32, 64, 3),
+    # stream gather modes: 1 event per dword load (C_out <= 64), 2 per
+    # dwordx4 load (64 < C_out <= 128, partly idle lanes), and the 1-event
+    # fallback (C_out % 4 != 0)
+    ("t2-conv-c36", 64, 32.0, 8, True, False, 2, 7, 5, 40, 36, 3),
+    ("t2-conv-c100-epi2", 64, 32.0, 8, True, False, 2, 5, 6, 48, 100, 3),
+    ("t2-conv-c66-vec1", 64, 32.0, 8, True, False, 2, 5, 5, 20, 66, 3),
+    ("t1-fc-300-84-epi2", 64, 0.0, 16, False, True, 33, 1, 1, 300, 84, 1),
 ]
 
 

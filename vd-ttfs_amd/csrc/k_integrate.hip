@@ -30,7 +30,7 @@ namespace vdttfs {
 namespace {
 
 constexpr int kBlockBins = 64;  // arrival bins handled per table / per VGPR of bin starts
-constexpr int kListPad = 8;     // zeroed entries after each pixel's merged list
+constexpr int kListPad = 16;    // zeroed entries after each pixel's merged list (two groups)
 constexpr int kMergeWaves = 4;
 
 // ---------------------------------------------------------------------------
@@ -244,13 +244,64 @@ __device__ __forceinline__ Vf<VEC> gather(const __amdgpu_buffer_rsrc_t r, int vo
     return o;
 }
 
-// Weight gathers from global memory through a buffer resource (VEC
-// consecutive c_out per lane).
+// Weight gathers of a group of 8 events.  A gather type fixes which c_out a
+// lane owns (c0(cb, lane) .. + OWN - 1) and fills w[g] with those c_out's
+// weights for event g.
+//
+// GlobalGather<VEC>: one buffer_load per event, the row offset in soffset;
+// lane owns VEC consecutive c_out of a 64*VEC block.  Lanes whose neurons
+// all fired skip their loads (exec-masked).  Measured: the gather cost
+// follows the active lanes, so masked lanes are free, while an out-of-range
+// address for them (to keep the loads unconditional and pipeline the next
+// group's gathers) made narrow layers slower.
 template <int VEC>
 struct GlobalGather {
+    static constexpr int OWN = VEC;
     __amdgpu_buffer_rsrc_t r;
     int voff;
-    __device__ __forceinline__ Vf<VEC> operator()(int row) const { return gather<VEC>(r, voff, row); }
+    __device__ static int c0(int cb, int lane) { return (cb * 64 + lane) * VEC; }
+    __device__ __forceinline__ void group(const int2 (&e)[8], Vf<VEC> (&w)[8], bool live) const {
+        if (live) {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) w[g] = gather<VEC>(r, voff, e[g].x);
+        }
+    }
+};
+
+// PairGather: for 64 < C_out <= 128 (a c_out row of at most 512 B), one
+// dwordx4 load fetches two events at once -- the lower half-wave loads event
+// 2i's row, the upper half event 2i+1's, 4 c_out per lane -- and two
+// v_permlane32_swap exchange the halves' (2,3) and (0,1) components, so that
+// lane (h, r) ends owning c_out 4r+2h, 4r+2h+1 with both events' weights.
+// Every load then carries 1 KB with all 64 lanes busy (a 4-c_out-per-lane
+// load would leave half the wave idle); lanes load for each other, so loads
+// are not skipped per lane.
+struct PairGather {
+    static constexpr int OWN = 2;
+    __amdgpu_buffer_rsrc_t r;
+    int lane_off;  // 16 * (lane % 32)
+    int h;         // lane / 32: which event of a load this lane fetches
+    __device__ static int c0(int, int lane) { return 4 * (lane & 31) + 2 * (lane >> 5); }
+    __device__ __forceinline__ void group(const int2 (&e)[8], Vf<2> (&w)[8], bool) const {
+        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = h == 0 ? e[2 * i].x : e[2 * i + 1].x;
+            const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, row + lane_off, 0, 0);
+            unsigned c0 = x.x, c1 = x.y, c2 = x.z, c3 = x.w;
+            // permlane32_swap(a, b) exchanges a's upper 32 lanes with b's lower 32
+            auto p = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
+            c0 = p[0];
+            c2 = p[1];
+            p = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
+            c1 = p[0];
+            c3 = p[1];
+            w[2 * i].v[0] = __uint_as_float(c0);
+            w[2 * i].v[1] = __uint_as_float(c1);
+            w[2 * i + 1].v[0] = __uint_as_float(c2);
+            w[2 * i + 1].v[1] = __uint_as_float(c3);
+        }
+    }
 };
 
 
@@ -260,7 +311,7 @@ struct GlobalGather {
 // delta_t, fire at carry >= theta[t] >= 1e-5, t >= t_min) or the CuLIF neuron
 // of T3V (I = fma(I, decay, in_t); V += I; fire at V >= th).  CuLIF events
 // carry alpha = 1, so fma(w, 1, acc) is exactly the reference's acc + w.
-template <bool COUNT, int VEC, bool CULIF, class G>
+template <bool COUNT, bool CULIF, class G, int VEC = G::OWN>
 __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
                                              const int2* __restrict__ list,
                                              const int32_t* __restrict__ bstart,
@@ -268,7 +319,7 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
                                              const G& gather_w, unsigned long long& cnt_proc,
                                              unsigned long long& cnt_bin) {
     const int lane = lane_id();
-    const int c0 = (cb * 64 + lane) * VEC;  // first c_out of this lane
+    const int c0 = G::c0(cb, lane);  // first c_out of this lane
     bool ok[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) ok[v] = c0 + v < a.C_out;
@@ -348,11 +399,15 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         float acc[VEC];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+        // one 64-byte scalar load of 8 (row, alpha) pairs per group, issued
+        // one group ahead so that its latency overlaps the current gathers;
+        // the list is zero-padded by two groups, so the look-ahead stays in
+        // the pixel's slot
+        Group8 ahead = *reinterpret_cast<const Group8*>(L + j);
         while (j < blk_end) {
             const int n = (blk_end - j) < 8 ? (blk_end - j) : 8;
-            // one 64-byte scalar load of 8 (row, alpha) pairs; the list is
-            // zero-padded past its end
-            const Group8 grp = *reinterpret_cast<const Group8*>(L + j);
+            const Group8 grp = ahead;
+            ahead = *reinterpret_cast<const Group8*>(L + j + 8);
             const int2* e = grp.v;
 #pragma unroll
             for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(e[g].x), "s"(e[g].y));
@@ -361,10 +416,7 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
             for (int g = 0; g < 8; ++g)
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) w[g].v[v] = 0.0f;
-            if (live) {
-#pragma unroll
-                for (int g = 0; g < 8; ++g) w[g] = gather_w(e[g].x);
-            }
+            gather_w.group(grp.v, w, live);
             if (bend >= j + n) {
                 // the whole group belongs to the open bin
                 if (n == 8) {
@@ -417,7 +469,9 @@ stream_done:
         if (ok[v]) out[pix * a.C_out + c0 + v] = res[v];
 }
 
-template <bool COUNT, int VEC, bool CULIF>
+// EPI = events per load: 1 (GlobalGather<VEC>) or 2 (PairGather, VEC = 2,
+// one c_out block).
+template <bool COUNT, int VEC, bool CULIF, int EPI>
 __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict__ out,
                                                 const int2* __restrict__ list,
                                                 const int32_t* __restrict__ bstart,
@@ -428,12 +482,24 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     map_block(a.n_cblk, cb, pg);
     const int64_t pix = pg * 4 + wave;
     if (pix >= a.n_pix) return;  // uniform per wave
-    const int c0 = (cb * 64 + lane_id()) * VEC;
-    GlobalGather<VEC> g;
-    g.r = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
-    g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
+    const int lane = lane_id();
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
     unsigned long long cnt_proc = 0, cnt_bin = 0;
-    stream_pixel<COUNT, VEC, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
+    if constexpr (EPI == 1) {
+        GlobalGather<VEC> g;
+        g.r = rsrc;
+        const int c0 = GlobalGather<VEC>::c0(cb, lane);
+        g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
+        stream_pixel<COUNT, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
+    } else {
+        static_assert(VEC == 2 && EPI == 2, "PairGather owns 2 c_out per lane");
+        PairGather g;
+        g.r = rsrc;
+        g.lane_off = 16 * (lane & 31);
+        g.h = lane >> 5;
+        stream_pixel<COUNT, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
+    }
     if (COUNT && lane_id() == 0) {
         atomicAdd(&a.counters[0], cnt_proc);
         atomicAdd(&a.counters[1], cnt_bin);
@@ -740,24 +806,35 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     a.C_out = sh.C_out;
     a.decay = culif ? culif->decay : 0.0f;
     a.th = culif ? culif->th : 0.0f;
-    // 4 c_out per lane once a wave's 64 lanes hold >= 128 c_out
-    const int vec = (sh.C_out >= 128 && sh.C_out % 4 == 0) ? 4 : 1;
-    a.n_cblk = (sh.C_out + 64 * vec - 1) / (64 * vec);
+    // 64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (MultiGather);
+    // wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block
+    // C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
+    // events per load there, as lanes whose neurons fired skip their loads
+    int vec = 1, epi = 1;
+    if (sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 128) {
+        epi = 2;
+        vec = 2;
+    } else if (sh.C_out % 4 == 0 && sh.C_out > 128) {
+        vec = 4;
+    }
+    a.n_cblk = epi > 1 ? 1 : (sh.C_out + 64 * vec - 1) / (64 * vec);
     a.w_bytes = (int)wbytes;
     const int waves = 4;
     const int64_t n_pg = (n_pix + waves - 1) / waves;
     const int64_t blocks = n_pg * a.n_cblk;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-#define VD_LAUNCH_STREAM(C, V, L)                                                               \
-    hipLaunchKernelGGL((k_stream<C, V, L>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
+#define VD_LAUNCH_STREAM(C, V, L, E)                                                               \
+    hipLaunchKernelGGL((k_stream<C, V, L, E>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
                        a, out, (const int2*)list, (const int32_t*)bstart, theta)
-#define VD_LAUNCH_STREAM_V(C, L)    \
-    do {                            \
-        if (vec == 4)               \
-            VD_LAUNCH_STREAM(C, 4, L); \
-        else                        \
-            VD_LAUNCH_STREAM(C, 1, L); \
+#define VD_LAUNCH_STREAM_V(C, L)              \
+    do {                                      \
+        if (epi == 2)                         \
+            VD_LAUNCH_STREAM(C, 2, L, 2);     \
+        else if (vec == 4)                    \
+            VD_LAUNCH_STREAM(C, 4, L, 1);     \
+        else                                  \
+            VD_LAUNCH_STREAM(C, 1, L, 1);     \
     } while (0)
     if (culif) {
         if (counters)
