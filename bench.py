@@ -50,9 +50,12 @@ def log(msg: str) -> None:
 
 
 def algorithmic_bytes(w, eproc, n_ev, n_cols, B):
-    """B_int per integrating layer: 4*E_proc (one fp32 weight per integrated
-    synapse) + 8*N_ev (event lists) + 4*OS*N_cols (chunk offsets)
-    + 4*C_out (bias) + 4*N_out (first-spike write)."""
+    """Fused bytes per integrating layer, B_int + 4*N_cols*C_in: the dense
+    input map read once, 4*E_proc (one fp32 weight per integrated synapse),
+    8*N_ev (event lists) + 4*OS*N_cols (chunk offsets), 4*C_out (bias) and
+    4*N_out (first-spike write).  Conv layers build their event lists straight
+    from the dense map; FC layers bucketize first -- either way the layer's
+    whole integrate (bucketize + merge + stream) is priced and timed."""
     OS = w.consts.num_chunks + 1
     total = 0
     per_layer = []
@@ -61,7 +64,9 @@ def algorithmic_bytes(w, eproc, n_ev, n_cols, B):
             per_layer.append(0)
             continue
         n_out = B * l.H_out * l.W_out * l.C_out
-        b = 4 * int(eproc[i]) + 8 * int(n_ev[i]) + 4 * OS * int(n_cols[i]) + 4 * l.C_out + 4 * n_out
+        cin_col = l.C_in if l.kind == 0 else l.H_in * l.W_in * l.C_in
+        b = (4 * int(eproc[i]) + 8 * int(n_ev[i]) + 4 * OS * int(n_cols[i]) + 4 * l.C_out + 4 * n_out
+             + 4 * int(n_cols[i]) * cin_col)
         per_layer.append(b)
         total += b
     return total, per_layer
@@ -397,7 +402,8 @@ def bench_ttfs(args) -> int:
     eproc, ebin, n_ev, n_cols = net.count(d_img)
     b_int, per_layer = algorithmic_bytes(w, eproc, n_ev, n_cols, B)
     ms_step = elapsed * 1000.0 / args.steps
-    integ_ms_step = integ_ms / args.steps
+    # a layer's whole integrate: the bucketize pass (FC layers) + merge + stream
+    integ_ms_step = (integ_ms + bkt_ms) / args.steps
     launches_per_step = integ_n / args.steps
     achieved = b_int / (integ_ms_step * 1e-3) / 1e9
     key = workload_key(B, w.consts) if vgg else f"{w.name} B={B} T={w.consts.T} delta={w.consts.delta}"
@@ -432,9 +438,10 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": (tr[0] / tr[1]) if tr else None,
-            "kernel": "integrator = k_merge + k_stream per integrating layer (k_integrate_generic "
-                      "for layers under 32 outputs); a launch is one layer's integrate, achieved = "
-                      "algorithmic bytes of a step / integrator time of a step",
+            "kernel": "integrator = a layer's k_merge_dense + k_stream (conv) or k_bucketize + "
+                      "k_merge + k_stream (FC; k_integrate_generic under 32 outputs); a launch is "
+                      "one layer's integrate, achieved = fused algorithmic bytes of a step / "
+                      "integrator time of a step",
             "algorithmic_bytes_per_step": b_int,
             "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
             "traffic_per_step": tr[0] if tr else None,

@@ -345,18 +345,25 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
     if (!d_out || !d_in || !d_kernel || !d_bias || !d_lut_decay || !d_lut_th)
         return set_error(VDTTFS_E_INVALID, "layer_forward: null buffer");
     const int64_t cols = is_fc ? B : (int64_t)B * H_in * W_in;
-    VD_TRY(ensure_bin_scratch(ctx, (size_t)cols * C_in, (size_t)cols));
     const int64_t n_pix = is_fc ? B : (int64_t)B * H_out * W_out;
     const int64_t cap = merged_list_cap(s);
     VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     const bool count = eproc || ebin;
     if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
-    VD_TRY(launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, (vd_event*)ctx->bin_ev,
-                                 (int32_t*)ctx->bin_off, nullptr));
-    VD_TRY(launch_integrate_bins(ctx, d_out, (const vd_event*)ctx->bin_ev,
-                                 (const int32_t*)ctx->bin_off, (int2*)ctx->mrg_list, cap,
-                                 (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
-                                 count ? ctx->d_counters : nullptr));
+    if (integrate_dense_ok(ctx, s)) {
+        // conv: merged lists straight from the dense map
+        VD_TRY(launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, (int2*)ctx->mrg_list, cap,
+                                      (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
+                                      count ? ctx->d_counters : nullptr));
+    } else {
+        VD_TRY(ensure_bin_scratch(ctx, (size_t)cols * C_in, (size_t)cols));
+        VD_TRY(launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, (vd_event*)ctx->bin_ev,
+                                     (int32_t*)ctx->bin_off, nullptr));
+        VD_TRY(launch_integrate_bins(ctx, d_out, (const vd_event*)ctx->bin_ev,
+                                     (const int32_t*)ctx->bin_off, (int2*)ctx->mrg_list, cap,
+                                     (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
+                                     count ? ctx->d_counters : nullptr));
+    }
     if (count) {
         unsigned long long h[4];
         VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));

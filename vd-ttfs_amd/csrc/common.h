@@ -98,6 +98,14 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
                           int2* list, int64_t list_cap, int32_t* bstart, const float* W,
                           const float* bias, const float* theta, int t_min, const IntegShape& s,
                           unsigned long long* counters, const CulifNeuron* culif = nullptr);
+// Conv layers of the merged-list path: the merged lists are built straight
+// from the dense spike map d_in (no bucketize pass); alpha is the layer's
+// decay LUT.  Same results as bucketize + launch_integrate_bins.
+bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& s);
+int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
+                           int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
+                           const float* theta, int t_min, const IntegShape& s,
+                           unsigned long long* counters, const CulifNeuron* culif = nullptr);
 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
 int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,

@@ -7,7 +7,7 @@
 // c_out; conv weights are re-laid out OIHW -> HWIO once at creation (one
 // weight row per event); an FC layer's input is flattened in the
 // reference's NCHW order, because the order of the per-step sums follows
-// the input index.  Conv layers run bucketize -> merge -> stream with the
+// the input index.  Conv layers run (bucketize ->) merge -> stream with the
 // CuLIF neuron and alpha = 1 (fma(w, 1, acc) is the reference's acc + w).
 // The recurrent FC layer's feed-forward sums are computed per (sample, step)
 // in parallel from its dense input (k_fc_currents) before the per-step
@@ -273,12 +273,21 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
                 break;
             case VDTTFS_CULIF_CONV: {
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;
-                VD_TRY(launch_bucketize_bins(ctx, cur, cols, d.C_in, net->ones, net->ev, net->off,
-                                             count_here ? ctx->d_counters + 2 : nullptr));
                 IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3, 1, 0};
-                VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
-                                             net->bstart, l.W, nullptr, nullptr, 0, sh,
-                                             count_here ? ctx->d_counters : nullptr, &nrn));
+                // narrow inputs build the merged lists from the dense map (the
+                // bin-layout bucketize then only counts retained events)
+                const bool dense = integrate_dense_ok(ctx, sh);
+                if (!dense || count_here)
+                    VD_TRY(launch_bucketize_bins(ctx, cur, cols, d.C_in, net->ones, net->ev, net->off,
+                                                 count_here ? ctx->d_counters + 2 : nullptr));
+                if (dense)
+                    VD_TRY(launch_integrate_dense(ctx, l.out, cur, net->ones, net->list, l.list_cap,
+                                                  net->bstart, l.W, nullptr, nullptr, 0, sh,
+                                                  count_here ? ctx->d_counters : nullptr, &nrn));
+                else
+                    VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
+                                                 net->bstart, l.W, nullptr, nullptr, 0, sh,
+                                                 count_here ? ctx->d_counters : nullptr, &nrn));
                 if (count_here) {
                     unsigned long long h[4];
                     VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));

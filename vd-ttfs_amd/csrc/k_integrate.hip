@@ -174,6 +174,144 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// k_merge_dense: the same merged list built straight from the dense NHWC
+// spike map, for conv layers with C_in <= 64, so they need no separate
+// bucketize pass.  One wave per output pixel counting-sorts the pixel's
+// receptive events by arrival bin in LDS.  The pixel's (tap, cin) elements,
+// flattened in (kh, kw, cin) order, are taken 64 per chunk (a 3-channel
+// layer's 27 elements are one chunk): pass 1 counts every bin, a wave scan
+// gives the bin starts, pass 2 (re-reading the chunk, now in cache) places
+// each event at its bin's
+// cursor plus its rank among the chunk's lanes of the same bin.  The rank
+// comes from a multisplit of bit ballots (same-bin mask = AND over the bin's
+// bits of the matching ballot), so the order within a bin is (kh, kw, cin) --
+// the reference's per-bin fma order.  Neighbouring pixels read the same
+// columns, which stay in L2.
+struct DenseMergeArgs {
+    int2* list;            // [n_pix][cap]
+    int32_t* bstart;       // [n_pix][T+1]
+    const float* in;       // [n_cols][C_in] spike times
+    const float* alpha;    // decay LUT, T+1 entries
+    int64_t n_pix;
+    int64_t cap;
+    int T;
+    float tfs;
+    int alpha_by_time;
+    int nbits;             // bits of a bin index (ceil(log2 T))
+    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad;
+    int rowbytes;          // C_out * 4
+    float inv_cin;         // 1 / C_in
+};
+
+constexpr int kDenseMaxBins = 256;
+constexpr int kDenseMaxCin = 64;
+
+template <int KMAX>
+__global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs a) {
+    __shared__ int cur_all[kMergeWaves][kDenseMaxBins];
+    __shared__ int kinfo_all[kMergeWaves][2 * KMAX];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
+    if (pix >= a.n_pix) return;  // uniform per wave
+    int* cur = cur_all[wave];
+    int* kinfo = kinfo_all[wave];
+    const int w_out = (int)(pix % a.W_out);
+    const int64_t q = pix / a.W_out;
+    const int h_out = (int)(q % a.H_out);
+    const int img = (int)(q / a.H_out);
+    // in-bounds receptive columns, compacted in (kh, kw) order
+    int nk;
+    {
+        bool v = false;
+        int col = 0;
+        if (lane < a.K_h * a.K_w) {
+            const int kh = lane / a.K_w, kw = lane - kh * a.K_w;
+            const int hi = h_out - a.pad + kh, wi = w_out - a.pad + kw;
+            v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
+            col = (img * a.H_in + hi) * a.W_in + wi;
+        }
+        const uint64_t m = __ballot(v);
+        nk = uniform(__popcll(m));
+        if (v) {
+            const int slot = __popcll(m & lanemask_lt());
+            kinfo[slot] = col;
+            kinfo[KMAX + slot] = lane * a.C_in * a.rowbytes;
+        }
+    }
+    for (int t = lane; t < a.T; t += 64) cur[t] = 0;
+    wave_sync();
+    const int nel = nk * a.C_in;  // <= KMAX * 64
+    // element f of the pixel: tap k = f / C_in (the quotient's fractional
+    // part is >= 0.5 / 64, so the float product rounds it correctly), cin c
+    auto element = [&](int f, float& x, int& rowb) {
+        const int k = (int)(((float)f + 0.5f) * a.inv_cin);
+        const int c = f - k * a.C_in;
+        x = a.in[(int64_t)kinfo[k] * a.C_in + c];
+        rowb = kinfo[KMAX + k] + c * a.rowbytes;
+    };
+    // pass 1: events per bin
+    for (int f0 = 0; f0 < nel; f0 += 64) {
+        float x = kInfTime;
+        int rowb = 0;
+        if (f0 + lane < nel) element(f0 + lane, x, rowb);
+        const int b = arrival_bin(x, a.tfs, a.T);
+        if (b >= 0) atomicAdd(&cur[b], 1);
+    }
+    wave_sync();
+    // bin starts: lane l scans bins 4l .. 4l+3
+    int32_t* bs = a.bstart + pix * (int64_t)(a.T + 1);
+    int v4[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * lane + i;
+        v4[i] = t < a.T ? cur[t] : 0;
+        sum += v4[i];
+    }
+    const int incl = wave_incl_scan(sum);
+    int run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * lane + i;
+        if (t < a.T) {
+            cur[t] = run;
+            bs[t] = run;
+        }
+        run += v4[i];
+    }
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (lane == 0) bs[a.T] = total;
+    wave_sync();
+    // pass 2: stable placement, chunk by chunk in (kh, kw, cin) order
+    int2* out = a.list + pix * a.cap;
+    const uint64_t lt = lanemask_lt();
+    for (int f0 = 0; f0 < nel; f0 += 64) {
+        float x = kInfTime;
+        int rowb = 0;
+        if (f0 + lane < nel) element(f0 + lane, x, rowb);
+        const int b = arrival_bin(x, a.tfs, a.T);
+        const bool valid = b >= 0;
+        uint64_t m = __ballot(valid);
+        if (m == 0) continue;  // uniform
+        for (int bit = 0; bit < a.nbits; ++bit) {
+            const bool set = valid && ((b >> bit) & 1);
+            const uint64_t bb = __ballot(set);
+            m &= set ? bb : ~bb;
+        }
+        if (valid) {
+            const int pos = cur[b] + __popcll(m & lt);
+            const float al = a.alpha[alpha_index(x, b, a.alpha_by_time, a.T)];
+            out[pos] = make_int2(rowb, __float_as_int(al));
+        }
+        wave_sync();
+        if (valid && (m & lt) == 0) cur[b] += __popcll(m);
+        wave_sync();
+    }
+    // zeroed tail: the stream kernel reads whole groups of 8 entries
+    for (int i = lane; i < kListPad; i += 64) out[total + i] = make_int2(0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // k_stream: one wave64 per (output pixel, 64-wide c_out block); lanes are
 // c_out.  The merged list is read through the scalar cache 8 events at a time
 // (one s_load_dwordx16), each event costs one buffer_load (the weight row's
@@ -305,13 +443,30 @@ struct PairGather {
 };
 
 
+// List reader: groups of 8 merged events (row, alpha) as wave-uniform
+// SGPRs, one s_load_dwordx16 per group, read one group ahead (the list is
+// zero-padded by two groups).
+struct ScalarList {
+    const int2* L;
+    Group8 ahead;
+    __device__ __forceinline__ void start(const int2* L_, int j, int64_t) {
+        L = L_;
+        ahead = *reinterpret_cast<const Group8*>(L + j);
+    }
+    __device__ __forceinline__ Group8 take(int j) {
+        const Group8 g = ahead;
+        ahead = *reinterpret_cast<const Group8*>(L + j + 8);
+        return g;
+    }
+};
+
 // Integrates one output pixel for one c_out block (lane = VEC c_out) from its
 // merged event list and writes the first-spike times.  CULIF selects the
 // neuron that closes each bin: the LUT-threshold neuron of T1V/T2V (carry +=
 // delta_t, fire at carry >= theta[t] >= 1e-5, t >= t_min) or the CuLIF neuron
 // of T3V (I = fma(I, decay, in_t); V += I; fire at V >= th).  CuLIF events
 // carry alpha = 1, so fma(w, 1, acc) is exactly the reference's acc + w.
-template <bool COUNT, bool CULIF, class G, int VEC = G::OWN>
+template <bool COUNT, bool CULIF, class G, class LR = ScalarList, int VEC = G::OWN>
 __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
                                              const int2* __restrict__ list,
                                              const int32_t* __restrict__ bstart,
@@ -399,15 +554,12 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         float acc[VEC];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-        // one 64-byte scalar load of 8 (row, alpha) pairs per group, issued
-        // one group ahead so that its latency overlaps the current gathers;
-        // the list is zero-padded by two groups, so the look-ahead stays in
-        // the pixel's slot
-        Group8 ahead = *reinterpret_cast<const Group8*>(L + j);
+        // groups of 8 (row, alpha) pairs, read one group (chunk) ahead
+        LR lr;
+        lr.start(L, j, a.cap);
         while (j < blk_end) {
             const int n = (blk_end - j) < 8 ? (blk_end - j) : 8;
-            const Group8 grp = ahead;
-            ahead = *reinterpret_cast<const Group8*>(L + j + 8);
+            const Group8 grp = lr.take(j);
             const int2* e = grp.v;
 #pragma unroll
             for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(e[g].x), "s"(e[g].y));
@@ -743,53 +895,23 @@ int merged_list_cap(const IntegShape& sh) {
     return (sh.is_fc ? 1 : sh.K_h * sh.K_w) * sh.C_in + kListPad;
 }
 
-int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
-                          int2* list, int64_t list_cap, int32_t* bstart, const float* W,
-                          const float* bias, const float* theta, int t_min, const IntegShape& sh,
-                          unsigned long long* counters, const CulifNeuron* culif) {
-    const int T = ctx->c.T, D = ctx->c.delta;
-    const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
-    const int64_t wbytes = (int64_t)nk_max * sh.C_in * sh.C_out * 4;
-    const bool wave_ok = sh.C_out >= 32 && nk_max <= 25 && wbytes < INT64_C(0x7fffffff) &&
-                         sh.C_in < (1 << 24);
-    if (!wave_ok) {
-        if (culif)
-            return set_error(VDTTFS_E_UNSUPPORTED,
-                             "CuLIF engine layers need C_out >= 32, <= 25 taps and < 2 GB of weights");
-        return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
-    }
-    const int64_t n_pix = (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
-    const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
-    if (!list || !bstart || list_cap < cap)
-        return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
-    MergeArgs m{};
-    m.list = list;
-    m.bstart = bstart;
-    m.ev = ev;
-    m.off = off;
-    m.n_pix = n_pix;
-    m.cap = cap;
-    m.T = T;
-    m.H_in = sh.H_in;
-    m.W_in = sh.W_in;
-    m.C_in = sh.C_in;
-    m.H_out = sh.H_out;
-    m.W_out = sh.W_out;
-    m.K_h = sh.K_h;
-    m.K_w = sh.K_w;
-    m.pad = sh.pad;
-    m.is_fc = sh.is_fc;
-    m.rowbytes = sh.C_out * 4;
-    const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
-    if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-    if (nk_max == 1)
-        hipLaunchKernelGGL(k_merge<1>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
-    else if (nk_max <= 9)
-        hipLaunchKernelGGL(k_merge<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
-    else
-        hipLaunchKernelGGL(k_merge<25>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
-    VD_HIP(hipGetLastError());
+namespace {
 
+// Shape limits of the merged-list path (merge + k_stream).
+bool wave_path_ok(const IntegShape& sh, int64_t* wbytes) {
+    const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
+    *wbytes = (int64_t)nk_max * sh.C_in * sh.C_out * 4;
+    return sh.C_out >= 32 && nk_max <= 25 && *wbytes < INT64_C(0x7fffffff) && sh.C_in < (1 << 24);
+}
+
+int64_t n_pixels(const IntegShape& sh) {
+    return (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
+}
+
+int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
+                  const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
+                  const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
+    const int64_t n_pix = n_pixels(sh);
     StreamArgs a{};
     a.out = out;
     a.list = list;
@@ -800,14 +922,14 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     a.counters = counters;
     a.n_pix = n_pix;
     a.cap = cap;
-    a.T = T;
-    a.D = D;
+    a.T = ctx->c.T;
+    a.D = ctx->c.delta;
     a.t_min = t_min;
     a.C_out = sh.C_out;
     a.decay = culif ? culif->decay : 0.0f;
     a.th = culif ? culif->th : 0.0f;
-    // 64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (MultiGather);
-    // wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block
+    // 64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (PairGather);
+    // wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block.
     // C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
     // events per load there, as lanes whose neurons fired skip their loads
     int vec = 1, epi = 1;
@@ -826,7 +948,7 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
 #define VD_LAUNCH_STREAM(C, V, L, E)                                                               \
     hipLaunchKernelGGL((k_stream<C, V, L, E>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, \
-                       a, out, (const int2*)list, (const int32_t*)bstart, theta)
+                       a, out, list, bstart, theta)
 #define VD_LAUNCH_STREAM_V(C, L)              \
     do {                                      \
         if (epi == 2)                         \
@@ -851,6 +973,106 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
 #undef VD_LAUNCH_STREAM
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
+}
+
+}  // namespace
+
+// Measured per VGG layer against bucketize + k_merge: the dense merge is
+// faster up to C_in = 64 and slower beyond, where each pixel's wave has many
+// chunks and few pixels share the work; up to 9 taps (a 5x5 kernel's 25
+// chunks spill registers).
+bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    int64_t wbytes;
+    return !sh.is_fc && wave_path_ok(sh, &wbytes) && ctx->c.T <= kDenseMaxBins &&
+           sh.C_in <= kDenseMaxCin && sh.K_h * sh.K_w <= 9;
+}
+
+int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
+                          int2* list, int64_t list_cap, int32_t* bstart, const float* W,
+                          const float* bias, const float* theta, int t_min, const IntegShape& sh,
+                          unsigned long long* counters, const CulifNeuron* culif) {
+    int64_t wbytes;
+    if (!wave_path_ok(sh, &wbytes)) {
+        if (culif)
+            return set_error(VDTTFS_E_UNSUPPORTED,
+                             "CuLIF engine layers need C_out >= 32, <= 25 taps and < 2 GB of weights");
+        return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
+    }
+    const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
+    const int64_t n_pix = n_pixels(sh);
+    const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
+    if (!list || !bstart || list_cap < cap)
+        return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
+    MergeArgs m{};
+    m.list = list;
+    m.bstart = bstart;
+    m.ev = ev;
+    m.off = off;
+    m.n_pix = n_pix;
+    m.cap = cap;
+    m.T = ctx->c.T;
+    m.H_in = sh.H_in;
+    m.W_in = sh.W_in;
+    m.C_in = sh.C_in;
+    m.H_out = sh.H_out;
+    m.W_out = sh.W_out;
+    m.K_h = sh.K_h;
+    m.K_w = sh.K_w;
+    m.pad = sh.pad;
+    m.is_fc = sh.is_fc;
+    m.rowbytes = sh.C_out * 4;
+    const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
+    if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    if (nk_max == 1)
+        hipLaunchKernelGGL(k_merge<1>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    else if (nk_max <= 9)
+        hipLaunchKernelGGL(k_merge<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    else
+        hipLaunchKernelGGL(k_merge<25>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    VD_HIP(hipGetLastError());
+    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
+}
+
+int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
+                           int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
+                           const float* theta, int t_min, const IntegShape& sh,
+                           unsigned long long* counters, const CulifNeuron* culif) {
+    int64_t wbytes;
+    if (!integrate_dense_ok(ctx, sh) || !wave_path_ok(sh, &wbytes))
+        return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
+    const int nk_max = sh.K_h * sh.K_w;
+    const int64_t n_pix = n_pixels(sh);
+    const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
+    if (!list || !bstart || list_cap < cap)
+        return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
+    DenseMergeArgs m{};
+    m.list = list;
+    m.bstart = bstart;
+    m.in = in;
+    m.alpha = alpha;
+    m.n_pix = n_pix;
+    m.cap = cap;
+    m.T = ctx->c.T;
+    m.tfs = ctx->c.tfs;
+    m.alpha_by_time = ctx->c.alpha_by_time;
+    int nbits = 0;
+    while ((1 << nbits) < m.T) ++nbits;
+    m.nbits = nbits;
+    m.H_in = sh.H_in;
+    m.W_in = sh.W_in;
+    m.C_in = sh.C_in;
+    m.H_out = sh.H_out;
+    m.W_out = sh.W_out;
+    m.K_h = sh.K_h;
+    m.K_w = sh.K_w;
+    m.pad = sh.pad;
+    m.rowbytes = sh.C_out * 4;
+    m.inv_cin = 1.0f / (float)sh.C_in;
+    const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
+    if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    hipLaunchKernelGGL(k_merge_dense<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
+    VD_HIP(hipGetLastError());
+    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
 }
 
 }  // namespace vdttfs

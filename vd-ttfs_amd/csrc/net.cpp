@@ -155,19 +155,32 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             s.K_w = fc ? 1 : d.K_w;
             s.pad = (fc || !ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
             if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
+            // conv layers build their merged lists from the dense map; the
+            // bin-layout bucketize runs for FC layers, and in a counting
+            // forward for its retained-event count
+            const bool dense = integrate_dense_ok(ctx, s);
             TimedPair tb{}, ti{};
-            if (net->timing && !count) VD_TRY(mark(net, &tb.a));
-            VD_TRY(launch_bucketize_bins(ctx, cur, l.cols, l.cin_col, l.alpha, net->ev, net->off,
-                                         count ? ctx->d_counters + 2 : nullptr));
-            if (net->timing && !count) {
-                VD_TRY(mark(net, &tb.b));
-                tb.kind = 1;
-                net->pending.push_back(tb);
-                ti.a = tb.b;
+            if (!dense || count) {
+                if (net->timing && !count) VD_TRY(mark(net, &tb.a));
+                VD_TRY(launch_bucketize_bins(ctx, cur, l.cols, l.cin_col, l.alpha, net->ev, net->off,
+                                             count ? ctx->d_counters + 2 : nullptr));
+                if (net->timing && !count) {
+                    VD_TRY(mark(net, &tb.b));
+                    tb.kind = 1;
+                    net->pending.push_back(tb);
+                    ti.a = tb.b;
+                }
+            } else if (net->timing) {
+                VD_TRY(mark(net, &ti.a));
             }
-            VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
-                                         net->bstart, l.W, l.bias, l.theta, l.t_min, s,
-                                         count ? ctx->d_counters : nullptr));
+            if (dense)
+                VD_TRY(launch_integrate_dense(ctx, l.out, cur, l.alpha, net->list, l.list_cap,
+                                              net->bstart, l.W, l.bias, l.theta, l.t_min, s,
+                                              count ? ctx->d_counters : nullptr));
+            else
+                VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
+                                             net->bstart, l.W, l.bias, l.theta, l.t_min, s,
+                                             count ? ctx->d_counters : nullptr));
             if (net->timing && !count) {
                 VD_TRY(mark(net, &ti.b));
                 ti.kind = 0;

@@ -12,7 +12,7 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
 benchmark, and the same two counters over ``bench.py --copy-calibration``
 (an elementwise copy of a known number of bytes).  Each counter is scaled by
 known_bytes / counted_bytes of the copy, then summed over the integrator
-dispatches (k_merge + k_stream, or the generic integrator) of one
+dispatches (bucketize + merge + stream, or the generic integrator) of one
 non-counting forward.  The last line is machine-readable and is what
 bench.py reports as ``roofline.traffic``.
 """
@@ -24,7 +24,8 @@ import os
 import re
 import sys
 
-INTEGRATOR = ("k_merge", "k_stream", "k_integrate_generic")
+# every kernel of a layer's integrate: bucketize (FC layers), merge, stream
+INTEGRATOR = ("k_bucketize", "k_merge", "k_stream", "k_integrate_generic")
 COPY_BYTES_DEFAULT = 1 << 30  # bench.py --copy-calibration moves 2^28 floats each way
 
 
@@ -89,7 +90,7 @@ def layers(d: str, name: str) -> str:
         out.append("| %d | %s | %s | %.1f |" % (i, n, r["Grid_Size_X"], us))
     out.append("")
     out.append("kernel time of the last non-counting forward: %.1f us, of which integrator "
-               "(k_merge + k_stream) %.1f us" % (tot, integ))
+               "(bucketize + merge + stream) %.1f us" % (tot, integ))
     return "\n".join(out)
 
 
@@ -134,10 +135,10 @@ def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str,
         if n.startswith(INTEGRATOR):
             tf += fb
             tw += wb
-            if not n.startswith("k_merge"):
+            if n.startswith(("k_stream", "k_integrate_generic")):
                 n_integ += 1
     lines.append("")
-    lines.append(f"integrator (k_merge + k_stream) per forward: FETCH {tf:.6g} B, WRITE {tw:.6g} B, "
+    lines.append(f"integrator (bucketize + merge + stream) per forward: FETCH {tf:.6g} B, WRITE {tw:.6g} B, "
                  f"{n_integ} integrating layers")
     lines.append(f"TRAFFIC_PER_STEP_BYTES={tf + tw:.0f} LAUNCHES_PER_STEP={n_integ} "
                  f"FETCH_SCALE={ff:.5f} WRITE_SCALE={wf:.5f}")
