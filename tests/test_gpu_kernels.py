@@ -172,6 +172,35 @@ def test_integrate_paths_bitexact(gpu_ctx_factory, case):
     np.testing.assert_array_equal(d_out3.download(), exp)
 
 
+@pytest.mark.parametrize("shape", ["conv", "fc"])
+def test_integrate_theta_not_monotone(gpu_ctx_factory, shape):
+    """Threshold tables the engine may not skip empty bins on: a shuffled
+    theta (rises and falls), entries below 1e-5 and t_min > 0, next to the
+    monotone decaying table the skip relies on."""
+    say(f"integrate non-monotone theta ({shape})")
+    rng = np.random.default_rng(77)
+    tc = consts(64, 0.0, 8, True)
+    ctx = gpu_ctx_factory(tc)
+    is_fc = shape == "fc"
+    sp, Wt, bias, n_cols, shp = layer_inputs(rng, tc, is_fc, 6 if is_fc else 2, 6, 6,
+                                              40 if is_fc else 12, 64, 3)
+    sp = np.where(rng.random(sp.size) < 0.7, np.float32(9999.0), sp).astype(np.float32)  # sparse: empty bins
+    alpha, theta_mono = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    theta_mix = rng.permutation(theta_mono).astype(np.float32)
+    theta_mix[5:9] = np.float32(1e-6)
+    d_in, d_W, d_b, d_a = ctx.to_device(sp), ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha)
+    for theta, t_min in ((theta_mix, 3), (theta_mono, 0), (theta_mono * np.float32(0.3), 7)):
+        exp, ep, eb = oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shp, t_min, is_fc)
+        d_t = ctx.to_device(theta)
+        d_out = ctx.empty(exp.size, np.float32)
+        ctx.layer_forward(d_out, d_in, d_W, d_b, d_a, d_t, t_min, is_fc=is_fc, **shp)
+        ctx.synchronize()
+        assert np.any(exp < INF) and np.any(exp == INF)
+        np.testing.assert_array_equal(d_out.download(), exp)
+        gp, gb = ctx.layer_forward(d_out, d_in, d_W, d_b, d_a, d_t, t_min, is_fc=is_fc, count=True, **shp)
+        assert (gp, gb) == (ep, eb)
+
+
 def test_integrate_oversized_bins(gpu_ctx_factory):
     """Bins holding more events than the wave's merged list (windowed path)."""
     say("integrate oversized bins")

@@ -485,7 +485,8 @@ __global__ __launch_bounds__(1024) void k_culif_fc_rec(CRecArgs a) {
 //   cur[n][t][o] = sum over j ascending with step(x[n][j]) == t of W_t[j][o]
 // is summed exactly as the reference's bucket order sums it (W_t is the
 // [in][out] transpose: each term is one coalesced row segment).
-constexpr int kFcBins = 4;
+constexpr int kFcBins = 2;    // arrival steps per wave
+constexpr int kFcUnroll = 4;  // 64-input chunks loaded together
 
 __global__ __launch_bounds__(256) void k_fc_currents(const float* __restrict__ x,
                                                      const float* __restrict__ W,
@@ -505,26 +506,34 @@ __global__ __launch_bounds__(256) void k_fc_currents(const float* __restrict__ x
     float acc[kFcBins];
 #pragma unroll
     for (int k = 0; k < kFcBins; ++k) acc[k] = 0.0f;
-    for (int base = 0; base < F; base += 64) {
-        const int j = base + lane;
-        const int st = culif_bin(j < F ? X[j] : kInfTime, T);
+    for (int base0 = 0; base0 < F; base0 += 64 * kFcUnroll) {
+        int st[kFcUnroll];
 #pragma unroll
-        for (int k = 0; k < kFcBins; ++k) {
-            uint64_t m = __ballot(st == t0 + k);
-            while (m) {
-                // up to 8 gathers in flight, added in ascending j
-                int js[8];
+        for (int r = 0; r < kFcUnroll; ++r) {
+            const int j = base0 + 64 * r + lane;
+            st[r] = culif_bin(j < F ? X[j] : kInfTime, T);
+        }
 #pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    js[g] = m ? base + (int)__builtin_ctzll(m) : -1;
-                    m &= m - 1;
+        for (int r = 0; r < kFcUnroll; ++r) {
+            const int base = base0 + 64 * r;
+#pragma unroll
+            for (int k = 0; k < kFcBins; ++k) {
+                uint64_t m = __ballot(st[r] == t0 + k);
+                while (m) {
+                    // up to 8 gathers in flight, added in ascending j
+                    int js[8];
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        js[g] = m ? base + (int)__builtin_ctzll(m) : -1;
+                        m &= m - 1;
+                    }
+                    float w[8];
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) w[g] = js[g] >= 0 ? W[(int64_t)js[g] * out_f + oo] : 0.0f;
+#pragma unroll
+                    for (int g = 0; g < 8; ++g)
+                        if (js[g] >= 0) acc[k] = acc[k] + w[g];
                 }
-                float w[8];
-#pragma unroll
-                for (int g = 0; g < 8; ++g) w[g] = js[g] >= 0 ? W[(int64_t)js[g] * out_f + oo] : 0.0f;
-#pragma unroll
-                for (int g = 0; g < 8; ++g)
-                    if (js[g] >= 0) acc[k] = acc[k] + w[g];
             }
         }
     }
