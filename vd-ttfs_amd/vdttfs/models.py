@@ -21,7 +21,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import check, lib
+from ._lib import Blob, BlobLayer, check, lib
 from .core import (CULIF_CONV, CULIF_FC, CULIF_FC_REC, CULIF_POOL, CULIF_RAW_CONV, LAYER_CONV,
                    LAYER_FC, LAYER_POOL, LAYER_VMEM, READOUT_ARGMAX, READOUT_ARGMIN, CulifLayerSpec,
                    Layer, TaskConsts, task3_consts)
@@ -85,6 +85,44 @@ def _fc(seed, idx, cin, cout, tc, td=0.0, vmem=False, H=1, W=1, C=None):
 
 def _pool(H, W, Cc):
     return Layer(LAYER_POOL, H, W, Cc, H // 2, W // 2, Cc)
+
+
+def write_weights_blob(path: str, layers) -> int:
+    """Writes the integrating layers (conv, FC, vmem readout) of a layer list
+    in the reference's weights format (the save side of WIO1:31-70, read back
+    by vdttfs_blob_read / the drivers): conv kernels HWIO, FC kernels
+    [C_in][C_out], one bias per output, one tc_fire and one td float.
+    Returns the number of layers written."""
+    integ = [l for l in layers if l.kernel is not None]
+    arr = (BlobLayer * len(integ))()
+    keep = []
+    fp = C.POINTER(C.c_float)
+    for i, l in enumerate(integ):
+        k = np.ascontiguousarray(l.kernel, np.float32).ravel()
+        b = np.ascontiguousarray(l.bias, np.float32).ravel()
+        keep += [k, b]
+        if l.kind == LAYER_CONV:
+            shape = (l.K_h, l.K_w, l.C_in, l.C_out)
+        else:
+            shape = (l.H_in * l.W_in * l.C_in, l.C_out)
+        if k.size != int(np.prod(shape)) or b.size != l.C_out:
+            raise ValueError(f"layer {i}: kernel/bias sizes do not match {shape}")
+        e = arr[i]
+        e.ndim = len(shape)
+        for j, v in enumerate(shape):
+            e.shape[j] = v
+        e.kernel_elems = k.size
+        e.kernel = k.ctypes.data_as(fp)
+        e.bias_ndim = 1
+        e.bias_size = b.size
+        e.bias = b.ctypes.data_as(fp)
+        e.tc_ndim = 1
+        e.td_ndim = 1
+        e.tc_fire = l.tc_fire
+        e.td = l.td
+    blob = Blob(len(integ), arr)
+    check(lib().vdttfs_blob_write(path.encode(), C.byref(blob)))
+    return len(integ)
 
 
 def lenet5(seed: int = 1, T: int = 64, delta: int = 16) -> Workload:
