@@ -27,10 +27,11 @@ def spike_map(rng, n, T, p=0.5):
     return s
 
 
-# C_in <= 4 runs the LDS-tiled kernel (16-pixel row tiles, ragged here);
-# larger C_in the per-pixel scalar-load kernel
+# C_in <= 4 runs the LDS-tiled kernel (16-pixel row tiles, ragged here),
+# larger C_in the lane-broadcast kernel (T > 64: several 64-step blocks)
 @pytest.mark.parametrize("T,delta,C_out,C_in,W", [(64, 32, 70, 2, 37), (48, 16, 64, 2, 7),
-                                                  (32, 32, 5, 1, 16), (64, 32, 64, 5, 11),
+                                                  (32, 32, 5, 1, 16), (80, 16, 40, 3, 9),
+                                                  (64, 32, 64, 4, 20), (64, 32, 64, 5, 11),
                                                   (80, 16, 33, 6, 5)])
 def test_conv1_raw(gpu_ctx_factory, T, delta, C_out, C_in, W):
     say(f"culif conv1_raw T={T} delta={delta} C_out={C_out} C_in={C_in} W={W}")
@@ -45,6 +46,29 @@ def test_conv1_raw(gpu_ctx_factory, T, delta, C_out, C_in, W):
     got = d_out.download()
     assert np.any(exp < INF) and np.any(exp == INF)
     np.testing.assert_array_equal(got, exp)
+
+
+def test_conv1_raw_nonfinite_weight(gpu_ctx_factory):
+    """An infinite weight turns the reference's fma with a zero input into NaN:
+    every in-bounds tap is integrated, zero inputs included."""
+    say("culif conv1_raw with an infinite weight")
+    T, delta = 64, 32
+    ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
+    rng = np.random.default_rng(34)
+    N, C_in, C_out, H, W = 1, 2, 64, 6, 5
+    data = (rng.random((N, C_in, H, W, T)) < 0.1).astype(np.float32)
+    w = (rng.standard_normal((C_out, C_in, 3, 3)) * 0.8).astype(np.float32)
+    w[3, 1, 1, 1] = np.inf
+    exp = oracle.culif_conv1_raw(data, w, N, C_in, C_out, H, W, T, delta, 0.5, 1.0)
+    d_out = ctx.empty(exp.size)
+    ctx.culif_conv1_raw(ctx.to_device(data), d_out, ctx.to_device(w), N, C_in, C_out, H, W, 0.5, 1.0)
+    np.testing.assert_array_equal(d_out.download(), exp)
+    # the non-finite weight changes c_out 3 (inf * 1 fires at once, inf * 0 is
+    # NaN and never fires), so skipping zero inputs would have shown
+    w0 = w.copy()
+    w0[3, 1, 1, 1] = 0.0
+    ref0 = oracle.culif_conv1_raw(data, w0, N, C_in, C_out, H, W, T, delta, 0.5, 1.0)
+    assert np.any(exp.reshape(C_out, H, W)[3] != ref0.reshape(C_out, H, W)[3])
 
 
 def test_bucketize_conv_and_fc(gpu_ctx_factory):
