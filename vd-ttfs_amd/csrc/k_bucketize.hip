@@ -5,8 +5,9 @@
 //  * pass 1 builds a wave-private histogram in LDS (order-free atomics);
 //  * a wave prefix scan turns it into bucket offsets, written coalesced;
 //  * pass 2 scatters stably: lanes sharing a bucket are ranked in lane
-//    (= ascending cin) order with ballot + popcount, one distinct bucket per
-//    iteration, so the output order is exactly the reference's serial loop.
+//    (= ascending cin) order by a bitwise multisplit (one ballot per bit of
+//    the bucket index), so the output order is exactly the reference's
+//    serial loop.
 // Two output layouts share the code:
 //  * REF  - buckets are Delta-wide chunks, events (cin, raw t): bit-exact
 //           reference layout (off[col*(NC+1)+c], cin/tin[col*C_in+pos]);
@@ -96,7 +97,10 @@ __global__ __launch_bounds__(256) void k_bucketize(
     }
     wave_sync();
 
-    // pass 2: stable scatter
+    // pass 2: stable scatter; a lane's rank in its bucket is the number of
+    // lower lanes of its column with the same bucket (multisplit over the
+    // ceil(log2 nb) bits of the bucket index), so one pass per chunk
+    const int nbits = nb > 1 ? 32 - __clz(nb - 1) : 0;
     for (int base = 0; base < c_in; base += seg_size) {
         const int i = base + l;
         float t = 0.0f;
@@ -106,33 +110,29 @@ __global__ __launch_bounds__(256) void k_bucketize(
             tb = arrival_bin(t, p.tfs, p.T);
         }
         const int b = (tb < 0) ? -1 : (BINS ? tb : tb / p.delta);
-        bool active = b >= 0;
-        while (true) {
-            const uint64_t act = __ballot(active);
-            if (act == 0) break;
-            const int first = __ffsll((unsigned long long)act) - 1;
-            const int bsel = __shfl(b, first, 64);
-            const bool mine = active && (b == bsel);
-            const uint64_t ms = __ballot(mine) & segmask;
-            int pos = 0;
-            if (mine) {
-                pos = cur[seg * OS + bsel] + __popcll(ms & lt);
-                const int64_t dst = col * (int64_t)c_in + pos;
-                if (BINS) {
-                    vd_event e;
-                    e.key = (uint32_t)i | ((uint32_t)tb << 24);
-                    e.alpha = alpha[alpha_index(t, tb, p.alpha_by_time, p.T)];
-                    out_ev[dst] = e;
-                } else {
-                    out_cin[dst] = i;
-                    out_tin[dst] = t;
-                }
-            }
-            wave_sync();
-            if (mine && (ms & lt) == 0) cur[seg * OS + bsel] += __popcll(ms);
-            wave_sync();
-            active = active && !mine;
+        const bool active = b >= 0;
+        // lanes of this column in the same bucket: AND of per-bit ballots
+        uint64_t same = __ballot(active) & segmask;
+        for (int k = 0; k < nbits; ++k) {
+            const uint64_t ones = __ballot(active && ((b >> k) & 1));
+            same &= ((b >> k) & 1) ? ones : ~ones;
         }
+        if (active) {
+            const int pos = cur[seg * OS + b] + __popcll(same & lt);
+            const int64_t dst = col * (int64_t)c_in + pos;
+            if (BINS) {
+                vd_event e;
+                e.key = (uint32_t)i | ((uint32_t)tb << 24);
+                e.alpha = alpha[alpha_index(t, tb, p.alpha_by_time, p.T)];
+                out_ev[dst] = e;
+            } else {
+                out_cin[dst] = i;
+                out_tin[dst] = t;
+            }
+        }
+        wave_sync();
+        if (active && (same & lt) == 0) cur[seg * OS + b] += __popcll(same);
+        wave_sync();
     }
 }
 
