@@ -182,6 +182,35 @@ def test_culif_engine_small(gpu_ctx_factory):
     np.testing.assert_array_equal(pred, rpred)
 
 
+def test_culif_engine_narrow_convs(gpu_ctx_factory):
+    """Conv layers with C_out <= 64 build their merged lists in LDS inside the
+    integrating kernel (one wave per pixel); every layer against the oracle,
+    and bit-identical across chunk widths."""
+    say("culif engine with C_out <= 64 convs (lists in LDS) vs oracle")
+    H, W, F = 24, 20, 48 * 12 * 10
+    k = models.kaiming
+    L = [vdttfs.CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, H, W, 32, k(7, 0, (32, 2, 3, 3), 18), None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 32, H, W, 60, k(7, 1, (60, 32, 3, 3), 288), None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 60, H, W, 48, k(7, 2, (48, 60, 3, 3), 540), None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_POOL, 48, H, W, 48, None, None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_FC, F, 1, 1, 11, k(7, 3, (11, F), F), None, 0.5, 1.0)]
+    w = models.CulifWorkload("narrow", vdttfs.task3_consts(T=64, delta=32), L, (2, H, W), 11, 7,
+                             meta={"decay": 0.5, "th": 1.0, "density": 0.05, "sigma_px": 6.0,
+                                   "vmax_px_per_step": 0.5})
+    B = 3
+    ev = models.dvs_events(w, B)
+    outs, pred = run_engine(gpu_ctx_factory(w.consts), w, B, ev)
+    ref, rpred = oracle.culif_net_forward(w.layers, ev, B, 64, 32)
+    for i, (g, o) in enumerate(zip(outs, ref)):
+        o = o.reshape(g.shape)
+        assert np.any(o < INF), f"layer {i} silent"
+        assert np.array_equal(g, o), f"layer {i} differs at {np.flatnonzero(g != o)[:8]}"
+    np.testing.assert_array_equal(pred, rpred)
+    outs16, _ = run_engine(gpu_ctx_factory(vdttfs.task3_consts(T=64, delta=16)), w, B, ev)
+    for a, b in zip(outs16, outs):
+        assert np.array_equal(a, b)
+
+
 def test_culif_config4_full(gpu_ctx_factory):
     """Config 4 at full size (2x128x128, T=64, B=64): samples 0-1 equal the
     oracle at every layer; Delta in {16, 64} gives bit-identical maps."""

@@ -102,6 +102,10 @@ LAYER_CASES = [
     ("t2-conv-c100-epi2", 64, 32.0, 8, True, False, 2, 5, 6, 48, 100, 3),
     ("t2-conv-c66-vec1", 64, 32.0, 8, True, False, 2, 5, 5, 20, 66, 3),
     ("t1-fc-300-84-epi2", 64, 0.0, 16, False, True, 33, 1, 1, 300, 84, 1),
+    # C_in <= 64, <= 9 taps, C_out <= 64, T <= 64: merged list built in LDS by
+    # the integrating kernel (Task 1 alpha-by-bin, valid conv; Task 2 same conv)
+    ("t1-conv3x3-lds-list", 64, 0.0, 16, False, False, 3, 11, 9, 48, 40, 3),
+    ("t2-conv3x3-lds-list-c3", 64, 32.0, 8, True, False, 4, 12, 10, 3, 64, 3),
 ]
 
 

@@ -205,17 +205,16 @@ struct DenseMergeArgs {
 
 constexpr int kDenseMaxBins = 256;
 constexpr int kDenseMaxCin = 64;
+constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 
-template <int KMAX>
-__global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs a) {
-    __shared__ int cur_all[kMergeWaves][kDenseMaxBins];
-    __shared__ int kinfo_all[kMergeWaves][2 * KMAX];
+// Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
+// tail zeroed) and its T+1 bin starts into `bs`, and returns the list length.
+// `cur` (T ints) and `kinfo` (2 * KMAX ints) are the wave's LDS scratch.  The
+// outputs are HBM (k_merge_dense) or the wave's LDS (k_stream_dense).
+template <int KMAX, class ListPtr, class BinPtr>
+__device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo,
+                                           ListPtr out, BinPtr bs) {
     const int lane = lane_id();
-    const int wave = uniform(threadIdx.x >> 6);
-    const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
-    if (pix >= a.n_pix) return;  // uniform per wave
-    int* cur = cur_all[wave];
-    int* kinfo = kinfo_all[wave];
     const int w_out = (int)(pix % a.W_out);
     const int64_t q = pix / a.W_out;
     const int h_out = (int)(q % a.H_out);
@@ -236,7 +235,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
         if (v) {
             const int slot = __popcll(m & lanemask_lt());
             kinfo[slot] = col;
-            kinfo[KMAX + slot] = lane * a.C_in * a.rowbytes;
+            kinfo[KMAX + slot] = lane * a.C_in;  // first weight row of the tap
         }
     }
     for (int t = lane; t < a.T; t += 64) cur[t] = 0;
@@ -244,23 +243,22 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
     const int nel = nk * a.C_in;  // <= KMAX * 64
     // element f of the pixel: tap k = f / C_in (the quotient's fractional
     // part is >= 0.5 / 64, so the float product rounds it correctly), cin c
-    auto element = [&](int f, float& x, int& rowb) {
+    auto element = [&](int f, float& x, int& row) {
         const int k = (int)(((float)f + 0.5f) * a.inv_cin);
         const int c = f - k * a.C_in;
         x = a.in[(int64_t)kinfo[k] * a.C_in + c];
-        rowb = kinfo[KMAX + k] + c * a.rowbytes;
+        row = kinfo[KMAX + k] + c;
     };
     // pass 1: events per bin
     for (int f0 = 0; f0 < nel; f0 += 64) {
         float x = kInfTime;
-        int rowb = 0;
-        if (f0 + lane < nel) element(f0 + lane, x, rowb);
+        int row = 0;
+        if (f0 + lane < nel) element(f0 + lane, x, row);
         const int b = arrival_bin(x, a.tfs, a.T);
         if (b >= 0) atomicAdd(&cur[b], 1);
     }
     wave_sync();
     // bin starts: lane l scans bins 4l .. 4l+3
-    int32_t* bs = a.bstart + pix * (int64_t)(a.T + 1);
     int v4[4], sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -283,12 +281,11 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
     if (lane == 0) bs[a.T] = total;
     wave_sync();
     // pass 2: stable placement, chunk by chunk in (kh, kw, cin) order
-    int2* out = a.list + pix * a.cap;
     const uint64_t lt = lanemask_lt();
     for (int f0 = 0; f0 < nel; f0 += 64) {
         float x = kInfTime;
-        int rowb = 0;
-        if (f0 + lane < nel) element(f0 + lane, x, rowb);
+        int row = 0;
+        if (f0 + lane < nel) element(f0 + lane, x, row);
         const int b = arrival_bin(x, a.tfs, a.T);
         const bool valid = b >= 0;
         uint64_t m = __ballot(valid);
@@ -301,7 +298,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
         if (valid) {
             const int pos = cur[b] + __popcll(m & lt);
             const float al = a.alpha[alpha_index(x, b, a.alpha_by_time, a.T)];
-            out[pos] = make_int2(rowb, __float_as_int(al));
+            out[pos] = make_int2(row * a.rowbytes, __float_as_int(al));
         }
         wave_sync();
         if (valid && (m & lt) == 0) cur[b] += __popcll(m);
@@ -309,6 +306,18 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
     }
     // zeroed tail: the stream kernel reads whole groups of 8 entries
     for (int i = lane; i < kListPad; i += 64) out[total + i] = make_int2(0, 0);
+    return total;
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs a) {
+    __shared__ int cur_all[kMergeWaves][kDenseMaxBins];
+    __shared__ int kinfo_all[kMergeWaves][2 * KMAX];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
+    if (pix >= a.n_pix) return;  // uniform per wave
+    (void)dense_build<KMAX>(a, pix, cur_all[wave], kinfo_all[wave], a.list + pix * a.cap,
+                            a.bstart + pix * (int64_t)(a.T + 1));
 }
 
 // ---------------------------------------------------------------------------
@@ -449,8 +458,8 @@ struct PairGather {
 struct ScalarList {
     const int2* L;
     Group8 ahead;
-    __device__ __forceinline__ void start(const int2* L_, int j, int64_t) {
-        L = L_;
+    __device__ __forceinline__ void start(const void* L_, int j, const StreamArgs&) {
+        L = static_cast<const int2*>(L_);
         ahead = *reinterpret_cast<const Group8*>(L + j);
     }
     __device__ __forceinline__ Group8 take(int j) {
@@ -468,8 +477,8 @@ struct ScalarList {
 // carry alpha = 1, so fma(w, 1, acc) is exactly the reference's acc + w.
 template <bool COUNT, bool CULIF, class G, class LR = ScalarList, int VEC = G::OWN>
 __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
-                                             const int2* __restrict__ list,
-                                             const int32_t* __restrict__ bstart,
+                                             const void* __restrict__ L,
+                                             const int32_t* __restrict__ BS,
                                              const float* __restrict__ theta, int64_t pix, int cb,
                                              const G& gather_w, unsigned long long& cnt_proc,
                                              unsigned long long& cnt_bin) {
@@ -478,8 +487,6 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
     bool ok[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) ok[v] = c0 + v < a.C_out;
-    const int2* __restrict__ L = list + pix * a.cap;
-    const int32_t* __restrict__ BS = bstart + pix * (int64_t)(a.T + 1);
 
     float carry[VEC], cur[VEC], res[VEC];  // carry: membrane (V for CuLIF); cur: CuLIF current I
     bool alive[VEC];
@@ -556,7 +563,7 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
         // groups of 8 (row, alpha) pairs, read one group (chunk) ahead
         LR lr;
-        lr.start(L, j, a.cap);
+        lr.start(L, j, a);
         while (j < blk_end) {
             const int n = (blk_end - j) < 8 ? (blk_end - j) : 8;
             const Group8 grp = lr.take(j);
@@ -621,8 +628,38 @@ stream_done:
         if (ok[v]) out[pix * a.C_out + c0 + v] = res[v];
 }
 
-// EPI = events per load: 1 (GlobalGather<VEC>) or 2 (PairGather, VEC = 2,
-// one c_out block).
+// One (pixel, c_out block) with the gather type of EPI = events per load:
+// 1 (GlobalGather<VEC>) or 2 (PairGather, VEC = 2, one c_out block).  L and BS
+// are the pixel's merged list and bin starts; LR reads the list.
+template <bool COUNT, int VEC, bool CULIF, int EPI, class LR>
+__device__ __forceinline__ void stream_one(const StreamArgs& a, float* __restrict__ out,
+                                           const void* __restrict__ L, const int32_t* __restrict__ BS,
+                                           const float* __restrict__ theta, int64_t pix, int cb) {
+    const int lane = lane_id();
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    unsigned long long cnt_proc = 0, cnt_bin = 0;
+    if constexpr (EPI == 1) {
+        GlobalGather<VEC> g;
+        g.r = rsrc;
+        const int c0 = GlobalGather<VEC>::c0(cb, lane);
+        g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
+        stream_pixel<COUNT, CULIF, GlobalGather<VEC>, LR>(a, out, L, BS, theta, pix, cb, g, cnt_proc,
+                                                          cnt_bin);
+    } else {
+        static_assert(VEC == 2 && EPI == 2, "PairGather owns 2 c_out per lane");
+        PairGather g;
+        g.r = rsrc;
+        g.lane_off = 16 * (lane & 31);
+        g.h = lane >> 5;
+        stream_pixel<COUNT, CULIF, PairGather, LR>(a, out, L, BS, theta, pix, cb, g, cnt_proc, cnt_bin);
+    }
+    if (COUNT && lane == 0) {
+        atomicAdd(&a.counters[0], cnt_proc);
+        atomicAdd(&a.counters[1], cnt_bin);
+    }
+}
+
 template <bool COUNT, int VEC, bool CULIF, int EPI>
 __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict__ out,
                                                 const int2* __restrict__ list,
@@ -634,30 +671,79 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     map_block(a.n_cblk, cb, pg);
     const int64_t pix = pg * 4 + wave;
     if (pix >= a.n_pix) return;  // uniform per wave
-    const int lane = lane_id();
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
-    unsigned long long cnt_proc = 0, cnt_bin = 0;
-    if constexpr (EPI == 1) {
-        GlobalGather<VEC> g;
-        g.r = rsrc;
-        const int c0 = GlobalGather<VEC>::c0(cb, lane);
-        g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
-        stream_pixel<COUNT, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
-    } else {
-        static_assert(VEC == 2 && EPI == 2, "PairGather owns 2 c_out per lane");
-        PairGather g;
-        g.r = rsrc;
-        g.lane_off = 16 * (lane & 31);
-        g.h = lane >> 5;
-        stream_pixel<COUNT, CULIF>(a, out, list, bstart, theta, pix, cb, g, cnt_proc, cnt_bin);
-    }
-    if (COUNT && lane_id() == 0) {
-        atomicAdd(&a.counters[0], cnt_proc);
-        atomicAdd(&a.counters[1], cnt_bin);
-    }
+    stream_one<COUNT, VEC, CULIF, EPI, ScalarList>(a, out, list + pix * a.cap,
+                                                   bstart + pix * (int64_t)(a.T + 1), theta, pix, cb);
 }
 
+// ---------------------------------------------------------------------------
+// k_stream_dense: k_merge_dense and k_stream fused for layers whose pixel is
+// one wave of dword gathers (C_out <= 64) and T <= 64.  Each wave builds its
+// pixel's merged list and bin starts in its own LDS region, then streams the
+// list from there, so the list never reaches HBM.  The list is read 64
+// entries per LDS load (lane i holds entry base + i) with the next 64
+// prefetched; v_readlane turns a group's 8 entries into the wave-uniform
+// SGPRs that the gathers and fmas take.  Groups start at multiples of 8 (one
+// bin block), so a group never straddles two windows.
+// Measured on VGG-16 B=256: L0 (3->64) 659 us against 716 us for the two
+// kernels, L1 (64->64) 1958 against 1981.  With two events per load
+// (64 < C_out <= 128) it lost (848 against 734 us at L2), and 4-byte packed
+// entries (alpha by LUT index) lost on every layer, so neither is used.
+struct LdsList {
+    const int2* L;
+    int base;
+    int2 w0, w1;  // entries base + lane and base + 64 + lane
+    __device__ __forceinline__ void start(const void* L_, int j, const StreamArgs&) {
+        L = static_cast<const int2*>(L_);
+        base = j;
+        const int lane = lane_id();
+        w0 = L[base + lane];
+        w1 = L[base + 64 + lane];
+    }
+    __device__ __forceinline__ Group8 take(int j) {
+        if (j - base >= 64) {  // uniform
+            base += 64;
+            w0 = w1;
+            w1 = L[base + 64 + lane_id()];
+        }
+        const int k = j - base;
+        Group8 g;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            g.v[i].x = __builtin_amdgcn_readlane(w0.x, k + i);
+            g.v[i].y = __builtin_amdgcn_readlane(w0.y, k + i);
+        }
+        return g;
+    }
+};
+
+// LDS words of one wave's region: the list (rounded up to whole 64-entry
+// windows plus the prefetched one), T + 1 bin starts, T cursors, the tap
+// table; a multiple of 4 so every region stays 16-byte aligned.
+__host__ __device__ inline int fused_list_entries(int nel_max) {
+    return ((nel_max + kListPad + 63) / 64) * 64 + 64;
+}
+__host__ __device__ inline int fused_wave_words(int nel_max, int T) {
+    const int w = 2 * fused_list_entries(nel_max) + (T + 1) + T + 2 * 9;
+    return (w + 3) & ~3;
+}
+
+template <bool COUNT, int VEC, bool CULIF, int EPI>
+__global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamArgs a,
+                                                      float* __restrict__ out,
+                                                      const float* __restrict__ theta, int nel_max) {
+    extern __shared__ int lds_words[];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t pix = (int64_t)blockIdx.x * 4 + wave;
+    if (pix >= a.n_pix) return;  // uniform per wave
+    int* region = lds_words + wave * fused_wave_words(nel_max, a.T);
+    int2* L = reinterpret_cast<int2*>(region);
+    int* bs = region + 2 * fused_list_entries(nel_max);
+    int* cur = bs + a.T + 1;
+    int* kinfo = cur + a.T;
+    (void)dense_build<9>(m, pix, cur, kinfo, L, bs);
+    wave_sync();
+    stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
+}
 
 // ---------------------------------------------------------------------------
 struct GenArgs {
@@ -908,10 +994,15 @@ int64_t n_pixels(const IntegShape& sh) {
     return (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
 }
 
-int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
-                  const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
-                  const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
-    const int64_t n_pix = n_pixels(sh);
+// Gather mode of a layer: vec c_out per lane, epi events per load.
+//  64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (PairGather);
+//  wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block.
+//  C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
+//  events per load there, as lanes whose neurons fired skip their loads.
+StreamArgs stream_args(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
+                       const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
+                       const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif,
+                       int* vec, int* epi) {
     StreamArgs a{};
     a.out = out;
     a.list = list;
@@ -920,7 +1011,7 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
     a.bias = bias;
     a.theta = theta;
     a.counters = counters;
-    a.n_pix = n_pix;
+    a.n_pix = n_pixels(sh);
     a.cap = cap;
     a.T = ctx->c.T;
     a.D = ctx->c.delta;
@@ -928,19 +1019,26 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
     a.C_out = sh.C_out;
     a.decay = culif ? culif->decay : 0.0f;
     a.th = culif ? culif->th : 0.0f;
-    // 64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (PairGather);
-    // wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block.
-    // C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
-    // events per load there, as lanes whose neurons fired skip their loads
-    int vec = 1, epi = 1;
+    *vec = 1;
+    *epi = 1;
     if (sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 128) {
-        epi = 2;
-        vec = 2;
+        *epi = 2;
+        *vec = 2;
     } else if (sh.C_out % 4 == 0 && sh.C_out > 128) {
-        vec = 4;
+        *vec = 4;
     }
-    a.n_cblk = epi > 1 ? 1 : (sh.C_out + 64 * vec - 1) / (64 * vec);
+    a.n_cblk = *epi > 1 ? 1 : (sh.C_out + 64 * *vec - 1) / (64 * *vec);
     a.w_bytes = (int)wbytes;
+    return a;
+}
+
+int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
+                  const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
+                  const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
+    int vec, epi;
+    const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
+                                     counters, culif, &vec, &epi);
+    const int64_t n_pix = a.n_pix;
     const int waves = 4;
     const int64_t n_pg = (n_pix + waves - 1) / waves;
     const int64_t blocks = n_pg * a.n_cblk;
@@ -1070,6 +1168,31 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.inv_cin = 1.0f / (float)sh.C_in;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    int vec, epi;
+    const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
+                                     counters, culif, &vec, &epi);
+    const int nel_max = nk_max * sh.C_in;
+    const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
+    if (vec == 1 && epi == 1 && a.n_cblk == 1 && m.T <= kBlockBins && lds <= kFusedMaxLds) {
+        // C_out <= 64: build the list in LDS and stream it there
+#define VD_LAUNCH_FUSED(C, L)                                                                      \
+    hipLaunchKernelGGL((k_stream_dense<C, 1, L, 1>), dim3((unsigned)mblocks), dim3(64 * kMergeWaves), \
+                       lds, ctx->stream, m, a, out, theta, nel_max)
+        if (culif) {
+            if (counters)
+                VD_LAUNCH_FUSED(true, true);
+            else
+                VD_LAUNCH_FUSED(false, true);
+        } else {
+            if (counters)
+                VD_LAUNCH_FUSED(true, false);
+            else
+                VD_LAUNCH_FUSED(false, false);
+        }
+#undef VD_LAUNCH_FUSED
+        VD_HIP(hipGetLastError());
+        return VDTTFS_OK;
+    }
     hipLaunchKernelGGL(k_merge_dense<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
     VD_HIP(hipGetLastError());
     return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
