@@ -243,6 +243,29 @@ def test_launch_layer_sync_matches_oracle(gpu_ctx_factory):
     np.testing.assert_array_equal(d_out.download(), exp)
 
 
+@pytest.mark.parametrize("B,C_in,C_out", [(3, 100, 70), (256, 512, 10), (5, 2000, 9), (2, 9000, 3), (4, 64, 1)])
+def test_fc_vmem_shapes(gpu_ctx_factory, B, C_in, C_out):
+    """The wave-per-image kernel (C_in <= 2048, C_out in lane blocks of 64,
+    ragged tails, weights staged in LDS up to 6144 per block and read from
+    global memory beyond: 2000 x 9) and the thread-per-output kernel (wider
+    inputs) run the reference's fma chain in cin order: equal to the oracle
+    bit for bit."""
+    say(f"fc_vmem B={B} C_in={C_in} C_out={C_out}")
+    rng = np.random.default_rng(C_in + C_out)
+    tc = consts(64, 32.0, 8, True)
+    ctx = gpu_ctx_factory(tc)
+    xs = np.where(rng.random(B * C_in) < 0.6, rng.integers(0, 100, B * C_in), 9999).astype(np.float32)
+    xs[:3] = [-0.5, 96.0, 97.0]  # clamped to alpha[0]; t - TFS = T is kept; T + 1 is dropped
+    Wt = rng.standard_normal(C_in * C_out).astype(np.float32)
+    bias = rng.standard_normal(C_out).astype(np.float32)
+    alpha, _ = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_v = ctx.empty(B * C_out)
+    ctx.fc_vmem(ctx.to_device(xs), d_v, ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha),
+                B, C_in, C_out)
+    exp = oracle.fc_vmem(oracle.Consts.from_task(tc), xs, Wt, bias, alpha, B, C_in, C_out)
+    np.testing.assert_array_equal(d_v.download(), exp)
+
+
 def test_pool_vmem_readout_encode(gpu_ctx_factory):
     say("pool / vmem / readout / encoders")
     rng = np.random.default_rng(8)

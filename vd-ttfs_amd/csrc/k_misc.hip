@@ -71,7 +71,113 @@ __global__ void k_pool_min(const float* __restrict__ in, float* __restrict__ out
     }
 }
 
-// T2V:172-190: acc over inputs in cin order, then + bias.
+// T2V:172-190 with one wave per image, four images per block.  Each wave
+// first turns its image's spike times into alpha factors in LDS (one validity
+// bit per input); the block stages the weights of a 64-wide output block in
+// LDS with all its loads in flight; then each lane (an output) runs the fma
+// chain over the inputs in cin order, skipping invalid inputs exactly as the
+// reference does.  Weight tables beyond the stage are read from global
+// memory, eight loads ahead of the fmas.
+constexpr int kVmemImgs = 4;
+constexpr int kVmemMaxCin = 2048;
+constexpr int kVmemStage = 6144;
+
+__global__ __launch_bounds__(64 * kVmemImgs) void k_fc_vmem_wave(
+    const float* __restrict__ in, float* __restrict__ out, const float* __restrict__ W,
+    const float* __restrict__ bias, const float* __restrict__ alpha, int B, int C_in, int C_out, int T,
+    float tfs) {
+    __shared__ float fac_all[kVmemImgs][kVmemMaxCin];
+    __shared__ uint64_t valid_all[kVmemImgs][kVmemMaxCin / 64];
+    __shared__ float wst[kVmemStage];
+    __shared__ float alpha_s[256];  // T + 1 <= 256 entries
+    const int wave = uniform(threadIdx.x >> 6);
+    const int lane = lane_id();
+    const int img = blockIdx.x * kVmemImgs + wave;
+    const bool have = img < B;  // uniform per wave
+    float* fac = fac_all[wave];
+    uint64_t* valid = valid_all[wave];
+    for (int t = threadIdx.x; t <= T; t += 64 * kVmemImgs) alpha_s[t] = alpha[t];
+    __syncthreads();
+    if (have) {
+        const float* src = in + (int64_t)img * C_in;
+        for (int i0 = 0; i0 < C_in; i0 += 64 * 8) {
+            float tv[8];  // eight chunks of spike times in flight
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const int i = i0 + 64 * g + lane;
+                tv[g] = i < C_in ? src[i] : kInfTime;
+            }
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const int i = i0 + 64 * g + lane;
+                const bool ok = tv[g] < kInfTime && (tv[g] - tfs) <= (float)T;
+                int ti = ok ? (int)tv[g] : 0;
+                ti = ti < 0 ? 0 : (ti > T ? T : ti);
+                const uint64_t m = __ballot(ok);
+                if (i < C_in) fac[i] = ok ? alpha_s[ti] : 0.0f;
+                if (lane == 0 && i0 + 64 * g < C_in) valid[(i0 >> 6) + g] = m;
+            }
+        }
+    }
+    for (int c0 = 0; c0 < C_out; c0 += 64) {
+        const int ncol = (C_out - c0) < 64 ? (C_out - c0) : 64;
+        const bool staged = C_in * ncol <= kVmemStage;
+        __syncthreads();  // the previous block's readers are done with wst
+        if (staged) {
+            const int total = C_in * ncol;
+            for (int f0 = 0; f0 < total; f0 += 64 * kVmemImgs * 8) {
+                float v[8];
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const int f = f0 + g * 64 * kVmemImgs + (int)threadIdx.x;
+                    const int r = f / ncol;
+                    v[g] = f < total ? W[(int64_t)r * C_out + c0 + (f - r * ncol)] : 0.0f;
+                }
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const int f = f0 + g * 64 * kVmemImgs + (int)threadIdx.x;
+                    if (f < total) wst[f] = v[g];
+                }
+            }
+        }
+        __syncthreads();
+        if (!have) continue;
+        const bool on = lane < ncol;
+        const int lc = on ? lane : 0;
+        const float* wc = W + c0 + lc;
+        float acc = 0.0f;
+        // the fma chain in cin order; `wload(i)` is this lane's weight of input i
+        auto chain = [&](auto&& wload) {
+            for (int i0 = 0; i0 < C_in; i0 += 64) {
+                const uint64_t mv = valid[i0 >> 6];
+                const uint64_t m = ((uint64_t)(uint32_t)uniform((int)(mv >> 32)) << 32) |
+                                   (uint32_t)uniform((int)(uint32_t)mv);
+                const int n = (C_in - i0) < 64 ? (C_in - i0) : 64;
+                for (int j0 = 0; j0 < n; j0 += 8) {
+                    float w[8], f[8];
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        const int i = i0 + j0 + g;
+                        const int ic = i < C_in ? i : C_in - 1;
+                        w[g] = wload(ic);
+                        f[g] = fac[ic];
+                    }
+#pragma unroll
+                    for (int g = 0; g < 8; ++g)
+                        if ((m >> (j0 + g)) & 1) acc = __builtin_fmaf(w[g], f[g], acc);
+                }
+            }
+        };
+        if (staged)
+            chain([&](int i) { return wst[i * ncol + lc]; });
+        else
+            chain([&](int i) { return wc[(int64_t)i * C_out]; });
+        if (on) out[(int64_t)img * C_out + c0 + lane] = acc + bias[c0 + lane];
+    }
+}
+
+// T2V:172-190: acc over inputs in cin order, then + bias (one thread per
+// output; inputs wider than the wave kernel's LDS table).
 __global__ void k_fc_vmem(const float* __restrict__ in, float* __restrict__ out,
                           const float* __restrict__ W, const float* __restrict__ bias,
                           const float* __restrict__ alpha, int B, int C_in, int C_out, int T,
@@ -160,8 +266,13 @@ int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W,
                    const float* alpha, int B, int C_in, int C_out) {
     const int64_t n = (int64_t)B * C_out;
     if (n <= 0) return VDTTFS_OK;
-    hipLaunchKernelGGL(k_fc_vmem, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, in, out, W,
-                       bias, alpha, B, C_in, C_out, ctx->c.T, ctx->c.tfs);
+    if (C_in <= kVmemMaxCin && C_in > 0)
+        hipLaunchKernelGGL(k_fc_vmem_wave, dim3((unsigned)((B + kVmemImgs - 1) / kVmemImgs)),
+                           dim3(64 * kVmemImgs), 0, ctx->stream, in, out, W, bias, alpha, B, C_in, C_out,
+                           ctx->c.T, ctx->c.tfs);
+    else
+        hipLaunchKernelGGL(k_fc_vmem, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, in, out, W,
+                           bias, alpha, B, C_in, C_out, ctx->c.T, ctx->c.tfs);
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }
