@@ -211,6 +211,35 @@ def test_culif_engine_narrow_convs(gpu_ctx_factory):
         assert np.array_equal(a, b)
 
 
+def test_culif_engine_conv1_inputs_and_weights(gpu_ctx_factory):
+    """The engine's conv1 integrates from masks of nonzero steps when every
+    weight is finite: inputs other than 1.0 (read back under the site's
+    flag), -0.0 (skipped like 0) and T > 64 (two step blocks) match the
+    oracle; an infinite weight keeps the dense kernel (inf * 0 = NaN)."""
+    for T, delta in ((64, 32), (96, 32)):
+        w = models.culif7(H=24, W=24, T=T, delta=delta)
+        B = 2
+        ev = models.dvs_events(w, B)
+        rng = np.random.default_rng(40 + T)
+        vals = np.array([0.5, 2.0, -1.0, -0.0, 1.0], np.float32)
+        pick = rng.random(ev.shape) < 0.3
+        ev = np.where((ev != 0) & pick, vals[rng.integers(0, vals.size, ev.shape)], ev).astype(np.float32)
+        ev[1] = np.where(ev[1] != 0, 1.0, 0.0)  # sample 1 stays binary
+        layers = list(w.layers)
+        for inf_w in (False, True):
+            say(f"culif engine conv1 T={T} non-binary inputs, inf weight={inf_w}")
+            if inf_w:
+                W0 = layers[0].weight.copy()
+                W0[5, 1, 2, 0] = np.inf
+                layers[0] = vdttfs.CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, 24, 24, 64, W0, None, 0.5, 1.0)
+            ww = models.CulifWorkload("conv1-check", w.consts, layers, w.in_shape, w.n_classes, w.seed, w.meta)
+            outs, _ = run_engine(gpu_ctx_factory(w.consts), ww, B, ev)
+            ref, _ = oracle.culif_net_forward(ww.layers, ev, B, T, delta)
+            g, o = outs[0], ref[0].reshape(outs[0].shape)
+            assert np.any(o < INF) and np.any(o == INF)
+            assert np.array_equal(g, o), f"conv1 differs at {np.flatnonzero(g != o)[:8]}"
+
+
 def test_culif_config4_full(gpu_ctx_factory):
     """Config 4 at full size (2x128x128, T=64, B=64): samples 0-1 equal the
     oracle at every layer; Delta in {16, 64} gives bit-identical maps."""

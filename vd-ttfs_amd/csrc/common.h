@@ -115,6 +115,12 @@ int launch_readout(vdttfs_ctx* ctx, const float* out, int B, int C, int32_t* pre
 
 // ---- CuLIF (T3V) ----
 int check_culif_consts(const vdttfs_ctx* ctx);
+// conv1_raw from per-site masks of nonzero steps (finite weights only; mask
+// [N*C_in*H*W][ceil(T/64)] uint64, nonbin the same shape in uint32).
+bool culif_conv1_mask_ok(int C_in);
+int launch_culif_conv1_mask(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N, int C_in,
+                            int C_out, int H, int Wd, int nhwc_out, float decay, float th, uint64_t* mask,
+                            uint32_t* nonbin);
 int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
                            int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th);
 // Reference layout; site s = (n, hw), element c at (n*C + c)*HW + hw (FC: HW = 1).

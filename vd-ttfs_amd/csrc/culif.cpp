@@ -12,6 +12,7 @@
 // The recurrent FC layer's feed-forward sums are computed per (sample, step)
 // in parallel from its dense input (k_fc_currents) before the per-step
 // recurrence.
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -63,6 +64,8 @@ struct vdttfs_culif_net {
     int32_t* roff = nullptr;
     float* flat = nullptr;     // NCHW flatten of a spatial map before an FC
     float* cur = nullptr;      // FC_REC feed-forward currents [B][T][out]
+    uint64_t* raw_mask = nullptr;  // conv1_raw event masks (finite weights, C_in <= 4)
+    uint32_t* raw_nonbin = nullptr;
     bool timing = false;
     std::vector<hipEvent_t> pool;      // 2 per layer per timed forward
     size_t pool_used = 0;
@@ -84,7 +87,7 @@ void destroy_impl(vdttfs_culif_net* net) {
             if (q) (void)hipFree(q);
     for (void* q : {(void*)net->ones, (void*)net->ev, (void*)net->off, (void*)net->list,
                     (void*)net->bstart, (void*)net->rcin, (void*)net->rtin, (void*)net->roff,
-                    (void*)net->flat, (void*)net->cur})
+                    (void*)net->flat, (void*)net->cur, (void*)net->raw_mask, (void*)net->raw_nonbin})
         if (q) (void)hipFree(q);
     delete net;
 }
@@ -162,6 +165,15 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
                 l.nhwc = 1;
                 std::vector<float> w(d.weight, d.weight + (size_t)d.C_out * d.C_in * 9);
                 VD_TRY(upload(&l.W, w));
+                // integrating from event masks skips zero inputs, exact only
+                // when w * 0 == 0 for every weight
+                bool finite = true;
+                for (float v : w) finite = finite && std::isfinite(v);
+                if (finite && culif_conv1_mask_ok(d.C_in)) {
+                    const size_t units = (size_t)B * d.C_in * d.H_in * d.W_in * ((T + 63) / 64);
+                    VD_TRY(dalloc((void**)&net->raw_mask, units * sizeof(uint64_t)));
+                    VD_TRY(dalloc((void**)&net->raw_nonbin, units * sizeof(uint32_t)));
+                }
                 break;
             }
             case VDTTFS_CULIF_CONV: {
@@ -268,8 +280,12 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
         }
         switch (d.kind) {
             case VDTTFS_CULIF_RAW_CONV:
-                VD_TRY(launch_culif_conv1_raw(ctx, d_data, l.out, l.W, B, d.C_in, d.C_out, d.H_in, d.W_in,
-                                              1, d.decay, d.th));
+                if (net->raw_mask)
+                    VD_TRY(launch_culif_conv1_mask(ctx, d_data, l.out, l.W, B, d.C_in, d.C_out, d.H_in,
+                                                   d.W_in, 1, d.decay, d.th, net->raw_mask, net->raw_nonbin));
+                else
+                    VD_TRY(launch_culif_conv1_raw(ctx, d_data, l.out, l.W, B, d.C_in, d.C_out, d.H_in,
+                                                  d.W_in, 1, d.decay, d.th));
                 break;
             case VDTTFS_CULIF_CONV: {
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;

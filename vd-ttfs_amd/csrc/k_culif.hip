@@ -215,6 +215,152 @@ __global__ __launch_bounds__(256) void k_culif_conv1_lane(RawArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// conv1_raw from event masks (the engine's path when every weight is finite).
+// k_culif_event_masks reads the dense [N][C][H][W][T] input once and keeps,
+// per site and 64-step block, the mask of nonzero steps and a flag set when
+// a nonzero value is not exactly 1.0.  k_culif_conv1_mask then integrates
+// from the masks: a step's input current is the fma chain over the taps whose
+// bit is set, in the reference's (c_in, ky, kx) order, with v = 1.0 (or the
+// value itself under the flag).  Skipping the zero taps is exact for finite
+// weights: the chain starts at +0.0f and fma(w, 0, acc) = acc + (+-0) = acc
+// for every acc the chain can hold (it is never -0), so only the taps with a
+// nonzero input change it.  A non-finite weight turns w * 0 into NaN, so such
+// layers keep the dense kernels above.
+struct MaskArgs {
+    const float* data;
+    uint64_t* mask;    // [site][nblk]
+    uint32_t* nonbin;  // [site][nblk]
+    int64_t units;     // sites * nblk
+    int T, nblk;
+};
+
+constexpr int kMaskUnitsPerWave = 8;
+constexpr int kMaskMaxCin = 3;  // taps held in registers and in 32-bit step masks: C_in * 9 <= 27
+
+__global__ __launch_bounds__(256) void k_culif_event_masks(MaskArgs a) {
+    const int lane = lane_id();
+    const int64_t u0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kMaskUnitsPerWave;
+    if (u0 >= a.units) return;  // uniform per wave
+    float v[kMaskUnitsPerWave];
+#pragma unroll
+    for (int q = 0; q < kMaskUnitsPerWave; ++q) {
+        const int64_t u = u0 + q;
+        const int64_t site = u / a.nblk;
+        const int t = (int)(u - site * a.nblk) * 64 + lane;
+        v[q] = (u < a.units && t < a.T) ? a.data[site * a.T + t] : 0.0f;
+    }
+    uint64_t my_m = 0;
+    uint32_t my_nb = 0;
+#pragma unroll
+    for (int q = 0; q < kMaskUnitsPerWave; ++q) {
+        const uint64_t m = __ballot(v[q] != 0.0f);
+        const uint64_t nb = __ballot(v[q] != 0.0f && v[q] != 1.0f);
+        if (lane == q) {
+            my_m = m;
+            my_nb = nb != 0;
+        }
+    }
+    if (lane < kMaskUnitsPerWave && u0 + lane < a.units) {
+        a.mask[u0 + lane] = my_m;
+        a.nonbin[u0 + lane] = my_nb;
+    }
+}
+
+// One wave per output pixel and 64-wide c_out block (lanes = c_out), four
+// pixels of one c_out block per workgroup; NK = C_in * 9 taps, the block's
+// weights in LDS (w_lds[k][lane]).  Per 64-step block the tap masks are
+// transposed so that lane t holds the taps with input at step t (NK <= 32
+// bits); a step with input then visits only its set taps, in ascending k,
+// one LDS read and one add each (fma(w, 1, in) is exactly in + w).  All T
+// steps run the neuron update (a step without input still decays I and adds
+// it to V).
+template <int NK>
+__global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint64_t* __restrict__ mask,
+                                                          const uint32_t* __restrict__ nonbin, int nblk) {
+    static_assert(NK <= 32, "tap masks are 32-bit");
+    __shared__ float w_lds[NK][64];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t b = blockIdx.x;
+    const int cb = (int)(b % a.n_cblk);
+    for (int i = threadIdx.x; i < NK * 64; i += 256) {
+        const int k = i >> 6, cc = cb * 64 + (i & 63);
+        w_lds[k][i & 63] = cc < a.C_out ? a.W[(int64_t)cc * NK + k] : 0.0f;
+    }
+    __syncthreads();
+    const int pix = uniform((int)((b / a.n_cblk) * 4 + wave));  // n_pix < 2^31 (host check)
+    if (pix >= a.n_pix) return;  // uniform per wave
+    const int x = pix % a.Wd;
+    const int y = (pix / a.Wd) % a.H;
+    const int n = pix / (a.Wd * a.H);
+    const int lane = lane_id();
+    const int c = cb * 64 + lane;
+    const bool ok = c < a.C_out;
+    // site of tap k, or -1 out of bounds (skipped, as the reference does)
+    auto tap_site = [&](int k) {
+        const int ci = k / 9, iy = y + (k % 9) / 3 - 1, ix = x + k % 3 - 1;
+        return (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? ((n * a.C_in + ci) * a.H + iy) * a.Wd + ix : -1;
+    };
+    float I = 0.0f, V = 0.0f, res = kInfTime;
+    bool alive = ok;
+    for (int tb = 0; tb < nblk; ++tb) {
+        uint32_t tapm = 0;  // lane t: taps with input at step t0 + t
+        uint32_t nbm = 0;   // taps whose nonzero inputs are not all 1.0 (uniform)
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int st = tap_site(k);
+            if (st >= 0) {  // uniform
+                const uint64_t mk = mask[(int64_t)st * nblk + tb];
+                tapm |= (uint32_t)((mk >> lane) & 1ull) << k;
+                nbm |= (nonbin[(int64_t)st * nblk + tb] != 0 ? 1u : 0u) << k;
+            }
+        }
+        const uint64_t any = __ballot(tapm != 0);  // steps with input (none at t >= T)
+        const int t0 = tb * 64;
+        const int tn = (a.T - t0) < 64 ? (a.T - t0) : 64;
+        for (int t8 = 0; t8 < tn; t8 += 8) {
+            // eight steps without input while every lane's current is zero
+            // change nothing: I stays 0, V stays V (the threshold is fixed),
+            // and a lane with V >= th would have fired at the step before
+            if (((any >> t8) & 0xffull) == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) continue;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t = t8 + u;
+                float in = 0.0f;
+                if ((any >> t) & 1) {
+                    uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)tapm, t);
+                    if (tm & nbm) {
+                        // an input value other than 1.0 at this step (rare)
+                        while (tm) {
+                            const int k = __builtin_ctz(tm);
+                            tm &= tm - 1;
+                            const float v =
+                                ((nbm >> k) & 1) ? a.data[(int64_t)tap_site(k) * a.T + t0 + t] : 1.0f;
+                            in = __builtin_fmaf(w_lds[k][lane], v, in);
+                        }
+                    } else {
+                        while (tm) {
+                            const int k = __builtin_ctz(tm);
+                            tm &= tm - 1;
+                            in = __builtin_fmaf(w_lds[k][lane], 1.0f, in);
+                        }
+                    }
+                }
+                if (t < tn) {  // uniform; only a last partial block stops early
+                    I = __builtin_fmaf(I, a.decay, in);
+                    V = V + I;
+                    const bool f = alive && V >= a.th;
+                    res = f ? (float)(t0 + t) : res;
+                    alive = alive && !f;
+                }
+            }
+            if (__ballot(alive) == 0) goto done;
+        }
+    }
+done:
+    if (ok) a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+}
+
+// ---------------------------------------------------------------------------
 // Reference-layout bucketize (T3V:70-106).  Site s = (n, hw): element c at
 // (n*C + c)*HW + hw; an FC input is HW = 1, C = F.  tb = (int)t, kept if
 // 0 <= tb < T; chunks of D; events in ascending c within a chunk.
@@ -582,11 +728,10 @@ int check_culif_consts(const vdttfs_ctx* ctx) {
     return VDTTFS_OK;
 }
 
-int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
-                           int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th) {
-    VD_TRY(check_culif_consts(ctx));
-    if (N <= 0 || C_in <= 0 || C_out <= 0 || H <= 0 || Wd <= 0)
-        return set_error(VDTTFS_E_INVALID, "culif_conv1_raw: non-positive shape");
+namespace {
+
+RawArgs raw_args(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N, int C_in,
+                 int C_out, int H, int Wd, int nhwc_out, float decay, float th) {
     RawArgs a{};
     a.data = data;
     a.out = out;
@@ -611,6 +756,17 @@ int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const
     }
     a.decay = decay;
     a.th = th;
+    return a;
+}
+
+}  // namespace
+
+int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
+                           int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th) {
+    VD_TRY(check_culif_consts(ctx));
+    if (N <= 0 || C_in <= 0 || C_out <= 0 || H <= 0 || Wd <= 0)
+        return set_error(VDTTFS_E_INVALID, "culif_conv1_raw: non-positive shape");
+    const RawArgs a = raw_args(ctx, data, out, W, N, C_in, C_out, H, Wd, nhwc_out, decay, th);
     if (C_in <= kTileMaxCin) {
         const int64_t blocks = (int64_t)N * H * ((Wd + kTileX - 1) / kTileX) * a.n_cblk;
         if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_raw: grid too large");
@@ -621,6 +777,47 @@ int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const
     const int64_t blocks = ((a.n_pix + 3) / 4) * a.n_cblk;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_raw: grid too large");
     hipLaunchKernelGGL(k_culif_conv1_lane, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
+bool culif_conv1_mask_ok(int C_in) { return C_in >= 1 && C_in <= kMaskMaxCin; }
+
+int launch_culif_conv1_mask(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N, int C_in,
+                            int C_out, int H, int Wd, int nhwc_out, float decay, float th, uint64_t* mask,
+                            uint32_t* nonbin) {
+    VD_TRY(check_culif_consts(ctx));
+    if (N <= 0 || C_in <= 0 || C_out <= 0 || H <= 0 || Wd <= 0)
+        return set_error(VDTTFS_E_INVALID, "culif_conv1_mask: non-positive shape");
+    if (!culif_conv1_mask_ok(C_in))
+        return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: C_in %d > %d", C_in, kMaskMaxCin);
+    const RawArgs a = raw_args(ctx, data, out, W, N, C_in, C_out, H, Wd, nhwc_out, decay, th);
+    const int nblk = (a.T + 63) / 64;
+    const int64_t sites = (int64_t)N * C_in * H * Wd;
+    if (a.n_pix >= (INT64_C(1) << 31) || sites >= (INT64_C(1) << 31))
+        return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: more than 2^31 sites");
+    MaskArgs m{data, mask, nonbin, sites * nblk, a.T, nblk};
+    const int64_t mwaves = (m.units + kMaskUnitsPerWave - 1) / kMaskUnitsPerWave;
+    const int64_t mblocks = (mwaves + 3) / 4;
+    if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: grid too large");
+    hipLaunchKernelGGL(k_culif_event_masks, dim3((unsigned)mblocks), dim3(256), 0, ctx->stream, m);
+    VD_HIP(hipGetLastError());
+    const int64_t blocks = ((a.n_pix + 3) / 4) * a.n_cblk;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: grid too large");
+    switch (C_in) {
+        case 1:
+            hipLaunchKernelGGL(k_culif_conv1_mask<9>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a,
+                               mask, nonbin, nblk);
+            break;
+        case 2:
+            hipLaunchKernelGGL(k_culif_conv1_mask<18>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a,
+                               mask, nonbin, nblk);
+            break;
+        default:
+            hipLaunchKernelGGL(k_culif_conv1_mask<27>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a,
+                               mask, nonbin, nblk);
+            break;
+    }
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }
