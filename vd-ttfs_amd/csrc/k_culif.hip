@@ -235,6 +235,7 @@ struct MaskArgs {
 };
 
 constexpr int kMaskUnitsPerWave = 8;
+constexpr int kMaskPixPerWave = 16;  // consecutive output pixels per wave
 constexpr int kMaskMaxCin = 3;  // taps held in registers and in 32-bit step masks: C_in * 9 <= 27
 
 __global__ __launch_bounds__(256) void k_culif_event_masks(MaskArgs a) {
@@ -266,8 +267,9 @@ __global__ __launch_bounds__(256) void k_culif_event_masks(MaskArgs a) {
     }
 }
 
-// One wave per output pixel and 64-wide c_out block (lanes = c_out), four
-// pixels of one c_out block per workgroup; NK = C_in * 9 taps, the block's
+// One wave per kMaskPixPerWave consecutive output pixels and a 64-wide c_out
+// block (lanes = c_out), four waves of one c_out block per workgroup; NK =
+// C_in * 9 taps, the block's
 // weights in LDS (w_lds[k][lane]).  Per 64-step block the tap masks are
 // transposed so that lane t holds the taps with input at step t (NK <= 32
 // bits); a step with input then visits only its set taps, in ascending k,
@@ -287,77 +289,80 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
         w_lds[k][i & 63] = cc < a.C_out ? a.W[(int64_t)cc * NK + k] : 0.0f;
     }
     __syncthreads();
-    const int pix = uniform((int)((b / a.n_cblk) * 4 + wave));  // n_pix < 2^31 (host check)
-    if (pix >= a.n_pix) return;  // uniform per wave
-    const int x = pix % a.Wd;
-    const int y = (pix / a.Wd) % a.H;
-    const int n = pix / (a.Wd * a.H);
-    const int lane = lane_id();
-    const int c = cb * 64 + lane;
-    const bool ok = c < a.C_out;
-    // site of tap k, or -1 out of bounds (skipped, as the reference does)
-    auto tap_site = [&](int k) {
-        const int ci = k / 9, iy = y + (k % 9) / 3 - 1, ix = x + k % 3 - 1;
-        return (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? ((n * a.C_in + ci) * a.H + iy) * a.Wd + ix : -1;
-    };
-    float I = 0.0f, V = 0.0f, res = kInfTime;
-    bool alive = ok;
-    for (int tb = 0; tb < nblk; ++tb) {
-        uint32_t tapm = 0;  // lane t: taps with input at step t0 + t
-        uint32_t nbm = 0;   // taps whose nonzero inputs are not all 1.0 (uniform)
+    const int pix0 = uniform((int)((b / a.n_cblk) * 4 + wave)) * kMaskPixPerWave;  // < 2^31 (host check)
+    for (int pq = 0; pq < kMaskPixPerWave; ++pq) {
+        const int pix = pix0 + pq;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        const int x = pix % a.Wd;
+        const int y = (pix / a.Wd) % a.H;
+        const int n = pix / (a.Wd * a.H);
+        const int lane = lane_id();
+        const int c = cb * 64 + lane;
+        const bool ok = c < a.C_out;
+        // site of tap k, or -1 out of bounds (skipped, as the reference does)
+        auto tap_site = [&](int k) {
+            const int ci = k / 9, iy = y + (k % 9) / 3 - 1, ix = x + k % 3 - 1;
+            return (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? ((n * a.C_in + ci) * a.H + iy) * a.Wd + ix : -1;
+        };
+        float I = 0.0f, V = 0.0f, res = kInfTime;
+        bool alive = ok;
+        for (int tb = 0; tb < nblk; ++tb) {
+            uint32_t tapm = 0;  // lane t: taps with input at step t0 + t
+            uint32_t nbm = 0;   // taps whose nonzero inputs are not all 1.0 (uniform)
 #pragma unroll
-        for (int k = 0; k < NK; ++k) {
-            const int st = tap_site(k);
-            if (st >= 0) {  // uniform
-                const uint64_t mk = mask[(int64_t)st * nblk + tb];
-                tapm |= (uint32_t)((mk >> lane) & 1ull) << k;
-                nbm |= (nonbin[(int64_t)st * nblk + tb] != 0 ? 1u : 0u) << k;
+            for (int k = 0; k < NK; ++k) {
+                const int st = tap_site(k);
+                if (st >= 0) {  // uniform
+                    const uint64_t mk = mask[(int64_t)st * nblk + tb];
+                    tapm |= (uint32_t)((mk >> lane) & 1ull) << k;
+                    nbm |= (nonbin[(int64_t)st * nblk + tb] != 0 ? 1u : 0u) << k;
+                }
             }
-        }
-        const uint64_t any = __ballot(tapm != 0);  // steps with input (none at t >= T)
-        const int t0 = tb * 64;
-        const int tn = (a.T - t0) < 64 ? (a.T - t0) : 64;
-        for (int t8 = 0; t8 < tn; t8 += 8) {
-            // eight steps without input while every lane's current is zero
-            // change nothing: I stays 0, V stays V (the threshold is fixed),
-            // and a lane with V >= th would have fired at the step before
-            if (((any >> t8) & 0xffull) == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) continue;
+            const uint64_t any = __ballot(tapm != 0);  // steps with input (none at t >= T)
+            const int t0 = tb * 64;
+            const int tn = (a.T - t0) < 64 ? (a.T - t0) : 64;
+            for (int t8 = 0; t8 < tn; t8 += 8) {
+                // eight steps without input while every lane's current is zero
+                // change nothing: I stays 0, V stays V (the threshold is fixed),
+                // and a lane with V >= th would have fired at the step before
+                if (((any >> t8) & 0xffull) == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) continue;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int t = t8 + u;
-                float in = 0.0f;
-                if ((any >> t) & 1) {
-                    uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)tapm, t);
-                    if (tm & nbm) {
-                        // an input value other than 1.0 at this step (rare)
-                        while (tm) {
-                            const int k = __builtin_ctz(tm);
-                            tm &= tm - 1;
-                            const float v =
-                                ((nbm >> k) & 1) ? a.data[(int64_t)tap_site(k) * a.T + t0 + t] : 1.0f;
-                            in = __builtin_fmaf(w_lds[k][lane], v, in);
-                        }
-                    } else {
-                        while (tm) {
-                            const int k = __builtin_ctz(tm);
-                            tm &= tm - 1;
-                            in = __builtin_fmaf(w_lds[k][lane], 1.0f, in);
+                for (int u = 0; u < 8; ++u) {
+                    const int t = t8 + u;
+                    float in = 0.0f;
+                    if ((any >> t) & 1) {
+                        uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)tapm, t);
+                        if (tm & nbm) {
+                            // an input value other than 1.0 at this step (rare)
+                            while (tm) {
+                                const int k = __builtin_ctz(tm);
+                                tm &= tm - 1;
+                                const float v =
+                                    ((nbm >> k) & 1) ? a.data[(int64_t)tap_site(k) * a.T + t0 + t] : 1.0f;
+                                in = __builtin_fmaf(w_lds[k][lane], v, in);
+                            }
+                        } else {
+                            while (tm) {
+                                const int k = __builtin_ctz(tm);
+                                tm &= tm - 1;
+                                in = __builtin_fmaf(w_lds[k][lane], 1.0f, in);
+                            }
                         }
                     }
+                    if (t < tn) {  // uniform; only a last partial block stops early
+                        I = __builtin_fmaf(I, a.decay, in);
+                        V = V + I;
+                        const bool f = alive && V >= a.th;
+                        res = f ? (float)(t0 + t) : res;
+                        alive = alive && !f;
+                    }
                 }
-                if (t < tn) {  // uniform; only a last partial block stops early
-                    I = __builtin_fmaf(I, a.decay, in);
-                    V = V + I;
-                    const bool f = alive && V >= a.th;
-                    res = f ? (float)(t0 + t) : res;
-                    alive = alive && !f;
-                }
+                if (__ballot(alive) == 0) goto done;
             }
-            if (__ballot(alive) == 0) goto done;
         }
-    }
 done:
-    if (ok) a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+        if (ok) a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -802,7 +807,7 @@ int launch_culif_conv1_mask(vdttfs_ctx* ctx, const float* data, float* out, cons
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: grid too large");
     hipLaunchKernelGGL(k_culif_event_masks, dim3((unsigned)mblocks), dim3(256), 0, ctx->stream, m);
     VD_HIP(hipGetLastError());
-    const int64_t blocks = ((a.n_pix + 3) / 4) * a.n_cblk;
+    const int64_t blocks = ((a.n_pix + 4 * kMaskPixPerWave - 1) / (4 * kMaskPixPerWave)) * a.n_cblk;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: grid too large");
     switch (C_in) {
         case 1:
