@@ -340,6 +340,7 @@ struct StreamArgs {
     int64_t n_pix;
     int64_t cap;
     int T, D, t_min, C_out, n_cblk;
+    int ppw;               // consecutive output pixels per wave
     int w_bytes;
     float decay, th;  // CuLIF neuron (T3V:62-63): I = I*decay + in; V += I; fire at V >= th
 };
@@ -669,10 +670,13 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     int cb;
     int64_t pg;
     map_block(a.n_cblk, cb, pg);
-    const int64_t pix = pg * 4 + wave;
-    if (pix >= a.n_pix) return;  // uniform per wave
-    stream_one<COUNT, VEC, CULIF, EPI, ScalarList>(a, out, list + pix * a.cap,
-                                                   bstart + pix * (int64_t)(a.T + 1), theta, pix, cb);
+    const int64_t pix0 = (pg * 4 + wave) * a.ppw;
+    for (int q = 0; q < a.ppw; ++q) {
+        const int64_t pix = pix0 + q;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        stream_one<COUNT, VEC, CULIF, EPI, ScalarList>(a, out, list + pix * a.cap,
+                                                       bstart + pix * (int64_t)(a.T + 1), theta, pix, cb);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -733,16 +737,20 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
                                                       const float* __restrict__ theta, int nel_max) {
     extern __shared__ int lds_words[];
     const int wave = uniform(threadIdx.x >> 6);
-    const int64_t pix = (int64_t)blockIdx.x * 4 + wave;
-    if (pix >= a.n_pix) return;  // uniform per wave
     int* region = lds_words + wave * fused_wave_words(nel_max, a.T);
     int2* L = reinterpret_cast<int2*>(region);
     int* bs = region + 2 * fused_list_entries(nel_max);
     int* cur = bs + a.T + 1;
     int* kinfo = cur + a.T;
-    (void)dense_build<9>(m, pix, cur, kinfo, L, bs);
-    wave_sync();
-    stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
+    const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.ppw;
+    for (int q = 0; q < a.ppw; ++q) {
+        const int64_t pix = pix0 + q;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        (void)dense_build<9>(m, pix, cur, kinfo, L, bs);
+        wave_sync();
+        stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
+        wave_sync();  // this pixel's list reads precede the next pixel's build
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1029,6 +1037,11 @@ StreamArgs stream_args(vdttfs_ctx* ctx, float* out, const int2* list, int64_t ca
     }
     a.n_cblk = *epi > 1 ? 1 : (sh.C_out + 64 * *vec - 1) / (64 * *vec);
     a.w_bytes = (int)wbytes;
+    // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
+    // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
+    // (VGG-16 B=256 at 2, 4, 8 pixels per wave: 30.4K -> 29.3K, 26.0K, 20.0K
+    // images/s; the 2^18-pixel CuLIF conv3: 3.68 -> 3.88 ms)
+    a.ppw = a.n_pix >= (INT64_C(1) << 20) ? 2 : 1;
     return a;
 }
 
@@ -1040,7 +1053,7 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
                                      counters, culif, &vec, &epi);
     const int64_t n_pix = a.n_pix;
     const int waves = 4;
-    const int64_t n_pg = (n_pix + waves - 1) / waves;
+    const int64_t n_pg = (n_pix + waves * a.ppw - 1) / (waves * a.ppw);
     const int64_t blocks = n_pg * a.n_cblk;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
@@ -1175,8 +1188,9 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
     if (vec == 1 && epi == 1 && a.n_cblk == 1 && m.T <= kBlockBins && lds <= kFusedMaxLds) {
         // C_out <= 64: build the list in LDS and stream it there
+        const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
 #define VD_LAUNCH_FUSED(C, L)                                                                      \
-    hipLaunchKernelGGL((k_stream_dense<C, 1, L, 1>), dim3((unsigned)mblocks), dim3(64 * kMergeWaves), \
+    hipLaunchKernelGGL((k_stream_dense<C, 1, L, 1>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), \
                        lds, ctx->stream, m, a, out, theta, nel_max)
         if (culif) {
             if (counters)
