@@ -690,7 +690,8 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
 // bin block), so a group never straddles two windows.
 // Measured on VGG-16 B=256: L0 (3->64) 659 us against 716 us for the two
 // kernels, L1 (64->64) 1958 against 1981.  With two events per load
-// (64 < C_out <= 128) it lost (848 against 734 us at L2), and 4-byte packed
+// (64 < C_out <= 128) it lost (848 against 734 us at L2; 9.22 against 8.53 ms
+// at the 2^20-pixel CuLIF conv2), and 4-byte packed
 // entries (alpha by LUT index) lost on every layer, so neither is used.
 struct LdsList {
     const int2* L;
