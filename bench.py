@@ -218,8 +218,9 @@ def bench_culif(args) -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
-            "kernel": "conv layers (bucketize + k_merge + k_stream<CuLIF>); achieved = fused "
-                      "algorithmic bytes of the conv layers / their HIP-event time",
+            "kernel": "conv layers after conv1 (C_in <= 64: k_merge_dense + k_stream<CuLIF>; "
+                      "wider: k_bucketize + k_merge + k_stream<CuLIF>); achieved = fused "
+                      "algorithmic bytes of those layers / their HIP-event time",
             "algorithmic_bytes_per_step": b_conv,
             "conv_ms_per_step": conv_ms,
         },
@@ -438,10 +439,11 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": (tr[0] / tr[1]) if tr else None,
-            "kernel": "integrator = a layer's k_merge_dense + k_stream (conv) or k_bucketize + "
-                      "k_merge + k_stream (FC; k_integrate_generic under 32 outputs); a launch is "
-                      "one layer's integrate, achieved = fused algorithmic bytes of a step / "
-                      "integrator time of a step",
+            "kernel": "integrator = a layer's k_stream_dense (conv, C_in <= 64, C_out <= 64: "
+                      "list built in LDS), k_merge_dense + k_stream (other conv, C_in <= 64) or "
+                      "k_bucketize + k_merge + k_stream (wider conv, FC); a launch is one layer's "
+                      "integrate, achieved = fused algorithmic bytes of a step / integrator time "
+                      "of a step",
             "algorithmic_bytes_per_step": b_int,
             "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
             "traffic_per_step": tr[0] if tr else None,

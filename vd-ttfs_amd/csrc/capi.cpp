@@ -80,6 +80,21 @@ int ensure_bin_scratch(vdttfs_ctx* ctx, size_t elems, size_t cols) {
     return VDTTFS_OK;
 }
 
+int zero_counters(vdttfs_ctx* ctx) {
+    VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * kCounterStripes * sizeof(unsigned long long), ctx->stream));
+    return VDTTFS_OK;
+}
+
+int read_counters(vdttfs_ctx* ctx, unsigned long long out[4]) {
+    unsigned long long h[4 * kCounterStripes];
+    VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
+    VD_HIP(hipStreamSynchronize(ctx->stream));
+    for (int k = 0; k < 4; ++k) out[k] = 0;
+    for (int s = 0; s < kCounterStripes; ++s)
+        for (int k = 0; k < 4; ++k) out[k] += h[4 * s + k];
+    return VDTTFS_OK;
+}
+
 int ensure_merge_scratch(vdttfs_ctx* ctx, size_t list_elems, size_t bstart_elems) {
     if (list_elems > ctx->mrg_list_elems || bstart_elems > ctx->mrg_bstart_elems || !ctx->mrg_list) {
         VD_HIP(hipStreamSynchronize(ctx->stream));
@@ -145,7 +160,8 @@ int vdttfs_create(const vdttfs_consts* consts, int device, vdttfs_ctx** out) {
     ctx->OS = ctx->NC + 1;
     ctx->device = device;
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipMalloc((void**)&ctx->d_counters, 4 * sizeof(unsigned long long));
+    if (e == hipSuccess)
+        e = hipMalloc((void**)&ctx->d_counters, 4 * kCounterStripes * sizeof(unsigned long long));
     if (e != hipSuccess) {
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -349,7 +365,7 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
     const int64_t cap = merged_list_cap(s);
     VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     const bool count = eproc || ebin;
-    if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
+    if (count) VD_TRY(zero_counters(ctx));
     if (integrate_dense_ok(ctx, s)) {
         // conv: merged lists straight from the dense map
         VD_TRY(launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, (int2*)ctx->mrg_list, cap,
@@ -366,8 +382,7 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
     }
     if (count) {
         unsigned long long h[4];
-        VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
-        VD_HIP(hipStreamSynchronize(ctx->stream));
+        VD_TRY(read_counters(ctx, h));
         if (eproc) *eproc = h[0];
         if (ebin) *ebin = h[1];
     }

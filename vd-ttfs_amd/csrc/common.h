@@ -35,12 +35,25 @@ struct vdttfs_ctx {
     void* mrg_list;
     void* mrg_bstart;
     size_t mrg_list_elems, mrg_bstart_elems;
-    unsigned long long* d_counters;  // 4 x u64
+    unsigned long long* d_counters;  // kCounterStripes x 4 u64 (summed on the host)
     hipEvent_t timer[2];             // vdttfs_timer_begin/end (created on first use)
     bool timer_ready;
 };
 
 namespace vdttfs {
+
+// Work counters (E_proc, E_bin, retained events) are striped: a kernel adds
+// to counters[4 * (blockIdx.x % kCounterStripes) + k], and the host sums the
+// stripes, so a million waves do not serialise on one address.
+constexpr int kCounterStripes = 64;
+#ifdef __HIPCC__
+__device__ __forceinline__ unsigned long long* counter_stripe(unsigned long long* c) {
+    return c + 4 * (blockIdx.x % kCounterStripes);
+}
+#endif
+int zero_counters(vdttfs_ctx* ctx);
+// Waits for the stream and sums the stripes into out[0..3].
+int read_counters(vdttfs_ctx* ctx, unsigned long long out[4]);
 
 int set_error(int code, const char* fmt, ...);
 int hip_error(hipError_t e, const char* what, int line);

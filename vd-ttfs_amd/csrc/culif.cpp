@@ -271,7 +271,7 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
         if (counts)
             for (int k = 0; k < 4; ++k) counts[k][i] = 0;
         if (count_here)
-            VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
+            VD_TRY(zero_counters(ctx));
         // an FC layer reads the previous map flattened in NCHW order
         const float* fc_in = cur;
         if ((d.kind == VDTTFS_CULIF_FC || d.kind == VDTTFS_CULIF_FC_REC) && cur_nhwc && (cH > 1 || cW > 1)) {
@@ -306,8 +306,7 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
                                                  count_here ? ctx->d_counters : nullptr, &nrn));
                 if (count_here) {
                     unsigned long long h[4];
-                    VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
-                    VD_HIP(hipStreamSynchronize(ctx->stream));
+                    VD_TRY(read_counters(ctx, h));
                     counts[0][i] = h[0];
                     counts[1][i] = h[1];
                     counts[2][i] = h[2];

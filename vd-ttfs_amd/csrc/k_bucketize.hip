@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void k_bucketize(
         if (n_ev_counter != nullptr) {
             int mine = (l == 0 && col_ok) ? cur[seg * OS + nb] : 0;
             for (int off = 32; off > 0; off >>= 1) mine += __shfl_xor(mine, off, 64);
-            if (lane == 0) atomicAdd(n_ev_counter, (unsigned long long)mine);
+            if (lane == 0) atomicAdd(counter_stripe(n_ev_counter), (unsigned long long)mine);
         }
     }
     wave_sync();

@@ -656,8 +656,9 @@ __device__ __forceinline__ void stream_one(const StreamArgs& a, float* __restric
         stream_pixel<COUNT, CULIF, PairGather, LR>(a, out, L, BS, theta, pix, cb, g, cnt_proc, cnt_bin);
     }
     if (COUNT && lane == 0) {
-        atomicAdd(&a.counters[0], cnt_proc);
-        atomicAdd(&a.counters[1], cnt_bin);
+        unsigned long long* c = counter_stripe(a.counters);
+        atomicAdd(&c[0], cnt_proc);
+        atomicAdd(&c[1], cnt_bin);
     }
 }
 
@@ -873,8 +874,9 @@ __global__ __launch_bounds__(256) void k_integrate_generic(GenArgs a) {
             my_bin += __shfl_xor(my_bin, o, 64);
         }
         if (lane_id() == 0) {
-            atomicAdd(&a.counters[0], my_proc);
-            atomicAdd(&a.counters[1], my_bin);
+            unsigned long long* c = counter_stripe(a.counters);
+            atomicAdd(&c[0], my_proc);
+            atomicAdd(&c[1], my_bin);
         }
     }
 }

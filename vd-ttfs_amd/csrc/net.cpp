@@ -154,7 +154,7 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             s.K_h = fc ? 1 : d.K_h;
             s.K_w = fc ? 1 : d.K_w;
             s.pad = (fc || !ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
-            if (count) VD_HIP(hipMemsetAsync(ctx->d_counters, 0, 4 * sizeof(unsigned long long), ctx->stream));
+            if (count) VD_TRY(zero_counters(ctx));
             // conv layers build their merged lists from the dense map; the
             // bin-layout bucketize runs for FC layers, and in a counting
             // forward for its retained-event count
@@ -188,8 +188,7 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             }
             if (count) {
                 unsigned long long h[4];
-                VD_HIP(hipMemcpyAsync(h, ctx->d_counters, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
-                VD_HIP(hipStreamSynchronize(ctx->stream));
+                VD_TRY(read_counters(ctx, h));
                 if (eproc) eproc[i] = h[0];
                 if (ebin) ebin[i] = h[1];
                 if (n_ev) n_ev[i] = h[2];
