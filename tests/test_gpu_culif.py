@@ -233,11 +233,16 @@ def test_culif_engine_conv1_inputs_and_weights(gpu_ctx_factory):
                 W0[5, 1, 2, 0] = np.inf
                 layers[0] = vdttfs.CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, 24, 24, 64, W0, None, 0.5, 1.0)
             ww = models.CulifWorkload("conv1-check", w.consts, layers, w.in_shape, w.n_classes, w.seed, w.meta)
-            outs, _ = run_engine(gpu_ctx_factory(w.consts), ww, B, ev)
-            ref, _ = oracle.culif_net_forward(ww.layers, ev, B, T, delta)
+            outs, pred = run_engine(gpu_ctx_factory(w.consts), ww, B, ev)
+            ref, rpred = oracle.culif_net_forward(ww.layers, ev, B, T, delta)
             g, o = outs[0], ref[0].reshape(outs[0].shape)
             assert np.any(o < INF) and np.any(o == INF)
             assert np.array_equal(g, o), f"conv1 differs at {np.flatnonzero(g != o)[:8]}"
+            # the rest of the network too (recurrent FC over 4608 inputs: a
+            # ragged last sort segment)
+            for i in range(1, len(outs)):
+                assert np.array_equal(outs[i], ref[i].reshape(outs[i].shape)), f"layer {i} differs"
+            np.testing.assert_array_equal(pred, rpred)
 
 
 def test_culif_config4_full(gpu_ctx_factory):

@@ -151,9 +151,22 @@ int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, c
                         const float* cur, float* out, const float* W, const float* Wrec, int N,
                         int in_f, int out_f, float decay, float th);
 // cur[n][t][o] = sum over inputs j ascending arriving at step t of W_t[j][o],
-// from the dense input x[N][F] (T3V arrival rule).
-int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F,
-                       int out_f);
+// from the dense input x[N][F] (T3V arrival rule).  The inputs are first
+// sorted by step into the scratch (sizes in int32 elements from
+// fc_sort_sizes; offs has the size of counts).
+struct FcSortSizes {
+    int segments;
+    int64_t counts, binstart, list;
+};
+struct FcSortScratch {
+    int32_t* counts;
+    int32_t* offs;
+    int32_t* binstart;
+    int32_t* list;
+};
+FcSortSizes fc_sort_sizes(int N, int F, int T);
+int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F, int out_f,
+                       const FcSortScratch& sc);
 int launch_nhwc_to_nchw(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H, int W);
 
 // shape validation shared by the entry points

@@ -12,6 +12,7 @@
 // The recurrent FC layer's feed-forward sums are computed per (sample, step)
 // in parallel from its dense input (k_fc_currents) before the per-step
 // recurrence.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -64,6 +65,7 @@ struct vdttfs_culif_net {
     int32_t* roff = nullptr;
     float* flat = nullptr;     // NCHW flatten of a spatial map before an FC
     float* cur = nullptr;      // FC_REC feed-forward currents [B][T][out]
+    FcSortScratch fcs{};           // FC_REC inputs sorted by arrival step
     uint64_t* raw_mask = nullptr;  // conv1_raw event masks (finite weights, C_in <= 4)
     uint32_t* raw_nonbin = nullptr;
     bool timing = false;
@@ -87,7 +89,8 @@ void destroy_impl(vdttfs_culif_net* net) {
             if (q) (void)hipFree(q);
     for (void* q : {(void*)net->ones, (void*)net->ev, (void*)net->off, (void*)net->list,
                     (void*)net->bstart, (void*)net->rcin, (void*)net->rtin, (void*)net->roff,
-                    (void*)net->flat, (void*)net->cur, (void*)net->raw_mask, (void*)net->raw_nonbin})
+                    (void*)net->flat, (void*)net->cur, (void*)net->raw_mask, (void*)net->raw_nonbin,
+                    (void*)net->fcs.counts, (void*)net->fcs.offs, (void*)net->fcs.binstart, (void*)net->fcs.list})
         if (q) (void)hipFree(q);
     delete net;
 }
@@ -149,6 +152,7 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
     std::vector<float> ones(T + 1, 1.0f);
     VD_TRY(upload(&net->ones, ones));
     int64_t max_ev = 1, max_cols = 1, max_list = 1, max_bstart = 1, max_flat = 1, max_cur = 1;
+    int64_t max_fc_counts = 1, max_fc_binstart = 1, max_fc_list = 1;
     int64_t max_rsites = 1, max_relems = 1;
     net->L.resize(n);
     for (int i = 0; i < n; ++i) {
@@ -215,6 +219,10 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
                 VD_TRY(upload(&l.Wrec, r));
                 if ((int64_t)B * T * d.C_out > max_cur) max_cur = (int64_t)B * T * d.C_out;
                 if (spatial_in && (int64_t)B * d.C_in > max_flat) max_flat = (int64_t)B * d.C_in;
+                const FcSortSizes z = fc_sort_sizes(B, d.C_in, T);
+                max_fc_counts = std::max(max_fc_counts, z.counts);
+                max_fc_binstart = std::max(max_fc_binstart, z.binstart);
+                max_fc_list = std::max(max_fc_list, z.list);
                 break;
             }
             case VDTTFS_CULIF_FC: {
@@ -239,6 +247,10 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
     VD_TRY(dalloc((void**)&net->roff, (size_t)max_rsites * OS * 4));
     VD_TRY(dalloc((void**)&net->flat, (size_t)max_flat * 4));
     VD_TRY(dalloc((void**)&net->cur, (size_t)max_cur * 4));
+    VD_TRY(dalloc((void**)&net->fcs.counts, (size_t)max_fc_counts * 4));
+    VD_TRY(dalloc((void**)&net->fcs.offs, (size_t)max_fc_counts * 4));
+    VD_TRY(dalloc((void**)&net->fcs.binstart, (size_t)max_fc_binstart * 4));
+    VD_TRY(dalloc((void**)&net->fcs.list, (size_t)max_fc_list * 4));
     return VDTTFS_OK;
 }
 
@@ -319,7 +331,7 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
                                          d.th));
                 break;
             case VDTTFS_CULIF_FC_REC:
-                VD_TRY(launch_fc_currents(ctx, fc_in, l.W, net->cur, B, d.C_in, d.C_out));
+                VD_TRY(launch_fc_currents(ctx, fc_in, l.W, net->cur, B, d.C_in, d.C_out, net->fcs));
                 VD_TRY(launch_culif_fc_rec(ctx, nullptr, nullptr, nullptr, net->cur, l.out, nullptr, l.Wrec, B,
                                            d.C_in, d.C_out, d.decay, d.th));
                 break;

@@ -637,71 +637,166 @@ __global__ __launch_bounds__(1024) void k_culif_fc_rec(CRecArgs a) {
     if (ok) a.out[(int64_t)n * a.out_f + i] = my_fire;
 }
 
-// Engine feed-forward currents of an FC layer, straight from the dense input
-// x[N][F] (no bucketize): one wave per (sample, kFcBins arrival steps, 64
-// outputs); lanes are outputs.  The wave scans the sample's inputs in
-// ascending j, 64 at a time, ballots the inputs arriving at each of its
-// steps (T3V:78 rule) and adds their weight rows in that order, so
-//   cur[n][t][o] = sum over j ascending with step(x[n][j]) == t of W_t[j][o]
-// is summed exactly as the reference's bucket order sums it (W_t is the
-// [in][out] transpose: each term is one coalesced row segment).
-constexpr int kFcBins = 2;    // arrival steps per wave
-constexpr int kFcUnroll = 4;  // 64-input chunks loaded together
+// Engine feed-forward currents of an FC layer:
+//   cur[n][t][o] = sum over inputs j ascending with step(x[n][j]) == t of W_t[j][o]
+// (T3V:78 arrival rule; W_t is the [in][out] transpose, so each term is one
+// coalesced row segment), summed in the reference's bucket order.  The
+// inputs of each sample are first counting-sorted by arrival step, stably in
+// j, by three small kernels over segments of kFcSeg inputs (one wave each):
+//   k_fcsort_count    per-segment step histogram (LDS atomics);
+//   k_fcsort_offsets  per-sample offsets, step-major then segment order;
+//   k_fcsort_scatter  each input's j to its step's list, ranked within a
+//                     64-input chunk by a bit-ballot multisplit.
+// k_fc_currents then gives each (sample, step, 64 outputs) wave its list:
+// 32 rows gathered at a time (entries read one group ahead), added in list (= ascending j) order.  Scanning
+// every input per step group instead left each wave about one gather per
+// 64-input chunk, a memory latency each.
+constexpr int kFcSeg = 2048;    // inputs per sort segment
+constexpr int kFcGroup = 32;    // rows gathered together
+constexpr int kFcListPad = 2 * kFcGroup;  // list entries readable past the end
 
-__global__ __launch_bounds__(256) void k_fc_currents(const float* __restrict__ x,
-                                                     const float* __restrict__ W,
-                                                     float* __restrict__ cur, int N, int T, int F,
-                                                     int out_f, int n_oblk, int n_tgrp) {
+__global__ __launch_bounds__(256) void k_fcsort_count(const float* __restrict__ x, int32_t* __restrict__ counts,
+                                                      int N, int F, int T, int S) {
+    __shared__ int cnt_all[4][256];
     const int wave = uniform(threadIdx.x >> 6);
-    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t group, oblk)
-    if (u >= (int64_t)N * n_tgrp * n_oblk) return;
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, segment)
+    if (u >= (int64_t)N * S) return;                   // uniform per wave
+    const int lane = lane_id();
+    int* cnt = cnt_all[wave];
+    for (int t = lane; t < T; t += 64) cnt[t] = 0;
+    wave_sync();
+    const int64_t n = u / S;
+    const int j0 = (int)(u - n * S) * kFcSeg;
+    const int j1 = (F - j0) < kFcSeg ? F : j0 + kFcSeg;
+    const float* __restrict__ X = x + n * F;
+    for (int jb = j0; jb < j1; jb += 64 * 4) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = jb + 64 * r + lane;
+            v[r] = j < j1 ? X[j] : kInfTime;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int b = culif_bin(v[r], T);
+            if (b >= 0) atomicAdd(&cnt[b], 1);
+        }
+    }
+    wave_sync();
+    for (int t = lane; t < T; t += 64) counts[u * T + t] = cnt[t];
+}
+
+// One block per sample, thread t = step (T <= 255 < blockDim).
+__global__ __launch_bounds__(256) void k_fcsort_offsets(const int32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ offs,
+                                                        int32_t* __restrict__ binstart, int T, int S) {
+    __shared__ int base[257];
+    const int64_t n = blockIdx.x;
+    const int t = threadIdx.x;
+    const int32_t* __restrict__ C = counts + n * S * T;
+    int tot = 0;
+    if (t < T)
+        for (int s = 0; s < S; ++s) tot += C[(int64_t)s * T + t];
+    if (t < T) base[t] = tot;
+    __syncthreads();
+    if (t == 0) {
+        int run = 0;
+        for (int k = 0; k < T; ++k) {
+            const int v = base[k];
+            base[k] = run;
+            run += v;
+        }
+        base[T] = run;
+    }
+    __syncthreads();
+    if (t <= T) binstart[n * (T + 1) + t] = base[t];
+    if (t < T) {
+        int run = base[t];
+        for (int s = 0; s < S; ++s) {
+            offs[(n * S + s) * T + t] = run;
+            run += C[(int64_t)s * T + t];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fcsort_scatter(const float* __restrict__ x,
+                                                        const int32_t* __restrict__ offs,
+                                                        int32_t* __restrict__ list, int N, int F, int T,
+                                                        int S, int nbits) {
+    __shared__ int cur_all[4][256];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;
+    if (u >= (int64_t)N * S) return;  // uniform per wave
+    const int lane = lane_id();
+    int* cur = cur_all[wave];
+    for (int t = lane; t < T; t += 64) cur[t] = offs[u * T + t];
+    wave_sync();
+    const int64_t n = u / S;
+    const int j0 = (int)(u - n * S) * kFcSeg;
+    const int j1 = (F - j0) < kFcSeg ? F : j0 + kFcSeg;
+    const float* __restrict__ X = x + n * F;
+    int32_t* __restrict__ Ln = list + n * F;
+    const uint64_t lt = lanemask_lt();
+    float v_next = j0 + lane < j1 ? X[j0 + lane] : kInfTime;
+    for (int jb = j0; jb < j1; jb += 64) {
+        const float v = v_next;
+        v_next = jb + 64 + lane < j1 ? X[jb + 64 + lane] : kInfTime;  // next chunk in flight
+        const int b = culif_bin(v, T);
+        const bool valid = b >= 0;
+        uint64_t m = __ballot(valid);
+        if (m == 0) continue;  // uniform
+        for (int bit = 0; bit < nbits; ++bit) {
+            const bool set = valid && ((b >> bit) & 1);
+            const uint64_t bb = __ballot(set);
+            m &= set ? bb : ~bb;
+        }
+        if (valid) Ln[cur[b] + __popcll(m & lt)] = jb + lane;
+        wave_sync();
+        if (valid && (m & lt) == 0) cur[b] += __popcll(m);
+        wave_sync();
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fc_currents(const int32_t* __restrict__ list,
+                                                     const int32_t* __restrict__ binstart,
+                                                     const float* __restrict__ W, float* __restrict__ cur,
+                                                     int N, int T, int F, int out_f, int n_oblk, int w_bytes) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t, oblk)
+    if (u >= (int64_t)N * T * n_oblk) return;          // uniform per wave
     const int ob = (int)(u % n_oblk);
-    const int t0 = (int)((u / n_oblk) % n_tgrp) * kFcBins;
-    const int64_t n = u / ((int64_t)n_oblk * n_tgrp);
+    const int t = (int)((u / n_oblk) % T);
+    const int64_t n = u / ((int64_t)n_oblk * T);
     const int lane = lane_id();
     const int o = ob * 64 + lane;
     const bool ok = o < out_f;
-    const int oo = ok ? o : 0;
-    const float* __restrict__ X = x + n * (int64_t)F;
-    float acc[kFcBins];
+    const int32_t* __restrict__ L = list + n * F;
+    const int beg = binstart[n * (T + 1) + t], end = binstart[n * (T + 1) + t + 1];
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, w_bytes, 0x00020000);
+    const int voff = (ok ? o : 0) * 4;
+    const int rowb = out_f * 4;
+    float acc = 0.0f;
+    // list entries one group ahead of the gathers; the list is padded, so
+    // entries past `end` are read but never used
+    int jn[kFcGroup];
 #pragma unroll
-    for (int k = 0; k < kFcBins; ++k) acc[k] = 0.0f;
-    for (int base0 = 0; base0 < F; base0 += 64 * kFcUnroll) {
-        int st[kFcUnroll];
+    for (int g = 0; g < kFcGroup; ++g) jn[g] = L[beg + g];
+    for (int i = beg; i < end; i += kFcGroup) {
+        int j[kFcGroup];
 #pragma unroll
-        for (int r = 0; r < kFcUnroll; ++r) {
-            const int j = base0 + 64 * r + lane;
-            st[r] = culif_bin(j < F ? X[j] : kInfTime, T);
+        for (int g = 0; g < kFcGroup; ++g) {
+            j[g] = jn[g];
+            jn[g] = L[i + kFcGroup + g];
         }
+        float w[kFcGroup];
 #pragma unroll
-        for (int r = 0; r < kFcUnroll; ++r) {
-            const int base = base0 + 64 * r;
+        for (int g = 0; g < kFcGroup; ++g)
+            w[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, (i + g < end ? j[g] : 0) * rowb, 0));
 #pragma unroll
-            for (int k = 0; k < kFcBins; ++k) {
-                uint64_t m = __ballot(st[r] == t0 + k);
-                while (m) {
-                    // up to 8 gathers in flight, added in ascending j
-                    int js[8];
-#pragma unroll
-                    for (int g = 0; g < 8; ++g) {
-                        js[g] = m ? base + (int)__builtin_ctzll(m) : -1;
-                        m &= m - 1;
-                    }
-                    float w[8];
-#pragma unroll
-                    for (int g = 0; g < 8; ++g) w[g] = js[g] >= 0 ? W[(int64_t)js[g] * out_f + oo] : 0.0f;
-#pragma unroll
-                    for (int g = 0; g < 8; ++g)
-                        if (js[g] >= 0) acc[k] = acc[k] + w[g];
-                }
-            }
-        }
+        for (int g = 0; g < kFcGroup; ++g)
+            if (i + g < end) acc = acc + w[g];
     }
-    if (ok) {
-#pragma unroll
-        for (int k = 0; k < kFcBins; ++k)
-            if (t0 + k < T) cur[(n * T + t0 + k) * out_f + o] = acc[k];
-    }
+    if (ok) cur[(n * T + t) * out_f + o] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -944,16 +1039,38 @@ int launch_culif_fc_rec(vdttfs_ctx* ctx, const int32_t* cin, const float* tin, c
     return VDTTFS_OK;
 }
 
-int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F,
-                       int out_f) {
+FcSortSizes fc_sort_sizes(int N, int F, int T) {
+    FcSortSizes z;
+    z.segments = (F + kFcSeg - 1) / kFcSeg;
+    z.counts = (int64_t)N * z.segments * T;
+    z.binstart = (int64_t)N * (T + 1);
+    z.list = (int64_t)N * F + kFcListPad;
+    return z;
+}
+
+int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float* cur, int N, int F, int out_f,
+                       const FcSortScratch& sc) {
     const int T = ctx->c.T;
+    if (N <= 0 || F <= 0 || out_f <= 0) return set_error(VDTTFS_E_INVALID, "fc currents: bad shape");
+    if ((int64_t)F * out_f * 4 >= (INT64_C(1) << 31) || (int64_t)N * F >= (INT64_C(1) << 31))
+        return set_error(VDTTFS_E_UNSUPPORTED, "fc currents: weights or inputs beyond 2^31");
+    const FcSortSizes z = fc_sort_sizes(N, F, T);
+    const int S = z.segments;
+    int nbits = 0;
+    while ((1 << nbits) < T) ++nbits;
+    const int64_t sblocks = ((int64_t)N * S + 3) / 4;
+    hipLaunchKernelGGL(k_fcsort_count, dim3((unsigned)sblocks), dim3(256), 0, ctx->stream, x, sc.counts, N, F,
+                       T, S);
+    hipLaunchKernelGGL(k_fcsort_offsets, dim3((unsigned)N), dim3(256), 0, ctx->stream, sc.counts, sc.offs,
+                       sc.binstart, T, S);
+    hipLaunchKernelGGL(k_fcsort_scatter, dim3((unsigned)sblocks), dim3(256), 0, ctx->stream, x, sc.offs, sc.list,
+                       N, F, T, S, nbits);
     const int n_oblk = (out_f + 63) / 64;
-    const int n_tgrp = (T + kFcBins - 1) / kFcBins;
-    const int64_t waves = (int64_t)N * n_tgrp * n_oblk;
+    const int64_t waves = (int64_t)N * T * n_oblk;
     const int64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "fc currents: grid too large");
-    hipLaunchKernelGGL(k_fc_currents, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, x, W_t, cur, N,
-                       T, F, out_f, n_oblk, n_tgrp);
+    hipLaunchKernelGGL(k_fc_currents, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, sc.list, sc.binstart,
+                       W_t, cur, N, T, F, out_f, n_oblk, (int)((int64_t)F * out_f * 4));
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }
