@@ -489,20 +489,27 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
 #pragma unroll
     for (int v = 0; v < VEC; ++v) ok[v] = c0 + v < a.C_out;
 
-    float carry[VEC], cur[VEC], res[VEC];  // carry: membrane (V for CuLIF); cur: CuLIF current I
+    // carry: membrane (V for CuLIF); cur: CuLIF current I; res: spike time.
+    // The CuLIF neuron tests "alive" as res == kInfTime (lanes past C_out
+    // start at -1): a bool array there is packed into bytes and cost about
+    // ten more VALU per bin closing (CuLIF conv2 8.5 -> 8.2 ms).  The same
+    // change made the T1V/T2V kernels slower (VGG-16 30.5K -> 27.9K
+    // images/s), so they keep the flags.
+    float carry[VEC], cur[VEC], res[VEC];
     bool alive[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
         carry[v] = (ok[v] && !CULIF) ? a.bias[c0 + v] : 0.0f;
         cur[v] = 0.0f;
-        res[v] = kInfTime;
+        res[v] = (CULIF && !ok[v]) ? -1.0f : kInfTime;
         alive[v] = ok[v];
     }
+#define VD_ALIVE(v) (CULIF ? res[v] == kInfTime : alive[v])
     bool live = ok[0];  // any neuron of the lane still integrating
     int live_chunk_n = 0;
     if (COUNT) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(alive[v]));
+        for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(VD_ALIVE(v)));
     }
     const int T = a.T, D = a.D;
     bool done = false;
@@ -523,7 +530,7 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         if (COUNT) {                                                                    \
             const int n_ = VD_BIN_START((b) + 1) - VD_BIN_START(b);                     \
             int nl_ = 0;                                                                \
-            _Pragma("unroll") for (int v = 0; v < VEC; ++v) nl_ += __popcll(__ballot(alive[v])); \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) nl_ += __popcll(__ballot(VD_ALIVE(v))); \
             cnt_bin += (unsigned long long)n_ * nl_;                                    \
             cnt_proc += (unsigned long long)n_ * live_chunk_n;                          \
         }                                                                               \
@@ -531,10 +538,8 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
             _Pragma("unroll") for (int v = 0; v < VEC; ++v) {                           \
                 cur[v] = __builtin_fmaf(cur[v], a.decay, (acc_)[v]);                    \
                 carry[v] = carry[v] + cur[v];                                           \
-                if (alive[v] && carry[v] >= a.th) {                                     \
-                    res[v] = (float)t_;                                                 \
-                    alive[v] = false;                                                   \
-                }                                                                       \
+                const bool f_ = VD_ALIVE(v) && carry[v] >= a.th;                        \
+                res[v] = f_ ? (float)t_ : res[v];                                       \
             }                                                                           \
         } else {                                                                        \
             const float th_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), (b))); \
@@ -547,12 +552,12 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
                 }                                                                       \
             }                                                                           \
         }                                                                               \
-        live = alive[0];                                                                \
-        _Pragma("unroll") for (int v = 1; v < VEC; ++v) live = live || alive[v];        \
+        live = VD_ALIVE(0);                                                             \
+        _Pragma("unroll") for (int v = 1; v < VEC; ++v) live = live || VD_ALIVE(v);     \
         const bool chunk_end_ = ((t_ + 1) % D) == 0;                                    \
         if (COUNT && chunk_end_) {                                                      \
             live_chunk_n = 0;                                                           \
-            _Pragma("unroll") for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(alive[v])); \
+            _Pragma("unroll") for (int v = 0; v < VEC; ++v) live_chunk_n += __popcll(__ballot(VD_ALIVE(v))); \
         }                                                                               \
         if (__ballot(live) == 0 && (!COUNT || chunk_end_)) done = true;                 \
     } while (0)
@@ -627,6 +632,7 @@ stream_done:
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
         if (ok[v]) out[pix * a.C_out + c0 + v] = res[v];
+#undef VD_ALIVE
 }
 
 // One (pixel, c_out block) with the gather type of EPI = events per load:
