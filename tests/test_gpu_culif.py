@@ -184,15 +184,17 @@ def test_culif_engine_small(gpu_ctx_factory):
 
 def test_culif_engine_narrow_convs(gpu_ctx_factory):
     """Conv layers with C_out <= 64 build their merged lists in LDS inside the
-    integrating kernel (one wave per pixel); every layer against the oracle,
-    and bit-identical across chunk widths."""
-    say("culif engine with C_out <= 64 convs (lists in LDS) vs oracle")
-    H, W, F = 24, 20, 48 * 12 * 10
+    integrating kernel (one wave per pixel), and a 20-wide conv packs three
+    pixels per wave (k_stream_narrow); every layer against the oracle, and
+    bit-identical across chunk widths."""
+    say("culif engine with C_out <= 64 convs (lists in LDS, narrow) vs oracle")
+    H, W, F = 24, 20, 20 * 12 * 10
     k = models.kaiming
     L = [vdttfs.CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, H, W, 32, k(7, 0, (32, 2, 3, 3), 18), None, 0.5, 1.0),
          vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 32, H, W, 60, k(7, 1, (60, 32, 3, 3), 288), None, 0.5, 1.0),
          vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 60, H, W, 48, k(7, 2, (48, 60, 3, 3), 540), None, 0.5, 1.0),
-         vdttfs.CulifLayerSpec(vdttfs.CULIF_POOL, 48, H, W, 48, None, None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 48, H, W, 20, k(7, 4, (20, 48, 3, 3), 432), None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_POOL, 20, H, W, 20, None, None, 0.5, 1.0),
          vdttfs.CulifLayerSpec(vdttfs.CULIF_FC, F, 1, 1, 11, k(7, 3, (11, F), F), None, 0.5, 1.0)]
     w = models.CulifWorkload("narrow", vdttfs.task3_consts(T=64, delta=32), L, (2, H, W), 11, 7,
                              meta={"decay": 0.5, "th": 1.0, "density": 0.05, "sigma_px": 6.0,

@@ -128,8 +128,8 @@ int validate(const vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n) {
         }
         if (d.kind == VDTTFS_CULIF_FC_REC && (!d.weight_rec || d.C_out > 1024))
             return set_error(VDTTFS_E_INVALID, "culif net: FC_REC layer %d needs weight_rec and <= 1024 outputs", i);
-        if (d.kind == VDTTFS_CULIF_CONV && (d.C_out < 32 || d.C_in >= (1 << 24)))
-            return set_error(VDTTFS_E_UNSUPPORTED, "culif net: conv layer %d needs C_out >= 32", i);
+        if (d.kind == VDTTFS_CULIF_CONV && d.C_in >= (1 << 24))
+            return set_error(VDTTFS_E_UNSUPPORTED, "culif net: conv layer %d needs C_in < 2^24", i);
         if (fc) {
             C = d.C_out;
             H = W = 1;

@@ -762,6 +762,110 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
 }
 
 // ---------------------------------------------------------------------------
+// k_stream_narrow: layers with C_out < 32 (LeNet's 6-, 16- and 10-wide
+// layers), where one pixel per wave would leave most lanes idle.  A wave
+// packs P = 64 / C_out pixels, lane = (pixel p, c_out c); each lane walks its
+// pixel's merged list (the k_merge output, (bin, tap, cin) order) bin by bin,
+// gathering W[row + c] per event, four events in flight, and closes every
+// bin in order with the neuron of the layer, as k_stream does.  Lanes of one
+// pixel read the same list entries; lanes of different pixels diverge only
+// in how many events a bin holds.  E_proc / E_bin count per lane with the
+// same rules as k_stream (a neuron counts a bin's events while it was alive
+// at the start of the chunk / of the bin).
+template <bool COUNT, bool CULIF>
+__global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __restrict__ out,
+                                                       const int2* __restrict__ list,
+                                                       const int32_t* __restrict__ bstart,
+                                                       const float* __restrict__ theta) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int lane = lane_id();
+    const int P = 64 / a.C_out;
+    const int p = lane / a.C_out, c = lane - p * a.C_out;
+    const int64_t pix = ((int64_t)blockIdx.x * 4 + wave) * P + p;
+    if (((int64_t)blockIdx.x * 4 + wave) * P >= a.n_pix) return;  // uniform per wave
+    const bool ok = p < P && pix < a.n_pix;
+    const int2* __restrict__ L = list + (ok ? pix : 0) * a.cap;
+    const int32_t* __restrict__ BS = bstart + (ok ? pix : 0) * (int64_t)(a.T + 1);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    const int voff = c * 4;
+    float carry = (ok && !CULIF) ? a.bias[c] : 0.0f;
+    float cur = 0.0f, res = kInfTime;
+    bool alive = ok, alive_chunk = ok;
+    unsigned long long cnt_proc = 0, cnt_bin = 0;
+    const int T = a.T, D = a.D;
+    int j = 0;
+    for (int t0 = 0; t0 < T; t0 += kBlockBins) {
+        const int nb = (T - t0) < kBlockBins ? (T - t0) : kBlockBins;
+        const float v_th = (!CULIF && lane < nb) ? theta[t0 + lane] : 0.0f;
+        bool done = false;
+        for (int b8 = 0; b8 < nb && !done; b8 += 8) {
+            int ends[8];  // bin ends of the next eight bins, loaded together
+#pragma unroll
+            for (int g = 0; g < 8; ++g) ends[g] = (ok && b8 + g < nb) ? BS[t0 + b8 + g + 1] : 0;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const int b = b8 + g;
+                if (b >= nb || done) break;  // uniform
+                const int t = t0 + b;
+                const int e_end = ends[g];
+                const int e_beg = j;
+                float acc = 0.0f;
+                while (__ballot(j < e_end)) {
+                    int2 e[4];
+                    float w[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) e[q] = (j + q < e_end) ? L[j + q] : make_int2(0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, e[q].x + voff, 0, 0));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (j + q < e_end) acc = __builtin_fmaf(w[q], __int_as_float(e[q].y), acc);
+                    j = (j + 4 < e_end) ? j + 4 : (j < e_end ? e_end : j);
+                }
+                if (COUNT) {
+                    const unsigned long long n = (unsigned long long)(e_end - e_beg);
+                    if (alive) cnt_bin += n;
+                    if (alive_chunk) cnt_proc += n;
+                }
+                if (CULIF) {
+                    cur = __builtin_fmaf(cur, a.decay, acc);
+                    carry = carry + cur;
+                    if (alive && carry >= a.th) {
+                        res = (float)t;
+                        alive = false;
+                    }
+                } else {
+                    const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+                    carry = carry + acc;
+                    if (t >= a.t_min && th >= 1e-5f && alive && carry >= th) {
+                        res = (float)t;
+                        alive = false;
+                    }
+                }
+                const bool chunk_end = ((t + 1) % D) == 0;
+                if (COUNT && chunk_end) alive_chunk = alive;
+                if (__ballot(alive) == 0 && (!COUNT || chunk_end)) done = true;
+            }
+        }
+        if (done) break;
+    }
+    if (ok) out[pix * a.C_out + c] = res;
+    if (COUNT) {
+        for (int o = 32; o > 0; o >>= 1) {
+            cnt_proc += __shfl_xor(cnt_proc, o, 64);
+            cnt_bin += __shfl_xor(cnt_bin, o, 64);
+        }
+        if (lane == 0) {
+            unsigned long long* cs = counter_stripe(a.counters);
+            atomicAdd(&cs[0], cnt_proc);
+            atomicAdd(&cs[1], cnt_bin);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 struct GenArgs {
     float* out;
     const int32_t* off;
@@ -1007,6 +1111,14 @@ bool wave_path_ok(const IntegShape& sh, int64_t* wbytes) {
     return sh.C_out >= 32 && nk_max <= 25 && *wbytes < INT64_C(0x7fffffff) && sh.C_in < (1 << 24);
 }
 
+// Layers narrower than the wave path (C_out < 32) take k_stream_narrow.
+bool narrow_path_ok(const IntegShape& sh, int64_t* wbytes) {
+    const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
+    *wbytes = (int64_t)nk_max * sh.C_in * sh.C_out * 4;
+    return sh.C_out >= 1 && sh.C_out < 32 && nk_max <= 25 && *wbytes < INT64_C(0x7fffffff) &&
+           sh.C_in < (1 << 24);
+}
+
 int64_t n_pixels(const IntegShape& sh) {
     return (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
 }
@@ -1095,6 +1207,36 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
     return VDTTFS_OK;
 }
 
+int launch_stream_narrow(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
+                         const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
+                         const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
+    int vec, epi;
+    const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
+                                     counters, culif, &vec, &epi);
+    const int P = 64 / sh.C_out;
+    const int64_t waves = (a.n_pix + P - 1) / P;
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks <= 0) return VDTTFS_OK;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+#define VD_LAUNCH_NARROW(C, L)                                                                      \
+    hipLaunchKernelGGL((k_stream_narrow<C, L>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a, out, \
+                       list, bstart, theta)
+    if (culif) {
+        if (counters)
+            VD_LAUNCH_NARROW(true, true);
+        else
+            VD_LAUNCH_NARROW(false, true);
+    } else {
+        if (counters)
+            VD_LAUNCH_NARROW(true, false);
+        else
+            VD_LAUNCH_NARROW(false, false);
+    }
+#undef VD_LAUNCH_NARROW
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
 }  // namespace
 
 // Measured per VGG layer against bucketize + k_merge: the dense merge is
@@ -1103,8 +1245,12 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
 // chunks spill registers).
 bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
     int64_t wbytes;
-    return !sh.is_fc && wave_path_ok(sh, &wbytes) && ctx->c.T <= kDenseMaxBins &&
-           sh.C_in <= kDenseMaxCin && sh.K_h * sh.K_w <= 9;
+    const int taps = sh.K_h * sh.K_w;
+    // narrow layers (k_stream_narrow) take 5x5 kernels too: their pixels have
+    // few receptive elements (LeNet: 25 and 150), where the closed-form merge
+    // spends its time on a 25-column x T table per pixel
+    const bool shape_ok = wave_path_ok(sh, &wbytes) ? taps <= 9 : (narrow_path_ok(sh, &wbytes) && taps <= 25);
+    return !sh.is_fc && shape_ok && ctx->c.T <= kDenseMaxBins && sh.C_in <= kDenseMaxCin;
 }
 
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
@@ -1112,10 +1258,11 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
                           const float* bias, const float* theta, int t_min, const IntegShape& sh,
                           unsigned long long* counters, const CulifNeuron* culif) {
     int64_t wbytes;
-    if (!wave_path_ok(sh, &wbytes)) {
+    const bool narrow = narrow_path_ok(sh, &wbytes);
+    if (!narrow && !wave_path_ok(sh, &wbytes)) {
         if (culif)
             return set_error(VDTTFS_E_UNSUPPORTED,
-                             "CuLIF engine layers need C_out >= 32, <= 25 taps and < 2 GB of weights");
+                             "CuLIF engine layers need <= 25 taps and < 2 GB of weights");
         return launch_integrate_generic_bins(ctx, out, ev, off, W, bias, theta, t_min, sh, counters);
     }
     const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
@@ -1150,6 +1297,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     else
         hipLaunchKernelGGL(k_merge<25>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
     VD_HIP(hipGetLastError());
+    if (narrow) return launch_stream_narrow(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
+                                            counters, culif);
     return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
 }
 
@@ -1158,7 +1307,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
                            const float* theta, int t_min, const IntegShape& sh,
                            unsigned long long* counters, const CulifNeuron* culif) {
     int64_t wbytes;
-    if (!integrate_dense_ok(ctx, sh) || !wave_path_ok(sh, &wbytes))
+    const bool narrow = narrow_path_ok(sh, &wbytes);
+    if (!integrate_dense_ok(ctx, sh) || (!narrow && !wave_path_ok(sh, &wbytes)))
         return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
     const int nk_max = sh.K_h * sh.K_w;
     const int64_t n_pix = n_pixels(sh);
@@ -1190,6 +1340,17 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.inv_cin = 1.0f / (float)sh.C_in;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    if (narrow) {
+        if (nk_max <= 9)
+            hipLaunchKernelGGL(k_merge_dense<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream,
+                               m);
+        else
+            hipLaunchKernelGGL(k_merge_dense<25>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0,
+                               ctx->stream, m);
+        VD_HIP(hipGetLastError());
+        return launch_stream_narrow(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters,
+                                    culif);
+    }
     int vec, epi;
     const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
                                      counters, culif, &vec, &epi);
