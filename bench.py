@@ -439,11 +439,11 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": (tr[0] / tr[1]) if tr else None,
-            "kernel": "integrator = a layer's k_stream_dense (conv, C_in <= 64, C_out <= 64: "
+            "kernel": "integrator = a layer's k_stream_dense (conv, C_in <= 64, 32 <= C_out <= 64: "
                       "list built in LDS), k_merge_dense + k_stream (other conv, C_in <= 64) or "
-                      "k_bucketize + k_merge + k_stream (wider conv, FC); a launch is one layer's "
-                      "integrate, achieved = fused algorithmic bytes of a step / integrator time "
-                      "of a step",
+                      "k_bucketize + k_merge + k_stream (wider conv, FC); layers with C_out < 32 "
+                      "stream with k_stream_narrow; a launch is one layer's integrate, achieved = "
+                      "fused algorithmic bytes of a step / integrator time of a step",
             "algorithmic_bytes_per_step": b_int,
             "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
             "traffic_per_step": tr[0] if tr else None,

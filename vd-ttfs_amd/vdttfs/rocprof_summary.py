@@ -66,7 +66,7 @@ def _forwards(rows, key_start="Start_Timestamp"):
     return fw
 
 
-_COUNTING = re.compile(r"^(k_stream(_dense)?<true|k_integrate_generic<\w+, \d+, true>)")
+_COUNTING = re.compile(r"^(k_stream(_dense|_narrow)?<true|k_integrate_generic<\w+, \d+, true>)")
 
 
 def _is_counting(forward) -> bool:
