@@ -236,6 +236,32 @@ int vdttfs_net_set_timing(vdttfs_net* net, int enable);
 int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
                            double* bucket_ms, int64_t* bucket_launches);
 
+/* ---- step-by-step (time-driven) baseline: the reference's GPU
+ *      denominator, T1S = task1_lenet_mnist/stepbystep_cuda/
+ *      snn_mnist_stepbystep.cu, T2S = task2_vgg16_cifar10/stepbystep_cuda/
+ *      bench_vgg_timedriven_baseline.cu ------------------------------------ */
+/* Every global step launches every layer: each neuron sums the weights of
+ * the inputs that spike at that step and fires once on the decaying
+ * threshold.  mode VDTTFS_STEP_T1 (T1S:47-103, 222-244): all layers share
+ * the step, V = fma(sum w, kv(t), V), the last layer's first spike is the
+ * output (argmin readout), T steps.  mode VDTTFS_STEP_T2 (T2S:53-200,
+ * 329-352): weighted layer d integrates at t - (d-1)*tfs in [0, T) with
+ * psp = fma chain of w*kv and fires at t - d*tfs, the last weighted layer
+ * keeps max(V + b) (argmax readout), (D-1)*tfs + T steps.  Decay and
+ * threshold use the context's T, tfs, vth and each layer's tc_fire/td as in
+ * vdttfs_net_create; convs use the context's padding rule. */
+#define VDTTFS_STEP_T1 1
+#define VDTTFS_STEP_T2 2
+typedef struct vdttfs_stepnet vdttfs_stepnet;
+int vdttfs_stepnet_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
+                          int64_t img_elems, int encode_mode, float tc_in, float td_in, int mode,
+                          vdttfs_stepnet** out);
+int vdttfs_stepnet_destroy(vdttfs_stepnet* net);
+/* encode -> all steps -> readout, stream-ordered; d_pred (nullable) gets B classes. */
+int vdttfs_stepnet_forward(vdttfs_stepnet* net, const float* d_img, int32_t* d_pred);
+/* The last layer's output [B][C] (first-spike steps or max V + b) and the step count. */
+int vdttfs_stepnet_output(vdttfs_stepnet* net, const float** d_out, int64_t* elems, int* steps);
+
 /* ---- CuLIF set: task 3 (T3V = task3_dvsgesture/vdttfs_cuda/
  *      snn_inference_timesorted.cu) ------------------------------------ */
 /* The current-based LIF neuron of T3V:58-62: per step I = I*decay + in

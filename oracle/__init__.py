@@ -227,6 +227,40 @@ def net_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td_in,
             "ebin": np.array(list(eb), np.uint64), "outs": outs}
 
 
+STEP_T1, STEP_T2 = 1, 2
+
+
+def stepnet_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td_in, mode,
+                    same_pad=False, nthreads=0):
+    """Step-by-step (time-driven) baseline network: T1S (mode 1) or T2S
+    (mode 2) semantics, see orc_stepnet_forward.  Returns dict(final, pred,
+    steps): final is B x C of the last layer (first-spike steps or max V+b)."""
+    n = len(layers)
+    arr = (OrcLayer * n)()
+    keep = []
+    fp = C.POINTER(C.c_float)
+    for i, l in enumerate(layers):
+        k = f32(l.kernel) if l.kernel is not None else None
+        b = f32(l.bias) if l.bias is not None else None
+        keep += [k, b]
+        pad = l.K_h // 2 if (l.kind == ORC_CONV and same_pad) else 0
+        arr[i] = OrcLayer(l.kind, l.H_in, l.W_in, l.C_in, l.H_out, l.W_out, l.C_out, l.K_h, l.K_w,
+                          pad, k.ctypes.data_as(fp) if k is not None else fp(),
+                          b.ctypes.data_as(fp) if b is not None else fp(), l.tc_fire, l.td)
+    last = layers[-1]
+    final = np.empty(B * last.H_out * last.W_out * last.C_out, np.float32)
+    pred = np.empty(B, np.int32)
+    steps = C.c_int(0)
+    img = f32(img)
+    cc = c.c()
+    rc = lib().orc_stepnet_forward(C.byref(cc), arr, C.c_int(n), C.c_int(B), _p(img), C.c_int64(img_elems),
+                                   C.c_int(encode_mode), C.c_float(tc_in), C.c_float(td_in), C.c_int(mode),
+                                   _p(final), _p(pred), C.byref(steps), C.c_int(nthreads))
+    if rc != 0:
+        raise RuntimeError(f"orc_stepnet_forward failed: {rc}")
+    return {"final": final, "pred": pred, "steps": steps.value}
+
+
 # ---- CuLIF set (T3V:30-225) -------------------------------------------------
 def _ci(*xs):
     return [C.c_int(int(x)) for x in xs]

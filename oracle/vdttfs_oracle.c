@@ -509,6 +509,184 @@ int orc_net_forward(const orc_consts* c, const orc_layer* layers, int n_layers, 
     return rc;
 }
 
+/* ----------------------- step-by-step baselines (T1S, T2S) ------------------ */
+
+/* Number of global steps: T (T1S:229) or, for T2S, until the last weighted
+ * layer's integration window [ (D-1)*tfs, (D-1)*tfs + T ) has passed
+ * (TIME_STEPS = 680 for 16 weighted layers, tfs 40, T 80; T2S:13). */
+static int step_count(const orc_consts* c, const orc_layer* layers, int n_layers, int mode) {
+    if (mode == 1) return c->T;
+    int D = 0;
+    for (int l = 0; l < n_layers; ++l)
+        if (layers[l].kind != ORC_POOL) ++D;
+    return (int)ceilf((float)(D - 1) * c->tfs + (float)c->T);
+}
+
+int orc_stepnet_forward(const orc_consts* c, const orc_layer* layers, int n_layers, int B,
+                        const float* img, int64_t img_elems_per_image, int encode_mode,
+                        float tc_in, float td_in, int mode, float* final_out, int32_t* pred,
+                        int* steps_out, int nthreads) {
+    if (n_layers <= 0 || (mode != 1 && mode != 2)) return -1;
+    const int T = c->T;
+    const int64_t n_img = (int64_t)B * img_elems_per_image;
+    float* tin = (float*)malloc(sizeof(float) * n_img);
+    unsigned char* s0 = (unsigned char*)calloc(n_img, 1);
+    unsigned char** spk = (unsigned char**)calloc(n_layers, sizeof(void*));
+    unsigned char** fired = (unsigned char**)calloc(n_layers, sizeof(void*));
+    float** vmem = (float**)calloc(n_layers, sizeof(void*));
+    int* depth = (int*)calloc(n_layers, sizeof(int));
+    float *tci = (float*)calloc(n_layers, sizeof(float)), *tdi = (float*)calloc(n_layers, sizeof(float));
+    int last_w = -1;
+    int rc = 0;
+    if (!tin || !s0 || !spk || !fired || !vmem || !depth || !tci || !tdi) rc = -2;
+    if (encode_mode == ORC_ENC_LOG) orc_encode_log(img, tin, n_img, tc_in, td_in, T);
+    else orc_encode_linear(img, tin, n_img, T);
+    {
+        int d = 0;
+        float tc = tc_in, td = td_in;
+        for (int l = 0; l < n_layers && rc == 0; ++l) {
+            const orc_layer* L = &layers[l];
+            int64_t n = layer_out_elems(L, B);
+            spk[l] = (unsigned char*)calloc(n, 1);
+            fired[l] = (unsigned char*)calloc(n, 1);
+            if (!spk[l] || !fired[l]) rc = -2;
+            if (L->kind != ORC_POOL) {
+                vmem[l] = (float*)calloc(n, sizeof(float));
+                if (!vmem[l]) rc = -2;
+                depth[l] = ++d;
+                tci[l] = tc;
+                tdi[l] = td;
+                tc = L->tc_fire;
+                td = L->td;
+                last_w = l;
+            }
+        }
+    }
+    const int steps = step_count(c, layers, n_layers, mode);
+    if (steps_out) *steps_out = steps;
+    const orc_layer* LL = &layers[n_layers - 1];
+    const int64_t n_out = layer_out_elems(LL, B);
+    for (int64_t i = 0; i < n_out && rc == 0; ++i) final_out[i] = (mode == 1) ? ORC_INF : -1e9f;
+    if (rc == 0 && last_w != n_layers - 1) rc = -3; /* the readout layer must be a weighted layer */
+
+    for (int t = 0; t < steps && rc == 0; ++t) {
+        for (int64_t i = 0; i < n_img; ++i) s0[i] = (tin[i] == (float)t);
+        const unsigned char* s_in = s0;
+        for (int l = 0; l < n_layers; ++l) {
+            const orc_layer* L = &layers[l];
+            const int64_t n = layer_out_elems(L, B);
+            unsigned char* so = spk[l];
+            unsigned char* fr = fired[l];
+            if (L->kind == ORC_POOL) {
+                const int Ho = L->H_in / 2, Wo = L->W_in / 2, C = L->C_in;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+                for (int64_t idx = 0; idx < n; ++idx) {
+                    if (fr[idx]) { so[idx] = 0; continue; }
+                    int ch = (int)(idx % C), w = (int)((idx / C) % Wo), h = (int)((idx / C / Wo) % Ho);
+                    int64_t b = idx / ((int64_t)C * Wo * Ho);
+                    so[idx] = 0;
+                    for (int i = 0; i < 2 && !so[idx]; ++i)
+                        for (int j = 0; j < 2; ++j) {
+                            int hi = h * 2 + i, wi = w * 2 + j;
+                            if (hi < L->H_in && wi < L->W_in &&
+                                s_in[((b * L->H_in + hi) * L->W_in + wi) * C + ch]) {
+                                so[idx] = 1;
+                                fr[idx] = 1;
+                                break;
+                            }
+                        }
+                }
+            } else {
+                const int is_fc = (L->kind != ORC_CONV);
+                const int out_layer = (l == n_layers - 1);
+                const int d = depth[l];
+                int int_ok, fire_ok;
+                float kv, th;
+                if (mode == 1) {
+                    int t_min = (int)ceilf(L->td);
+                    if (t_min < 0) t_min = 0;
+                    kv = expf(-((float)t - tdi[l]) / tci[l]);
+                    th = c->vth * expf(-((float)t - L->td) / L->tc_fire);
+                    int_ok = 1;
+                    fire_ok = t >= t_min;
+                } else {
+                    float t_integ = (float)t - (float)(d - 1) * c->tfs;
+                    float t_fire = (float)t - (float)d * c->tfs;
+                    float start = L->td > 0.0f ? ceilf(L->td) : 0.0f;
+                    kv = expf(-(t_integ - tdi[l]) / tci[l]);
+                    th = c->vth * expf(-(t_fire - L->td) / L->tc_fire);
+                    int_ok = t_integ >= 0.0f && t_integ < (float)T;
+                    fire_ok = t_fire >= start && t_fire < (float)T;
+                }
+                const int cin_tot = is_fc ? L->H_in * L->W_in * L->C_in : L->C_in;
+                float* V = vmem[l];
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+                for (int64_t nid = 0; nid < n; ++nid) {
+                    const int keep_max = (mode == 2 && out_layer);
+                    if (!keep_max && fr[nid]) { so[nid] = 0; continue; }
+                    int co, im, ho, wo;
+                    decode(nid, is_fc, is_fc ? 1 : L->H_out, is_fc ? 1 : L->W_out, L->C_out, &co, &im, &ho, &wo);
+                    if (int_ok) {
+                        float psp = 0.0f;
+                        if (is_fc) {
+                            const unsigned char* src = s_in + (int64_t)im * cin_tot;
+                            for (int ci = 0; ci < cin_tot; ++ci)
+                                if (src[ci]) {
+                                    float w = L->W[(int64_t)ci * L->C_out + co];
+                                    psp = (mode == 1) ? psp + w : fmaf(w, kv, psp);
+                                }
+                        } else {
+                            for (int kh = 0; kh < L->K_h; ++kh) {
+                                int hi = ho - L->pad + kh;
+                                if (hi < 0 || hi >= L->H_in) continue;
+                                for (int kw = 0; kw < L->K_w; ++kw) {
+                                    int wi = wo - L->pad + kw;
+                                    if (wi < 0 || wi >= L->W_in) continue;
+                                    const unsigned char* src =
+                                        s_in + (((int64_t)im * L->H_in + hi) * L->W_in + wi) * L->C_in;
+                                    int64_t wb = (int64_t)(kh * L->K_w + kw) * L->C_in;
+                                    for (int ci = 0; ci < L->C_in; ++ci)
+                                        if (src[ci]) {
+                                            float w = L->W[(wb + ci) * L->C_out + co];
+                                            psp = (mode == 1) ? psp + w : fmaf(w, kv, psp);
+                                        }
+                                }
+                            }
+                        }
+                        V[nid] = (mode == 1) ? fmaf(psp, kv, V[nid]) : V[nid] + psp;
+                    }
+                    so[nid] = 0;
+                    if (keep_max) {
+                        if (int_ok) {
+                            float v = V[nid] + L->bias[co];
+                            if (v > final_out[nid]) final_out[nid] = v;
+                        }
+                    } else if (fire_ok) {
+                        if (V[nid] + L->bias[co] >= th && th >= 1e-5f) {
+                            so[nid] = 1;
+                            fr[nid] = 1;
+                            if (mode == 1 && out_layer && final_out[nid] >= ORC_INF) final_out[nid] = (float)t;
+                        }
+                    }
+                }
+            }
+            s_in = so;
+        }
+    }
+    if (rc == 0 && pred) {
+        int C_last = LL->H_out * LL->W_out * LL->C_out;
+        if (mode == 1) orc_readout_argmin(final_out, B, C_last, pred);
+        else orc_readout_argmax(final_out, B, C_last, pred);
+    }
+    for (int l = 0; l < n_layers; ++l) {
+        if (spk) free(spk[l]);
+        if (fired) free(fired[l]);
+        if (vmem) free(vmem[l]);
+    }
+    free(tin); free(s0); free(spk); free(fired); free(vmem); free(depth); free(tci); free(tdi);
+    return rc;
+}
+
 /* ------------------------------- CuLIF (T3V) ------------------------------ */
 
 /* One chunk of the CuLIF neuron: T3V:58-62 (I = I*decay + in, V += I). */

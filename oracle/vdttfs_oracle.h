@@ -135,6 +135,29 @@ int orc_net_forward(const orc_consts* c, const orc_layer* layers, int n_layers, 
                     float** layer_outs, float* final_out, int32_t* pred,
                     uint64_t* eproc, uint64_t* ebin, int nthreads);
 
+/* ---- step-by-step (time-driven) baselines ----
+ * T1S = task1_lenet_mnist/stepbystep_cuda/snn_mnist_stepbystep.cu
+ * T2S = task2_vgg16_cifar10/stepbystep_cuda/bench_vgg_timedriven_baseline.cu
+ * Every weighted layer integrates, at each global step, the binary spikes
+ * its inputs emit at that step, and fires (once) on the decaying threshold.
+ *   mode 1 (T1S:47-103, 222-244): all layers share the step; psp = sum of the
+ *          spiking inputs' weights, V = fma(psp, kv(t), V); fire when
+ *          t >= t_min and V + b >= th(t) >= 1e-5; the output layer records its
+ *          first spike (argmin readout).
+ *   mode 2 (T2S:53-200, 329-352): weighted layer d (1-based) integrates at
+ *          t - (d-1)*tfs in [0, T) with psp = fma chain of w*kv, V += psp, and
+ *          fires at t - d*tfs in [ceil(td)+, T); the last weighted layer keeps
+ *          max(V + b) over its window (argmax readout).
+ * kv(t) = expf(-(t - td_prev)/tc_prev), th(t) = vth * expf(-(t - td)/tc),
+ * evaluated once per (layer, step).  Pools fire at the first step any of
+ * their 2x2 inputs spikes.  final_out (B x C of the last layer) gets the
+ * first-spike steps (mode 1) or max(V + b) (mode 2); steps_out the number
+ * of global steps run.  A VMEM layer is treated as the output FC. */
+int orc_stepnet_forward(const orc_consts* c, const orc_layer* layers, int n_layers, int B,
+                        const float* img, int64_t img_elems_per_image, int encode_mode,
+                        float tc_in, float td_in, int mode, float* final_out, int32_t* pred,
+                        int* steps_out, int nthreads);
+
 /* ---- CuLIF (T3V), config 4 ---- */
 /* conv1_raw_early (T3V:30-65): dense events [N][C_in][H][W][T], OIHW 3x3 pad 1. */
 void orc_culif_conv1_raw(const float* data, float* out, const float* weight, int N, int C_in,

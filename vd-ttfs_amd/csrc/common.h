@@ -169,6 +169,25 @@ int launch_fc_currents(vdttfs_ctx* ctx, const float* x, const float* W_t, float*
                        const FcSortScratch& sc);
 int launch_nhwc_to_nchw(vdttfs_ctx* ctx, const float* in, float* out, int N, int C, int H, int W);
 
+// Layer-table checks of vdttfs_net_create (shapes chain, kinds, weights).
+int validate_layer_table(const vdttfs_consts& c, const vdttfs_layer_desc* layers, int n, int64_t img_elems);
+
+// Step-by-step baseline (k_step.hip): one layer of a time-driven network.
+struct StepLayer {
+    int kind;
+    const float* W;
+    const float* bias;
+    int64_t n;  // neurons: B * H_out * W_out * C_out
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+};
+int launch_step_input(vdttfs_ctx* ctx, const float* tin, uint8_t* s, int64_t n, int t);
+int launch_step_neuron(vdttfs_ctx* ctx, const StepLayer& L, const uint8_t* s_in, uint8_t* s_out, float* vmem,
+                       uint8_t* fired, float* out, int mode, int int_ok, int fire_ok, int out_layer, float kv,
+                       float th, int t);
+int launch_step_pool(vdttfs_ctx* ctx, const uint8_t* s_in, uint8_t* s_out, uint8_t* fired, int64_t n, int H_in,
+                     int W_in, int C);
+int launch_step_fill(vdttfs_ctx* ctx, float* p, int64_t n, float v);
+
 // shape validation shared by the entry points
 int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s);
 

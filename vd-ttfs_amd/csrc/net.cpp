@@ -312,6 +312,12 @@ int create_impl(vdttfs_net* net, const vdttfs_layer_desc* layers, int n) {
 
 }  // namespace
 
+namespace vdttfs {
+int validate_layer_table(const vdttfs_consts& c, const vdttfs_layer_desc* layers, int n, int64_t img_elems) {
+    return validate(c, layers, n, img_elems);
+}
+}  // namespace vdttfs
+
 extern "C" {
 
 int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,

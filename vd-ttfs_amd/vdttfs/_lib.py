@@ -27,6 +27,7 @@ LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM = 0, 1, 2, 3
 ENCODE_LINEAR, ENCODE_LOG = 0, 1
 READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
+STEP_T1, STEP_T2 = 1, 2
 
 
 class VdttfsError(RuntimeError):
@@ -162,6 +163,10 @@ SIGNATURES = {
     "vdttfs_net_destroy": [_vp],
     "vdttfs_net_forward": [_vp, _vp, _vp],
     "vdttfs_net_layer_output": [_vp, _i, C.POINTER(_vp), C.POINTER(_i64)],
+    "vdttfs_stepnet_create": [_vp, C.POINTER(LayerDesc), _i, _i, _i64, _i, _f, _f, _i, C.POINTER(_vp)],
+    "vdttfs_stepnet_destroy": [_vp],
+    "vdttfs_stepnet_forward": [_vp, _vp, _vp],
+    "vdttfs_stepnet_output": [_vp, C.POINTER(_vp), C.POINTER(_i64), C.POINTER(_i)],
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
     "vdttfs_net_read_timing": [_vp, C.POINTER(C.c_double), C.POINTER(_i64),

@@ -17,7 +17,7 @@ import numpy as np
 from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
                    LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG,
                    READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
-                   CULIF_FC_REC, CULIF_FC)
+                   CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2)
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -328,6 +328,45 @@ class Net:
         check(lib().vdttfs_net_read_timing(self.handle, C.byref(im), C.byref(il), C.byref(bm),
                                            C.byref(bl)))
         return im.value, il.value, bm.value, bl.value
+
+
+class StepNet:
+    """The step-by-step (time-driven) baseline over the same layer table as
+    Net: T1S (STEP_T1) or T2S (STEP_T2) semantics (vdttfs_stepnet_*)."""
+
+    def __init__(self, ctx: Context, layers: list[Layer], B: int, img_elems: int,
+                 encode_mode=ENCODE_LINEAR, tc_in=16.0, td_in=0.0, mode=STEP_T1):
+        self.ctx = ctx
+        self.layers = layers
+        self.B = B
+        for l in layers:
+            if l.kernel is not None:
+                l.kernel = np.ascontiguousarray(l.kernel, np.float32)
+            if l.bias is not None:
+                l.bias = np.ascontiguousarray(l.bias, np.float32)
+        arr = (LayerDesc * len(layers))(*[l.to_c() for l in layers])
+        h = C.c_void_p()
+        check(lib().vdttfs_stepnet_create(ctx.handle, arr, len(layers), B, img_elems, encode_mode,
+                                          tc_in, td_in, mode, C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle is not None:
+            lib().vdttfs_stepnet_destroy(self.handle)
+            self.handle = None
+
+    def forward(self, d_img: DeviceArray, d_pred: DeviceArray | None = None):
+        check(lib().vdttfs_stepnet_forward(self.handle, d_img.ptr, d_pred.ptr if d_pred else None))
+
+    def output(self):
+        """(last layer's [B][C] output as numpy, number of global steps)."""
+        p = C.c_void_p()
+        n = C.c_int64()
+        steps = C.c_int()
+        check(lib().vdttfs_stepnet_output(self.handle, C.byref(p), C.byref(n), C.byref(steps)))
+        h = np.empty(n.value, np.float32)
+        check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), p, h.nbytes))
+        return h, steps.value
 
 
 @dataclass
