@@ -17,6 +17,9 @@ The other synthetic workloads print one line each in the same format
   python bench.py --workload lenet5     # config 2: LeNet-5, B=1024 (config 1 = its B=1 CPU leg)
   python bench.py --workload culif7     # config 4: 7-layer CuLIF on 2x128x128 events, B=64
   python bench.py --workload fc-sweep   # config 5: FC 4096x4096, B=512, density/T'/delta sweep
+  python bench.py --workload vgg16-timedriven | lenet5-timedriven
+                                        # the reference's step-by-step GPU baseline (T2S / T1S)
+                                        # on configs 3 / 2, with the event-driven speedup
 
 roofline.traffic is the integrator's HBM bytes per launch measured with
 rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs and written to
@@ -339,7 +342,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="vgg16", choices=["vgg16", "lenet5", "culif7", "fc-sweep"])
+    ap.add_argument("--workload", default="vgg16",
+                    choices=["vgg16", "lenet5", "culif7", "fc-sweep", "vgg16-timedriven", "lenet5-timedriven"])
     ap.add_argument("--batch", type=int, default=None,
                     help="default: 256 (vgg16), 1024 (lenet5), 64 (culif7), 512 (fc-sweep)")
     ap.add_argument("--delta", type=int, default=None,
@@ -358,7 +362,79 @@ def main() -> int:
         return bench_culif(args)
     if args.workload == "fc-sweep":
         return bench_fc_sweep(args)
+    if args.workload.endswith("-timedriven"):
+        return bench_timedriven(args)
     return bench_ttfs(args)
+
+
+def bench_timedriven(args) -> int:
+    """The reference's GPU denominator on the same configs: the step-by-step
+    (time-driven) network of T1S (LeNet-5, config 2) or T2S (VGG-16, config
+    3; layer d integrates at t - (d-1)*TFS and fires at t - d*TFS), one
+    thread per neuron per step, against the event-driven engine on the same
+    images in the same process.  The two are different neuron models (the
+    baseline sums a step's spiking weights, then scales by the step's decay),
+    so predictions are compared, not required to match."""
+    import vdttfs
+    from vdttfs import models
+
+    vgg = args.workload.startswith("vgg16")
+    B = args.batch or (256 if vgg else 1024)
+    w = models.vgg16(delta=args.delta or 8) if vgg else models.lenet5(delta=args.delta or 16)
+    mode = vdttfs.STEP_T2 if vgg else vdttfs.STEP_T1
+    img = models.images_for(w, B)
+    ctx = vdttfs.Context(w.consts, 0)
+    d_img = ctx.to_device(img)
+    d_pred = ctx.empty(B, np.int32)
+    steps = max(1, min(args.steps, 3))
+    sn = vdttfs.StepNet(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, mode)
+    log(f"bench: {w.name} time-driven ({'T2S' if vgg else 'T1S'}) B={B}, {steps} timed forwards")
+    sn.forward(d_img, d_pred)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        sn.forward(d_img, d_pred)
+    ctx.synchronize()
+    ms_td = (time.perf_counter() - t0) * 1000.0 / steps
+    _, n_steps = sn.output()
+    pred_td = d_pred.download()
+    sn.close()
+    net = vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
+    for _ in range(3):
+        net.forward(d_img, d_pred)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        net.forward(d_img, d_pred)
+    ctx.synchronize()
+    ms_ev = (time.perf_counter() - t0) * 1000.0 / 20
+    pred_ev = d_pred.download()
+    net.close()
+    ctx.close()
+    name = "VGG-16" if vgg else "LeNet-5"
+    out = {
+        "metric": f"images/sec/GPU for {name} time-driven (step-by-step) baseline bs={B}",
+        "value": B / (ms_td * 1e-3),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 1,
+        "ms_per_step": ms_td,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: the same seeded images and random-init weights as the event-driven workload",
+        "config": {"workload": f"{name} time-driven baseline ({'T2S' if vgg else 'T1S'} semantics)",
+                   "batch": B, "T": w.consts.T, "tfs": w.consts.tfs, "global_steps": n_steps,
+                   "parallelism": "none (one GPU)"},
+        "event_driven_images_per_s": B / (ms_ev * 1e-3),
+        "event_driven_ms_per_step": ms_ev,
+        "speedup_event_driven": ms_td / ms_ev,
+        "prediction_agreement": float(np.mean(pred_td == pred_ev)),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def bench_ttfs(args) -> int:
