@@ -198,6 +198,8 @@ int vdttfs_free_weights(vdttfs_ctx* ctx, vdttfs_dev_layer* layers, int num_layer
 #define VDTTFS_LAYER_VMEM 3   /* readout vmem  */
 #define VDTTFS_ENCODE_LINEAR 0
 #define VDTTFS_ENCODE_LOG    1
+#define VDTTFS_ENCODE_TIMES  2   /* the input already holds spike times (e.g. encoded under a
+                                    wider window, for temporal truncation); net engine only */
 #define VDTTFS_READOUT_ARGMIN 0
 #define VDTTFS_READOUT_ARGMAX 1
 #define VDTTFS_READOUT_ARGMIN_FIRST 2  /* T3V:291-298: argmin seeded with class 0 */
@@ -233,6 +235,17 @@ int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint6
  * synchronises and returns the summed milliseconds and launch count since
  * the last reset. */
 int vdttfs_net_set_timing(vdttfs_net* net, int enable);
+/* Per-layer integration windows T'_l (input-aware temporal truncation).  No
+ * counterpart in the reference, which compiles one TIME_WINDOW per program
+ * (T1V:12, T2V:12) and describes per-layer windows, chosen offline from
+ * spike-time percentiles, without code (README.md:46-54).  windows[i] in
+ * [1, T] runs layer i as if TIME_WINDOW were windows[i]: its bucketize keeps
+ * arrival bins tb < T'_l only, its neurons fire at steps t < T'_l, and T2's
+ * alpha index clamps at T'_l.  0 (or T) keeps the context window; pool
+ * layers ignore their entry.  windows == NULL resets every layer.  Setting
+ * every layer to T' gives the same outputs as a context created with T = T'
+ * (with the inputs encoded under the wider window, VDTTFS_ENCODE_TIMES). */
+int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers);
 int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
                            double* bucket_ms, int64_t* bucket_launches);
 

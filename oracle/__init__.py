@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libvdttfs_oracle.so")
 INF = np.float32(9999.0)
 
 ORC_CONV, ORC_FC, ORC_POOL, ORC_VMEM = 0, 1, 2, 3
-ENC_LINEAR, ENC_LOG = 0, 1
+ENC_LINEAR, ENC_LOG, ENC_TIMES = 0, 1, 2
 READ_ARGMIN, READ_ARGMAX, READ_T3 = 0, 1, 2
 
 

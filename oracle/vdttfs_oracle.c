@@ -462,6 +462,7 @@ int orc_net_forward(const orc_consts* c, const orc_layer* layers, int n_layers, 
     }
     int64_t n_img = (int64_t)B * img_elems_per_image;
     if (encode_mode == ORC_ENC_LOG) orc_encode_log(img, cur, n_img, tc_in, td_in, c->T);
+    else if (encode_mode == ORC_ENC_TIMES) memcpy(cur, img, sizeof(float) * (size_t)n_img);
     else orc_encode_linear(img, cur, n_img, c->T);
 
     float tc_i = tc_in, td_i = td_in;

@@ -113,7 +113,8 @@ void orc_readout_t3(const float* out, int B, int C, int32_t* pred);
 
 /* ---- network runner (the driver main()s: T1V:286-319, T2V:337-396) ---- */
 enum { ORC_CONV = 0, ORC_FC = 1, ORC_POOL = 2, ORC_VMEM = 3 };
-enum { ORC_ENC_LINEAR = 0, ORC_ENC_LOG = 1 };
+/* ORC_ENC_TIMES: the input already holds spike times (copied unchanged) */
+enum { ORC_ENC_LINEAR = 0, ORC_ENC_LOG = 1, ORC_ENC_TIMES = 2 };
 enum { ORC_READ_ARGMIN = 0, ORC_READ_ARGMAX = 1, ORC_READ_T3 = 2 };
 
 typedef struct orc_layer {

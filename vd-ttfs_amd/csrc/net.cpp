@@ -28,6 +28,7 @@ struct NetLayer {
     int cin_col = 0;   // elements per column
     int64_t list_cap = 0;  // merged-list entries per output pixel
     int t_min = 0;
+    int window = 0;  // integration window T'_l; 0 = the context's T
 };
 
 struct TimedPair {
@@ -121,20 +122,49 @@ int mark(vdttfs_net* net, hipEvent_t* e) {
     return VDTTFS_OK;
 }
 
+// Narrows the context's integration window to T' for one layer's launches
+// and restores it on exit.  The launchers read the window from the context,
+// and the LUT entries they index under T' (alpha[0..T'], theta[0..T'-1]) are
+// functions of t alone, so the layer's full-window LUTs serve unchanged.
+class WindowScope {
+  public:
+    WindowScope(vdttfs_ctx* ctx, int window) : ctx_(ctx), T_(ctx->c.T), NC_(ctx->NC), OS_(ctx->OS) {
+        if (window > 0 && window < T_) {
+            ctx->c.T = window;
+            ctx->NC = (window + ctx->c.delta - 1) / ctx->c.delta;
+            ctx->OS = ctx->NC + 1;
+        }
+    }
+    ~WindowScope() {
+        ctx_->c.T = T_;
+        ctx_->NC = NC_;
+        ctx_->OS = OS_;
+    }
+    WindowScope(const WindowScope&) = delete;
+    WindowScope& operator=(const WindowScope&) = delete;
+
+  private:
+    vdttfs_ctx* ctx_;
+    int T_, NC_, OS_;
+};
+
 // counters: nullable; when set, per-layer instrumented run
 int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t* eproc,
                  uint64_t* ebin, uint64_t* n_ev, uint64_t* n_cols) {
     vdttfs_ctx* ctx = net->ctx;
     const bool count = eproc || ebin || n_ev;
     const int64_t n_img = (int64_t)net->B * net->img_elems;
+    const float* cur = net->enc;
     if (net->encode_mode == VDTTFS_ENCODE_LOG)
         VD_TRY(launch_encode_log(ctx, d_img, net->enc, n_img, net->tc_in, net->td_in));
-    else
+    else if (net->encode_mode == VDTTFS_ENCODE_LINEAR)
         VD_TRY(launch_encode_linear(ctx, d_img, net->enc, n_img));
-    const float* cur = net->enc;
+    else
+        cur = d_img;  // VDTTFS_ENCODE_TIMES: the input already holds spike times
     for (size_t i = 0; i < net->L.size(); ++i) {
         NetLayer& l = net->L[i];
         const vdttfs_layer_desc& d = l.d;
+        WindowScope window(ctx, l.window);
         if (d.kind == VDTTFS_LAYER_POOL) {
             VD_TRY(launch_pool_min(ctx, cur, l.out, net->B, d.H_in, d.W_in, d.C_in));
         } else if (d.kind == VDTTFS_LAYER_VMEM) {
@@ -327,7 +357,8 @@ int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_la
     if (!out || !layers || n_layers <= 0 || B <= 0 || img_elems <= 0)
         return set_error(VDTTFS_E_INVALID, "net_create: bad argument");
     *out = nullptr;
-    if (encode_mode != VDTTFS_ENCODE_LINEAR && encode_mode != VDTTFS_ENCODE_LOG)
+    if (encode_mode != VDTTFS_ENCODE_LINEAR && encode_mode != VDTTFS_ENCODE_LOG &&
+        encode_mode != VDTTFS_ENCODE_TIMES)
         return set_error(VDTTFS_E_INVALID, "net_create: encode mode %d", encode_mode);
     if (readout != VDTTFS_READOUT_ARGMIN && readout != VDTTFS_READOUT_ARGMAX &&
         readout != VDTTFS_READOUT_ARGMIN_FIRST)
@@ -391,6 +422,24 @@ int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint6
 int vdttfs_net_set_timing(vdttfs_net* net, int enable) {
     if (!net) return set_error(VDTTFS_E_INVALID, "null net");
     net->timing = enable != 0;
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    const int n = (int)net->L.size();
+    if (windows && n_layers != n)
+        return set_error(VDTTFS_E_INVALID, "net_set_windows: %d windows for %d layers", n_layers, n);
+    const int T = net->ctx->c.T;
+    if (windows)
+        for (int i = 0; i < n; ++i)
+            if (net->L[i].d.kind != VDTTFS_LAYER_POOL && (windows[i] < 0 || windows[i] > T))
+                return set_error(VDTTFS_E_INVALID, "net_set_windows: layer %d window %d outside [0, %d]", i,
+                                 windows[i], T);
+    for (int i = 0; i < n; ++i) {
+        const int w = windows && net->L[i].d.kind != VDTTFS_LAYER_POOL ? windows[i] : 0;
+        net->L[i].window = w == T ? 0 : w;
+    }
     return VDTTFS_OK;
 }
 

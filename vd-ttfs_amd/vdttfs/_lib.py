@@ -24,7 +24,7 @@ E_NODEVICE = -7
 INF_TIME = 9999.0
 
 LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM = 0, 1, 2, 3
-ENCODE_LINEAR, ENCODE_LOG = 0, 1
+ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES = 0, 1, 2
 READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
 STEP_T1, STEP_T2 = 1, 2
@@ -169,6 +169,7 @@ SIGNATURES = {
     "vdttfs_stepnet_output": [_vp, C.POINTER(_vp), C.POINTER(_i64), C.POINTER(_i)],
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
+    "vdttfs_net_set_windows": [_vp, _vp, _i],
     "vdttfs_net_read_timing": [_vp, C.POINTER(C.c_double), C.POINTER(_i64),
                                C.POINTER(C.c_double), C.POINTER(_i64)],
     "vdttfs_synth_uniform": [C.c_uint64, C.c_uint64, _vp, _i64],

@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
-                   LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG,
+                   LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES,
                    READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
                    CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2)
 
@@ -321,6 +321,15 @@ class Net:
 
     def set_timing(self, on: bool):
         check(lib().vdttfs_net_set_timing(self.handle, int(on)))
+
+    def set_windows(self, windows=None):
+        """Per-layer integration windows T'_l (vdttfs_net_set_windows): one
+        entry per layer, 0 or T for the full window, pools ignored; None resets."""
+        if windows is None:
+            check(lib().vdttfs_net_set_windows(self.handle, None, 0))
+            return
+        w = np.ascontiguousarray(windows, np.int32)
+        check(lib().vdttfs_net_set_windows(self.handle, _ptr(w), int(w.size)))
 
     def read_timing(self):
         im, bm = C.c_double(), C.c_double()
