@@ -349,6 +349,9 @@ def main() -> int:
     ap.add_argument("--delta", type=int, default=None,
                     help="default: 8 (vgg16), 16 (lenet5), 32 (culif7)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--plans", default=None,
+                    help="vgg16/lenet5: per-layer launch plans written by python -m vdttfs.tune --out "
+                         "(default: the library's built-in choice)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size copy used to scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -358,6 +361,9 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.plans and args.workload not in ("vgg16", "lenet5"):
+        print(f"--plans applies to the vgg16 and lenet5 engine workloads, not {args.workload}", file=sys.stderr)
+        return 2
     if args.workload == "culif7":
         return bench_culif(args)
     if args.workload == "fc-sweep":
@@ -455,10 +461,13 @@ def bench_ttfs(args) -> int:
     img = models.images_for(w, B)
     ctx = vdttfs.Context(w.consts, 0)
     net = vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
+    if args.plans:
+        from vdttfs import tune
+        tune.apply_plans(net, tune.load_plans(args.plans, w, B))
     d_img = ctx.to_device(img)
     d_pred = ctx.empty(B, np.int32)
     log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
-        f"params={w.n_params}")
+        f"params={w.n_params} plans={args.plans or 'built-in'}")
 
     for _ in range(args.warmup):
         net.forward(d_img, d_pred)
@@ -507,7 +516,8 @@ def bench_ttfs(args) -> int:
         "config": {"workload": workload,
                    "key": key,
                    "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
-                   "seed": w.seed, "parallelism": "none (one GPU)"},
+                   "seed": w.seed, "parallelism": "none (one GPU)",
+                   "plans": os.path.relpath(args.plans, ROOT) if args.plans else "built-in"},
         "roofline": {
             "bound": "hbm",
             "achieved": achieved,

@@ -246,6 +246,43 @@ int vdttfs_net_set_timing(vdttfs_net* net, int enable);
  * every layer to T' gives the same outputs as a context created with T = T'
  * (with the inputs encoded under the wider window, VDTTFS_ENCODE_TIMES). */
 int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers);
+
+/* Per-layer launch plans of the integrator.  No counterpart in the
+ * reference: its one granularity knob is the compile-time chunk width Delta,
+ * chosen per task by a sweep (CHUNK_SELECTION.md:44-62).  This engine's
+ * results do not depend on Delta (one-step bins), and its launch choices per
+ * layer are these; every plan gives bit-identical results.  Fields: 0 = the
+ * built-in choice.
+ *   path:   VDTTFS_PATH_BINS (bucketize + per-pixel merge), VDTTFS_PATH_DENSE
+ *           (merge straight from the spike map; conv layers with <= 9 taps,
+ *           C_in <= 64, or narrow layers with <= 25 taps), VDTTFS_PATH_FUSED
+ *           (merge and integrate in one kernel, the list kept in LDS; dense
+ *           layers with C_out <= 64, T <= 64, gather 1)
+ *   gather: 1 one c_out per lane; 2 two events per 16-byte load (C_out a
+ *           multiple of 4 and <= 128); 4 four c_out per lane (C_out a
+ *           multiple of 4)
+ *   ppw:    output pixels per wave, 1..8
+ * Layers with C_out < 32 run one pixel per C_out lanes (gather 1, ppw =
+ * 64 / C_out, paths BINS or DENSE); layers outside the merged-list limits
+ * (> 25 taps) take the generic integrator (path BINS, gather and ppw 0).
+ * Pool and vmem layers have no plan.  set_plan(NULL) restores the built-in
+ * choice; an unsupported request fails with VDTTFS_E_UNSUPPORTED and leaves
+ * the layer's plan unchanged.  get_plan returns the resolved plan the next
+ * forward uses. */
+#define VDTTFS_PATH_AUTO  0
+#define VDTTFS_PATH_BINS  1
+#define VDTTFS_PATH_DENSE 2
+#define VDTTFS_PATH_FUSED 3
+typedef struct vdttfs_layer_plan {
+    int32_t path, gather, ppw;
+} vdttfs_layer_plan;
+int vdttfs_net_set_plan(vdttfs_net* net, int layer, const vdttfs_layer_plan* plan);
+int vdttfs_net_get_plan(vdttfs_net* net, int layer, vdttfs_layer_plan* out);
+/* Per-layer event time (bucketize + integrator launches, ms) summed over the
+ * timed forwards since the last read (timing enabled with
+ * vdttfs_net_set_timing); ms has n_layers entries, pools and vmem read 0.
+ * Resets the per-layer sums; vdttfs_net_read_timing keeps its own totals. */
+int vdttfs_net_read_layer_timing(vdttfs_net* net, double* ms, int n_layers);
 int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
                            double* bucket_ms, int64_t* bucket_launches);
 

@@ -1,0 +1,179 @@
+"""Launch plans (vdttfs_net_set_plan) and the granularity tuner: the
+built-in plan of each layer, rejection of plans the kernels cannot run,
+bit-exact outputs and equal work counts under every plan the kernels accept
+(against the oracle), and the tuner's Delta sweep and plan sweep."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import vdttfs
+from vdttfs import models, tune
+
+pytestmark = pytest.mark.gpu
+
+BINS, DENSE, FUSED = vdttfs.PATH_BINS, vdttfs.PATH_DENSE, vdttfs.PATH_FUSED
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_net(ctx, w, B):
+    return vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
+
+
+def test_builtin_plans_and_rejections(gpu_ctx_factory):
+    say("plans: VGG-16 B=16 built-in choices and rejections")
+    w = models.vgg16()
+    ctx = gpu_ctx_factory(w.consts)
+    net = make_net(ctx, w, 16)
+    try:
+        got = [net.get_plan(i) for i in range(len(w.layers))]
+        exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (DENSE, 2, 1), 4: (BINS, 2, 1), 6: (BINS, 4, 1),
+               10: (BINS, 4, 1), 16: (BINS, 4, 1), 18: (BINS, 4, 1)}
+        for i, p in exp.items():
+            assert got[i] == p, f"layer {i}: {got[i]}"
+        assert got[2] == (0, 0, 0) and got[19] == (0, 0, 0)  # pool, vmem
+        bad = [(18, FUSED, 0, 0),   # FC layers have no dense path
+               (10, 0, 2, 0),       # two events per load cover <= 128 c_out
+               (0, 0, 0, 9),        # at most 8 pixels per wave
+               (0, 4, 0, 0),        # unknown path
+               (4, DENSE, 0, 0),    # dense merge needs C_in <= 64
+               (1, FUSED, 4, 0),    # the fused kernel gathers one c_out per lane
+               (3, FUSED, 0, 0),    # ... and C_out <= 64
+               (0, 0, 3, 0),        # gather is 1, 2 or 4
+               (2, BINS, 0, 0)]     # pools have no integrator
+        net.set_plan(3, BINS, 1, 2)
+        for layer, path, gather, ppw in bad:
+            with pytest.raises(vdttfs.VdttfsError):
+                net.set_plan(layer, path, gather, ppw)
+        assert net.get_plan(3) == (BINS, 1, 2)  # a rejected request changes nothing
+        net.set_plan(3)
+        assert net.get_plan(3) == (DENSE, 2, 1)
+        net.set_plan(2)  # an empty plan on a pool is accepted
+    finally:
+        net.close()
+    w = models.lenet5()
+    ctx = gpu_ctx_factory(w.consts)
+    net = make_net(ctx, w, 16)
+    try:
+        assert net.get_plan(0) == (DENSE, 1, 10)   # C_out 6: 10 pixels per wave
+        assert net.get_plan(6) == (BINS, 1, 6)     # FC 84 -> 10
+        assert net.get_plan(4) == (BINS, 2, 1)     # FC 256 -> 120
+        with pytest.raises(vdttfs.VdttfsError):
+            net.set_plan(0, 0, 0, 2)
+        with pytest.raises(vdttfs.VdttfsError):
+            net.set_plan(0, FUSED)
+        net.set_plan(0, BINS)
+        assert net.get_plan(0) == (BINS, 1, 10)
+    finally:
+        net.close()
+
+
+def sweep_all_plans(ctx, w, B, img, ref, check_counts):
+    """Round r sets layer i to its (r mod n_i)-th accepted plan, so every plan
+    of every layer runs, in mixed settings; each round equals the oracle."""
+    net = make_net(ctx, w, B)
+    try:
+        cands = {i: tune.candidates(net, i) for i, l in enumerate(w.layers)
+                 if l.kind in (vdttfs.LAYER_CONV, vdttfs.LAYER_FC)}
+        rounds = max(len(c) for c in cands.values())
+        d_img = ctx.to_device(img)
+        d_pred = ctx.empty(B, np.int32)
+        for r in range(rounds):
+            for i, c in cands.items():
+                net.set_plan(i, *c[r % len(c)])
+            net.forward(d_img, d_pred)
+            ctx.synchronize()
+            for i, (l, o) in enumerate(zip(w.layers, ref["outs"])):
+                g = net.layer_output(i)
+                if l.kind == vdttfs.LAYER_VMEM:
+                    assert np.all(np.abs(g - o) <= 1e-5 * (np.abs(o) + 1e-3)), f"round {r} layer {i}"
+                else:
+                    assert np.array_equal(g, o), (f"round {r} layer {i} plan {net.get_plan(i)} differs at "
+                                                  f"{np.flatnonzero(g != o)[:8]}")
+            np.testing.assert_array_equal(d_pred.download(), ref["pred"])
+            if check_counts and r % 3 == 0:
+                eproc, ebin, _, _ = net.count(d_img)
+                np.testing.assert_array_equal(eproc, ref["eproc"], err_msg=f"round {r}")
+                np.testing.assert_array_equal(ebin, ref["ebin"], err_msg=f"round {r}")
+        d_img.free()
+        d_pred.free()
+        return {i: len(c) for i, c in cands.items()}
+    finally:
+        net.close()
+
+
+def oracle_ref(w, B, img):
+    return oracle.net_forward(oracle.Consts.from_task(w.consts), w.layers, B, img, w.img_elems,
+                              oracle.ENC_LINEAR, w.tc_in, w.td_in,
+                              oracle.READ_ARGMAX if w.readout == vdttfs.READOUT_ARGMAX else oracle.READ_ARGMIN,
+                              same_pad=bool(w.consts.conv_same_pad), keep_layers=True)
+
+
+def test_every_plan_matches_oracle_vgg(gpu_ctx_factory):
+    say("plans: VGG-16 B=16, every accepted plan of every layer vs oracle")
+    w = models.vgg16()
+    B = 16
+    img = models.images_for(w, B)
+    ref = oracle_ref(w, B, img)
+    n = sweep_all_plans(gpu_ctx_factory(w.consts), w, B, img, ref, check_counts=True)
+    assert n[0] >= 10 and n[10] == 6 and n[18] == 6
+
+
+def test_every_plan_matches_oracle_lenet(gpu_ctx_factory):
+    say("plans: LeNet-5 B=256, every accepted plan of every layer vs oracle")
+    w = models.lenet5()
+    B = 256
+    img = models.images_for(w, B)
+    ref = oracle_ref(w, B, img)
+    n = sweep_all_plans(gpu_ctx_factory(w.consts), w, B, img, ref, check_counts=True)
+    assert n[0] == 2 and n[6] == 1
+
+
+def test_tuner_lenet(gpu_ctx_factory):
+    say("tuner: LeNet-5 B=64 Delta sweep and plan sweep")
+    w = models.lenet5()
+    B = 64
+    img = models.images_for(w, B)
+    rows = tune.delta_sweep(w, img, B, (8, 16, 32), reps=1, rounds=1)
+    assert rows[0]["identical_to_first"] is None
+    assert all(r["identical_to_first"] for r in rows[1:])
+    assert all(r["ms_per_batch"] > 0 for r in rows)
+    r = tune.tune_plans(w, img, B, reps=1, rounds=1)
+    assert r["tuned_identical"]
+    assert [L["layer"] for L in r["layers"]] == [0, 2, 4, 5, 6]
+    for L in r["layers"]:
+        assert L["all_identical"] and L["best"] is not None
+        assert L["best"]["ms"] <= min(c["ms"] for c in L["candidates"]) + 1e-12
+    assert r["plans"][1] is None and r["plans"][0]["path"] in ("bins", "dense")
+
+
+def test_committed_vgg_plans_bit_identical(gpu_ctx_factory):
+    """The tuned plan file that bench.py --plans applies changes no output bit
+    at the benchmark size."""
+    import os
+
+    say("plans: VGG-16 B=256 committed tuned plans vs built-in")
+    w = models.vgg16()
+    B = 256
+    ctx = gpu_ctx_factory(w.consts)
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "configs",
+                        "plans_vgg16_b256.json")
+    img = ctx.to_device(models.images_for(w, B))
+    d_pred = ctx.empty(B, np.int32)
+    net = make_net(ctx, w, B)
+    try:
+        net.forward(img, d_pred)
+        ctx.synchronize()
+        ref = [net.layer_output(i) for i in range(len(w.layers))]
+        tune.apply_plans(net, tune.load_plans(path, w, B))
+        net.forward(img, d_pred)
+        ctx.synchronize()
+        for i in range(len(w.layers)):
+            assert np.array_equal(net.layer_output(i), ref[i]), f"layer {i}"
+    finally:
+        net.close()

@@ -103,6 +103,20 @@ struct IntegShape {
 };
 // Entries per pixel of the merged event list (receptive events + padding).
 int merged_list_cap(const IntegShape& s);
+// Launch choices of one layer on the merged-list integrator (0 = the
+// built-in choice): the list path (bucketize + k_merge, k_merge_dense, or
+// the fused k_stream_dense), the weight gather (1: one c_out per lane, 2: two
+// events per dwordx4 load, 4: four c_out per lane) and output pixels per
+// wave.  Values as VDTTFS_PATH_* / vdttfs_layer_plan.
+struct LaunchPlan {
+    int path = 0, gather = 0, ppw = 0;
+};
+constexpr int kMaxPixPerWave = 8;
+// Fills every field of *out: a requested field is checked against the
+// layer's shape (VDTTFS_E_UNSUPPORTED when the kernels cannot run it), a zero
+// field takes the built-in choice.
+int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& s, const LaunchPlan& req, LaunchPlan* out);
+
 // Engine integrator over the bin layout: merge per pixel, then stream.
 // list/bstart: merged-list scratch of n_pix*list_cap entries and
 // n_pix*(T+1) bin starts.  counters: nullable; [0] += eproc, [1] += ebin.
@@ -110,7 +124,8 @@ int merged_list_cap(const IntegShape& s);
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
                           int2* list, int64_t list_cap, int32_t* bstart, const float* W,
                           const float* bias, const float* theta, int t_min, const IntegShape& s,
-                          unsigned long long* counters, const CulifNeuron* culif = nullptr);
+                          unsigned long long* counters, const CulifNeuron* culif = nullptr,
+                          const LaunchPlan* plan = nullptr);
 // Conv layers of the merged-list path: the merged lists are built straight
 // from the dense spike map d_in (no bucketize pass); alpha is the layer's
 // decay LUT.  Same results as bucketize + launch_integrate_bins.
@@ -118,7 +133,8 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& s);
 int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
                            int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
                            const float* theta, int t_min, const IntegShape& s,
-                           unsigned long long* counters, const CulifNeuron* culif = nullptr);
+                           unsigned long long* counters, const CulifNeuron* culif = nullptr,
+                           const LaunchPlan* plan = nullptr);
 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
 int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,

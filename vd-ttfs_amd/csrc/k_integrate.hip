@@ -1123,15 +1123,12 @@ int64_t n_pixels(const IntegShape& sh) {
     return (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out);
 }
 
-// Gather mode of a layer: vec c_out per lane, epi events per load.
-//  64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load (PairGather);
-//  wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block.
-//  C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
-//  events per load there, as lanes whose neurons fired skip their loads.
+// Kernel arguments of a layer's stream; vec c_out per lane and epi events
+// per load follow the plan's gather (1: 1/1, 2: 2/2, 4: 4/1).
 StreamArgs stream_args(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
                        const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
                        const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif,
-                       int* vec, int* epi) {
+                       const LaunchPlan& p, int* vec, int* epi) {
     StreamArgs a{};
     a.out = out;
     a.list = list;
@@ -1148,30 +1145,21 @@ StreamArgs stream_args(vdttfs_ctx* ctx, float* out, const int2* list, int64_t ca
     a.C_out = sh.C_out;
     a.decay = culif ? culif->decay : 0.0f;
     a.th = culif ? culif->th : 0.0f;
-    *vec = 1;
-    *epi = 1;
-    if (sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 128) {
-        *epi = 2;
-        *vec = 2;
-    } else if (sh.C_out % 4 == 0 && sh.C_out > 128) {
-        *vec = 4;
-    }
+    *vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
+    *epi = p.gather == 2 ? 2 : 1;
     a.n_cblk = *epi > 1 ? 1 : (sh.C_out + 64 * *vec - 1) / (64 * *vec);
     a.w_bytes = (int)wbytes;
-    // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
-    // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
-    // (VGG-16 B=256 at 2, 4, 8 pixels per wave: 30.4K -> 29.3K, 26.0K, 20.0K
-    // images/s; the 2^18-pixel CuLIF conv3: 3.68 -> 3.88 ms)
-    a.ppw = a.n_pix >= (INT64_C(1) << 20) ? 2 : 1;
+    a.ppw = p.ppw > 0 ? p.ppw : 1;
     return a;
 }
 
 int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
                   const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
-                  const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
+                  const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif,
+                  const LaunchPlan& p) {
     int vec, epi;
     const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
-                                     counters, culif, &vec, &epi);
+                                     counters, culif, p, &vec, &epi);
     const int64_t n_pix = a.n_pix;
     const int waves = 4;
     const int64_t n_pg = (n_pix + waves * a.ppw - 1) / (waves * a.ppw);
@@ -1212,7 +1200,7 @@ int launch_stream_narrow(vdttfs_ctx* ctx, float* out, const int2* list, int64_t 
                          const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
     int vec, epi;
     const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
-                                     counters, culif, &vec, &epi);
+                                     counters, culif, LaunchPlan{}, &vec, &epi);
     const int P = 64 / sh.C_out;
     const int64_t waves = (a.n_pix + P - 1) / P;
     const int64_t blocks = (waves + 3) / 4;
@@ -1253,10 +1241,83 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
     return !sh.is_fc && shape_ok && ctx->c.T <= kDenseMaxBins && sh.C_in <= kDenseMaxCin;
 }
 
+namespace {
+
+bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
+    const int nel_max = sh.K_h * sh.K_w * sh.C_in;
+    const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, ctx->c.T) * sizeof(int);
+    return gather == 1 && sh.C_out <= 64 && ctx->c.T <= kBlockBins && lds <= kFusedMaxLds;
+}
+
+int plan_error(const IntegShape& sh, const char* what) {
+    return set_error(VDTTFS_E_UNSUPPORTED, "plan: %s (layer %dx%dx%d -> %d, %dx%d taps%s)", what, sh.H_in, sh.W_in,
+                     sh.C_in, sh.C_out, sh.K_h, sh.K_w, sh.is_fc ? ", fc" : "");
+}
+
+}  // namespace
+
+int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& req, LaunchPlan* out) {
+    if (req.path < 0 || req.path > VDTTFS_PATH_FUSED || req.gather < 0 || req.ppw < 0 || req.ppw > 64)
+        return set_error(VDTTFS_E_INVALID, "plan: path %d, gather %d, ppw %d out of range", req.path,
+                         req.gather, req.ppw);
+    int64_t wbytes;
+    const bool narrow = narrow_path_ok(sh, &wbytes);
+    const bool wave = !narrow && wave_path_ok(sh, &wbytes);
+    const bool dense = integrate_dense_ok(ctx, sh);
+    LaunchPlan p{};
+    if (!narrow && !wave) {  // the generic integrator: nothing to choose
+        if ((req.path && req.path != VDTTFS_PATH_BINS) || req.gather || req.ppw)
+            return plan_error(sh, "the generic integrator has no launch choices");
+        p.path = VDTTFS_PATH_BINS;
+        *out = p;
+        return VDTTFS_OK;
+    }
+    if (narrow) {  // one pixel per C_out lanes
+        const int P = 64 / sh.C_out;
+        if (req.path == VDTTFS_PATH_FUSED || (req.gather && req.gather != 1) || (req.ppw && req.ppw != P))
+            return plan_error(sh, "narrow layers take gather 1, 64 / C_out pixels per wave, paths bins or dense");
+        p.path = req.path ? req.path : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS);
+        if (p.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
+        p.gather = 1;
+        p.ppw = P;
+        *out = p;
+        return VDTTFS_OK;
+    }
+    // gather: 64 < C_out <= 128 (multiple of 4): 2 events per 1 KB load;
+    // wider layers: 4 c_out per lane (dwordx4), 64*4 c_out per block.
+    // C_out <= 64 keeps one dword load per event: measured faster than 2 or 4
+    // events per load there, as lanes whose neurons fired skip their loads.
+    if (req.gather) {
+        if (req.gather != 1 && req.gather != 2 && req.gather != 4) return plan_error(sh, "gather is 1, 2 or 4");
+        if (req.gather != 1 && sh.C_out % 4 != 0) return plan_error(sh, "gather 2 and 4 need C_out % 4 == 0");
+        if (req.gather == 2 && sh.C_out > 128) return plan_error(sh, "gather 2 covers at most 128 c_out");
+        p.gather = req.gather;
+    } else {
+        p.gather = (sh.C_out % 4 == 0 && sh.C_out > 64) ? (sh.C_out <= 128 ? 2 : 4) : 1;
+    }
+    // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
+    // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
+    // (VGG-16 B=256 at 2, 4, 8 pixels per wave: 30.4K -> 29.3K, 26.0K, 20.0K
+    // images/s; the 2^18-pixel CuLIF conv3: 3.68 -> 3.88 ms)
+    if (req.ppw > kMaxPixPerWave) return plan_error(sh, "at most 8 pixels per wave");
+    p.ppw = req.ppw ? req.ppw : (n_pixels(sh) >= (INT64_C(1) << 20) ? 2 : 1);
+    const bool fused = dense && fused_ok(ctx, sh, p.gather);
+    if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
+    if (req.path == VDTTFS_PATH_FUSED && !fused)
+        return plan_error(sh, "fused path needs the dense limits, C_out <= 64, T <= 64 and gather 1");
+    p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
+    *out = p;
+    return VDTTFS_OK;
+}
+
 int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const int32_t* off,
                           int2* list, int64_t list_cap, int32_t* bstart, const float* W,
                           const float* bias, const float* theta, int t_min, const IntegShape& sh,
-                          unsigned long long* counters, const CulifNeuron* culif) {
+                          unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
+    LaunchPlan p;
+    VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
+    if (plan && plan->path && plan->path != VDTTFS_PATH_BINS)
+        return set_error(VDTTFS_E_INVALID, "integrate_bins: the plan asks for a dense path");
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
     if (!narrow && !wave_path_ok(sh, &wbytes)) {
@@ -1299,17 +1360,21 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     VD_HIP(hipGetLastError());
     if (narrow) return launch_stream_narrow(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
                                             counters, culif);
-    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
+    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif, p);
 }
 
 int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
                            int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
                            const float* theta, int t_min, const IntegShape& sh,
-                           unsigned long long* counters, const CulifNeuron* culif) {
+                           unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
     if (!integrate_dense_ok(ctx, sh) || (!narrow && !wave_path_ok(sh, &wbytes)))
         return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
+    LaunchPlan p;
+    VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
+    if (p.path == VDTTFS_PATH_BINS)
+        return set_error(VDTTFS_E_INVALID, "integrate_dense: the plan asks for the bins path");
     const int nk_max = sh.K_h * sh.K_w;
     const int64_t n_pix = n_pixels(sh);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
@@ -1353,10 +1418,10 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     }
     int vec, epi;
     const StreamArgs a = stream_args(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh,
-                                     counters, culif, &vec, &epi);
+                                     counters, culif, p, &vec, &epi);
     const int nel_max = nk_max * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
-    if (vec == 1 && epi == 1 && a.n_cblk == 1 && m.T <= kBlockBins && lds <= kFusedMaxLds) {
+    if (p.path == VDTTFS_PATH_FUSED) {
         // C_out <= 64: build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
 #define VD_LAUNCH_FUSED(C, L)                                                                      \
@@ -1379,7 +1444,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     }
     hipLaunchKernelGGL(k_merge_dense<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream, m);
     VD_HIP(hipGetLastError());
-    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif);
+    return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif, p);
 }
 
 }  // namespace vdttfs

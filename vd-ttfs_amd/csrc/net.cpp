@@ -29,11 +29,13 @@ struct NetLayer {
     int64_t list_cap = 0;  // merged-list entries per output pixel
     int t_min = 0;
     int window = 0;  // integration window T'_l; 0 = the context's T
+    LaunchPlan plan;  // requested launch plan; zero fields = built-in choice
 };
 
 struct TimedPair {
     hipEvent_t a, b;
     int kind;  // 0 integrate, 1 bucketize
+    int layer;
 };
 
 }  // namespace
@@ -57,6 +59,7 @@ struct vdttfs_net {
     std::vector<TimedPair> pending;
     double ms[2] = {0, 0};
     int64_t launches[2] = {0, 0};
+    std::vector<double> layer_ms;
 };
 
 namespace {
@@ -122,6 +125,25 @@ int mark(vdttfs_net* net, hipEvent_t* e) {
     return VDTTFS_OK;
 }
 
+// Integrator shape of a CONV or FC layer (FC: one column of H*W*C inputs).
+IntegShape integ_shape(const vdttfs_net* net, const NetLayer& l) {
+    const vdttfs_layer_desc& d = l.d;
+    const bool fc = d.kind == VDTTFS_LAYER_FC;
+    IntegShape s{};
+    s.B = net->B;
+    s.is_fc = fc;
+    s.H_in = fc ? 1 : d.H_in;
+    s.W_in = fc ? 1 : d.W_in;
+    s.C_in = l.cin_col;
+    s.H_out = fc ? 1 : d.H_out;
+    s.W_out = fc ? 1 : d.W_out;
+    s.C_out = d.C_out;
+    s.K_h = fc ? 1 : d.K_h;
+    s.K_w = fc ? 1 : d.K_w;
+    s.pad = (fc || !net->ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
+    return s;
+}
+
 // Narrows the context's integration window to T' for one layer's launches
 // and restores it on exit.  The launchers read the window from the context,
 // and the LUT entries they index under T' (alpha[0..T'], theta[0..T'-1]) are
@@ -171,25 +193,16 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             VD_TRY(launch_fc_vmem(ctx, cur, l.out, l.W, l.bias, l.alpha, net->B,
                                   d.H_in * d.W_in * d.C_in, d.C_out));
         } else {
-            const bool fc = d.kind == VDTTFS_LAYER_FC;
-            IntegShape s{};
-            s.B = net->B;
-            s.is_fc = fc;
-            s.H_in = fc ? 1 : d.H_in;
-            s.W_in = fc ? 1 : d.W_in;
-            s.C_in = l.cin_col;
-            s.H_out = fc ? 1 : d.H_out;
-            s.W_out = fc ? 1 : d.W_out;
-            s.C_out = d.C_out;
-            s.K_h = fc ? 1 : d.K_h;
-            s.K_w = fc ? 1 : d.K_w;
-            s.pad = (fc || !ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
+            const IntegShape s = integ_shape(net, l);
             if (count) VD_TRY(zero_counters(ctx));
-            // conv layers build their merged lists from the dense map; the
-            // bin-layout bucketize runs for FC layers, and in a counting
-            // forward for its retained-event count
-            const bool dense = integrate_dense_ok(ctx, s);
+            // conv layers of the dense paths build their merged lists from
+            // the dense map; the bin-layout bucketize runs for the bins path,
+            // and in a counting forward for its retained-event count
+            LaunchPlan plan;
+            VD_TRY(resolve_plan(ctx, s, l.plan, &plan));
+            const bool dense = plan.path != VDTTFS_PATH_BINS;
             TimedPair tb{}, ti{};
+            tb.layer = ti.layer = (int)i;
             if (!dense || count) {
                 if (net->timing && !count) VD_TRY(mark(net, &tb.a));
                 VD_TRY(launch_bucketize_bins(ctx, cur, l.cols, l.cin_col, l.alpha, net->ev, net->off,
@@ -206,11 +219,11 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             if (dense)
                 VD_TRY(launch_integrate_dense(ctx, l.out, cur, l.alpha, net->list, l.list_cap,
                                               net->bstart, l.W, l.bias, l.theta, l.t_min, s,
-                                              count ? ctx->d_counters : nullptr));
+                                              count ? ctx->d_counters : nullptr, nullptr, &plan));
             else
                 VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
                                              net->bstart, l.W, l.bias, l.theta, l.t_min, s,
-                                             count ? ctx->d_counters : nullptr));
+                                             count ? ctx->d_counters : nullptr, nullptr, &plan));
             if (net->timing && !count) {
                 VD_TRY(mark(net, &ti.b));
                 ti.kind = 0;
@@ -348,6 +361,27 @@ int validate_layer_table(const vdttfs_consts& c, const vdttfs_layer_desc* layers
 }
 }  // namespace vdttfs
 
+namespace {
+
+// Waits for the stream and moves the pending event pairs into the totals.
+int drain_timing(vdttfs_net* net) {
+    VD_TRY(check_ctx(net->ctx));
+    VD_HIP(hipStreamSynchronize(net->ctx->stream));
+    if (net->layer_ms.size() != net->L.size()) net->layer_ms.assign(net->L.size(), 0.0);
+    for (const TimedPair& p : net->pending) {
+        float ms = 0;
+        VD_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+        net->ms[p.kind] += ms;
+        net->launches[p.kind] += 1;
+        net->layer_ms[p.layer] += ms;
+    }
+    net->pending.clear();
+    net->pool_used = 0;
+    return VDTTFS_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int vdttfs_net_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
@@ -443,19 +477,57 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
     return VDTTFS_OK;
 }
 
+int vdttfs_net_set_plan(vdttfs_net* net, int layer, const vdttfs_layer_plan* plan) {
+    if (!net || layer < 0 || layer >= (int)net->L.size())
+        return set_error(VDTTFS_E_INVALID, "net_set_plan: bad argument");
+    NetLayer& l = net->L[layer];
+    const bool integ = l.d.kind == VDTTFS_LAYER_CONV || l.d.kind == VDTTFS_LAYER_FC;
+    LaunchPlan req{};
+    if (plan) {
+        req.path = plan->path;
+        req.gather = plan->gather;
+        req.ppw = plan->ppw;
+    }
+    if (!integ) {
+        if (req.path || req.gather || req.ppw)
+            return set_error(VDTTFS_E_UNSUPPORTED, "net_set_plan: layer %d has no integrator", layer);
+        return VDTTFS_OK;
+    }
+    LaunchPlan resolved;
+    VD_TRY(resolve_plan(net->ctx, integ_shape(net, l), req, &resolved));
+    l.plan = req;
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_get_plan(vdttfs_net* net, int layer, vdttfs_layer_plan* out) {
+    if (!net || !out || layer < 0 || layer >= (int)net->L.size())
+        return set_error(VDTTFS_E_INVALID, "net_get_plan: bad argument");
+    const NetLayer& l = net->L[layer];
+    *out = vdttfs_layer_plan{0, 0, 0};
+    if (l.d.kind != VDTTFS_LAYER_CONV && l.d.kind != VDTTFS_LAYER_FC) return VDTTFS_OK;
+    vdttfs_ctx* ctx = net->ctx;
+    WindowScope window(ctx, l.window);
+    LaunchPlan p;
+    VD_TRY(resolve_plan(ctx, integ_shape(net, l), l.plan, &p));
+    *out = vdttfs_layer_plan{p.path, p.gather, p.ppw};
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_read_layer_timing(vdttfs_net* net, double* ms, int n_layers) {
+    if (!net || !ms || n_layers != (int)net->L.size())
+        return set_error(VDTTFS_E_INVALID, "net_read_layer_timing: bad argument");
+    VD_TRY(drain_timing(net));
+    for (int i = 0; i < n_layers; ++i) {
+        ms[i] = net->layer_ms[i];
+        net->layer_ms[i] = 0.0;
+    }
+    return VDTTFS_OK;
+}
+
 int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_launches,
                            double* bucket_ms, int64_t* bucket_launches) {
     if (!net) return set_error(VDTTFS_E_INVALID, "null net");
-    VD_TRY(check_ctx(net->ctx));
-    VD_HIP(hipStreamSynchronize(net->ctx->stream));
-    for (const TimedPair& p : net->pending) {
-        float ms = 0;
-        VD_HIP(hipEventElapsedTime(&ms, p.a, p.b));
-        net->ms[p.kind] += ms;
-        net->launches[p.kind] += 1;
-    }
-    net->pending.clear();
-    net->pool_used = 0;
+    VD_TRY(drain_timing(net));
     if (integ_ms) *integ_ms = net->ms[0];
     if (integ_launches) *integ_launches = net->launches[0];
     if (bucket_ms) *bucket_ms = net->ms[1];

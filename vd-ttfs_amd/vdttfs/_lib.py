@@ -28,6 +28,7 @@ ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES = 0, 1, 2
 READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
 STEP_T1, STEP_T2 = 1, 2
+PATH_AUTO, PATH_BINS, PATH_DENSE, PATH_FUSED = 0, 1, 2, 3
 
 
 class VdttfsError(RuntimeError):
@@ -102,6 +103,10 @@ class LayerDesc(C.Structure):
     ]
 
 
+class LayerPlan(C.Structure):
+    _fields_ = [("path", C.c_int32), ("gather", C.c_int32), ("ppw", C.c_int32)]
+
+
 class CulifLayer(C.Structure):
     _fields_ = [
         ("kind", C.c_int32),
@@ -170,6 +175,9 @@ SIGNATURES = {
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
     "vdttfs_net_set_windows": [_vp, _vp, _i],
+    "vdttfs_net_set_plan": [_vp, _i, _vp],
+    "vdttfs_net_get_plan": [_vp, _i, _vp],
+    "vdttfs_net_read_layer_timing": [_vp, _vp, _i],
     "vdttfs_net_read_timing": [_vp, C.POINTER(C.c_double), C.POINTER(_i64),
                                C.POINTER(C.c_double), C.POINTER(_i64)],
     "vdttfs_synth_uniform": [C.c_uint64, C.c_uint64, _vp, _i64],

@@ -17,7 +17,8 @@ import numpy as np
 from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
                    LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES,
                    READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
-                   CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2)
+                   CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2, LayerPlan, PATH_AUTO, PATH_BINS, PATH_DENSE,
+                   PATH_FUSED)
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -330,6 +331,24 @@ class Net:
             return
         w = np.ascontiguousarray(windows, np.int32)
         check(lib().vdttfs_net_set_windows(self.handle, _ptr(w), int(w.size)))
+
+    def set_plan(self, layer: int, path: int = 0, gather: int = 0, ppw: int = 0):
+        """Launch plan of one layer (vdttfs_net_set_plan); all zeros restores
+        the built-in choice."""
+        pl = LayerPlan(path, gather, ppw)
+        check(lib().vdttfs_net_set_plan(self.handle, layer, C.byref(pl)))
+
+    def get_plan(self, layer: int) -> tuple:
+        """(path, gather, ppw) the next forward uses for the layer."""
+        pl = LayerPlan()
+        check(lib().vdttfs_net_get_plan(self.handle, layer, C.byref(pl)))
+        return pl.path, pl.gather, pl.ppw
+
+    def read_layer_timing(self) -> np.ndarray:
+        """Per-layer event ms since the last read (timing must be enabled)."""
+        ms = np.zeros(len(self.layers), np.float64)
+        check(lib().vdttfs_net_read_layer_timing(self.handle, _ptr(ms), len(self.layers)))
+        return ms
 
     def read_timing(self):
         im, bm = C.c_double(), C.c_double()
