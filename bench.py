@@ -343,7 +343,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="vgg16",
-                    choices=["vgg16", "lenet5", "culif7", "fc-sweep", "vgg16-timedriven", "lenet5-timedriven"])
+                    choices=["vgg16", "lenet5", "culif7", "fc-sweep", "vgg16-timedriven", "lenet5-timedriven",
+                             "culif7-timedriven"])
     ap.add_argument("--batch", type=int, default=None,
                     help="default: 256 (vgg16), 1024 (lenet5), 64 (culif7), 512 (fc-sweep)")
     ap.add_argument("--delta", type=int, default=None,
@@ -384,6 +385,8 @@ def bench_timedriven(args) -> int:
     import vdttfs
     from vdttfs import models
 
+    if args.workload.startswith("culif7"):
+        return bench_timedriven_culif(args)
     vgg = args.workload.startswith("vgg16")
     B = args.batch or (256 if vgg else 1024)
     w = models.vgg16(delta=args.delta or 8) if vgg else models.lenet5(delta=args.delta or 16)
@@ -435,6 +438,69 @@ def bench_timedriven(args) -> int:
                    "batch": B, "T": w.consts.T, "tfs": w.consts.tfs, "global_steps": n_steps,
                    "parallelism": "none (one GPU)"},
         "event_driven_images_per_s": B / (ms_ev * 1e-3),
+        "event_driven_ms_per_step": ms_ev,
+        "speedup_event_driven": ms_td / ms_ev,
+        "prediction_agreement": float(np.mean(pred_td == pred_ev)),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_timedriven_culif(args) -> int:
+    """Config 4's denominator: the step-by-step CuLIF network of T3S (every
+    layer dense at every step, fire-once CuIF neurons), against the
+    event-driven CuLIF engine on the same event tensor in the same process.
+    Both run the same neuron; only fp32 summation order differs (T3S sums a
+    conv over c_in outermost), so predictions agree up to threshold ties."""
+    import vdttfs
+    from vdttfs import models
+
+    B = args.batch or 64
+    w = models.culif7(delta=args.delta or 32)
+    ev = models.dvs_events(w, B)
+    ctx = vdttfs.Context(w.consts, 0)
+    d_ev = ctx.to_device(ev)
+    d_pred = ctx.empty(B, np.int32)
+    steps = max(1, min(args.steps, 3))
+    sn = vdttfs.CulifStepNet(ctx, w.layers, B)
+    log(f"bench: {w.name} time-driven (T3S) B={B} T={w.consts.T}, {steps} timed forwards")
+    sn.forward(d_ev, d_pred)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        sn.forward(d_ev, d_pred)
+    ctx.synchronize()
+    ms_td = (time.perf_counter() - t0) * 1000.0 / steps
+    pred_td = d_pred.download()
+    sn.close()
+    net = vdttfs.CulifNet(ctx, w.layers, B)
+    for _ in range(3):
+        net.forward(d_ev, d_pred)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        net.forward(d_ev, d_pred)
+    ctx.synchronize()
+    ms_ev = (time.perf_counter() - t0) * 1000.0 / 20
+    pred_ev = d_pred.download()
+    net.close()
+    ctx.close()
+    out = {
+        "metric": f"samples/sec/GPU for the CuLIF-7 time-driven (step-by-step) baseline bs={B}",
+        "value": B / (ms_td * 1e-3),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 1,
+        "ms_per_step": ms_td,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: the same event tensor and random-init weights as the culif7 workload",
+        "config": {"workload": "CuLIF-7 time-driven baseline (T3S semantics), config 4",
+                   "batch": B, "T": w.consts.T, "global_steps": w.consts.T, "parallelism": "none (one GPU)"},
+        "event_driven_samples_per_s": B / (ms_ev * 1e-3),
         "event_driven_ms_per_step": ms_ev,
         "speedup_event_driven": ms_td / ms_ev,
         "prediction_agreement": float(np.mean(pred_td == pred_ev)),

@@ -302,6 +302,7 @@ int vdttfs_net_read_timing(vdttfs_net* net, double* integ_ms, int64_t* integ_lau
  * vdttfs_net_create; convs use the context's padding rule. */
 #define VDTTFS_STEP_T1 1
 #define VDTTFS_STEP_T2 2
+#define VDTTFS_STEP_T3 3  /* CuLIF network: vdttfs_stepnet_create_culif */
 typedef struct vdttfs_stepnet vdttfs_stepnet;
 int vdttfs_stepnet_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
                           int64_t img_elems, int encode_mode, float tc_in, float td_in, int mode,
@@ -395,6 +396,20 @@ int vdttfs_culif_net_read_timing(vdttfs_culif_net* net, double* ms, int64_t* for
  * events (n_ev) and bucket columns (n_cols); 0 for other layers. */
 int vdttfs_culif_net_count(vdttfs_culif_net* net, const float* d_data, uint64_t* eproc,
                            uint64_t* ebin, uint64_t* n_ev, uint64_t* n_cols);
+
+/* Step-by-step CuLIF baseline, T3S = task3_dvsgesture/stepbystep_cuda/
+ * snn_dvs_stepbystep.cu: for each of the context's T steps (T3S:220-252),
+ * every layer of the same table as vdttfs_culif_net_create computes every
+ * neuron's input current densely from that step's 0/1 spike map (the raw
+ * events for layer 0) -- conv over c_in, ky, kx, FC over inputs ascending,
+ * as fma(in, w, sum); the recurrent FC adds W_rec times its own spikes of
+ * step t-1 -- then runs the CuIF neuron I = fma(I, decay, cur); V += I,
+ * spiking once at V >= th (T3S:119-140).  Runs on the vdttfs_stepnet_*
+ * calls: forward(d_data [B][C_in][H][W][T], d_pred) with the first-spike
+ * readout (argmin from class 0, T3S:274-279); output gives the last layer's
+ * first-spike steps (9999 = none) and T. */
+int vdttfs_stepnet_create_culif(vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n_layers, int B,
+                                vdttfs_stepnet** out);
 
 /* ---- synthetic workloads (counter-mode splitmix64; host) --------------- */
 /* u = (z>>40) * 2^-24 with z = mix(seed + 0x9E3779B97F4A7C15*(stream*2^40+i+1)). */

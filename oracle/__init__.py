@@ -261,6 +261,47 @@ def stepnet_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td
     return {"final": final, "pred": pred, "steps": steps.value}
 
 
+class OrcCulifLayer(C.Structure):
+    _fields_ = [("kind", C.c_int), ("C_in", C.c_int), ("H_in", C.c_int), ("W_in", C.c_int), ("C_out", C.c_int),
+                ("w", C.POINTER(C.c_float)), ("w_rec", C.POINTER(C.c_float)), ("decay", C.c_float),
+                ("th", C.c_float)]
+
+
+def culif_stepnet_forward(layers, data, N, T, keep_layers=False, nthreads=0):
+    """Step-by-step CuLIF baseline (T3S semantics, see
+    orc_culif_stepnet_forward).  layers: vdttfs.CulifLayerSpec-like; data
+    [N][C][H][W][T].  Returns dict(final, pred, outs): first-spike steps of
+    the last layer (and of every layer, NCHW, with keep_layers)."""
+    n = len(layers)
+    arr = (OrcCulifLayer * n)()
+    keep = []
+    fp = C.POINTER(C.c_float)
+    elems = []
+    for i, l in enumerate(layers):
+        w = f32(l.weight) if l.weight is not None else None
+        r = f32(l.weight_rec) if l.weight_rec is not None else None
+        keep += [w, r]
+        arr[i] = OrcCulifLayer(l.kind, l.C_in, l.H_in, l.W_in, l.C_out,
+                               w.ctypes.data_as(fp) if w is not None else fp(),
+                               r.ctypes.data_as(fp) if r is not None else fp(), l.decay, l.th)
+        if l.kind in (3, 4):
+            elems.append(N * l.C_out)
+        elif l.kind == 2:
+            elems.append(N * l.C_in * (l.H_in // 2) * (l.W_in // 2))
+        else:
+            elems.append(N * l.C_out * l.H_in * l.W_in)
+    outs = [np.empty(e, np.float32) for e in elems] if keep_layers else None
+    outs_p = (C.POINTER(C.c_float) * n)(*[o.ctypes.data_as(fp) for o in outs]) if outs else None
+    final = np.empty(elems[-1], np.float32)
+    pred = np.empty(N, np.int32)
+    data = f32(data)
+    rc = lib().orc_culif_stepnet_forward(arr, C.c_int(n), C.c_int(N), _p(data), C.c_int(T), outs_p, _p(final),
+                                         _p(pred), C.c_int(nthreads))
+    if rc != 0:
+        raise RuntimeError(f"orc_culif_stepnet_forward failed: {rc}")
+    return {"final": final, "pred": pred, "outs": outs}
+
+
 # ---- CuLIF set (T3V:30-225) -------------------------------------------------
 def _ci(*xs):
     return [C.c_int(int(x)) for x in xs]

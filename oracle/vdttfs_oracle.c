@@ -949,3 +949,158 @@ float orc_culif_neuron_steps(const float* in, int T, float decay, float th) {
     }
     return ORC_INF;
 }
+
+/* ---- T3S: step-by-step CuLIF baseline ---------------------------------- */
+static int64_t culif_out_elems(const orc_culif_layer* L, int N) {
+    if (L->kind == ORC_CULIF_FC || L->kind == ORC_CULIF_FC_REC) return (int64_t)N * L->C_out;
+    if (L->kind == ORC_CULIF_POOL) return (int64_t)N * L->C_in * (L->H_in / 2) * (L->W_in / 2);
+    return (int64_t)N * L->C_out * L->H_in * L->W_in;
+}
+
+/* conv2d_kernel (T3S:41-68) at step t; raw: the input is data[site*T + t]. */
+static void s3_conv(const orc_culif_layer* L, int N, const float* in, int raw, int T, int t, float* cur,
+                    int nthreads) {
+    const int C_in = L->C_in, C_out = L->C_out, H = L->H_in, W = L->W_in;
+    const int64_t total = (int64_t)N * C_out * H * W;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        const int x = (int)(idx % W), y = (int)((idx / W) % H);
+        const int co = (int)((idx / ((int64_t)W * H)) % C_out);
+        const int64_t n = idx / ((int64_t)C_out * H * W);
+        float sum = 0.0f;
+        for (int c = 0; c < C_in; ++c)
+            for (int ky = 0; ky < 3; ++ky)
+                for (int kx = 0; kx < 3; ++kx) {
+                    const int iy = y + ky - 1, ix = x + kx - 1;
+                    if (iy < 0 || iy >= H || ix < 0 || ix >= W) continue;
+                    const int64_t site = ((n * C_in + c) * H + iy) * (int64_t)W + ix;
+                    const float v = raw ? in[site * T + t] : in[site];
+                    sum = fmaf(v, L->w[(((int64_t)co * C_in + c) * 3 + ky) * 3 + kx], sum);
+                }
+        cur[idx] = sum;
+    }
+}
+
+/* maxpool2d_kernel (T3S:70-94) */
+static void s3_pool(const orc_culif_layer* L, int N, const float* in, float* cur, int nthreads) {
+    const int C = L->C_in, H_in = L->H_in, W_in = L->W_in, H_out = H_in / 2, W_out = W_in / 2;
+    const int64_t total = (int64_t)N * C * H_out * W_out;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        const int xo = (int)(idx % W_out), yo = (int)((idx / W_out) % H_out);
+        const int c = (int)((idx / ((int64_t)W_out * H_out)) % C);
+        const int64_t n = idx / ((int64_t)C * H_out * W_out);
+        float m = -1e9f;
+        for (int dy = 0; dy < 2; ++dy)
+            for (int dx = 0; dx < 2; ++dx)
+                m = fmaxf(m, in[((n * C + c) * H_in + (yo * 2 + dy)) * (int64_t)W_in + (xo * 2 + dx)]);
+        cur[idx] = m;
+    }
+}
+
+/* fc_kernel (T3S:96-109): cur[row][col] = sum_i in[row][i] * w[col][i]; with
+ * add = 1 the sum is added to cur afterwards (add_tensors_kernel, T3S:111-114). */
+static void s3_fc(const float* in, const float* w, float* cur, int N, int in_f, int out_f, int add,
+                  int nthreads) {
+    const int64_t total = (int64_t)N * out_f;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        const int64_t row = idx / out_f;
+        const int col = (int)(idx % out_f);
+        float sum = 0.0f;
+        for (int i = 0; i < in_f; ++i) sum = fmaf(in[row * in_f + i], w[(int64_t)col * in_f + i], sum);
+        cur[idx] = add ? cur[idx] + sum : sum;
+    }
+}
+
+/* cuif_step_kernel (T3S:119-140) */
+static void s3_neuron(const float* cur, float* I, float* V, float* spk, unsigned char* fired, float* ft,
+                      int64_t n, float decay, float th, int t) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float ci = fmaf(I[i], decay, cur[i]);
+        const float cv = V[i] + ci;
+        I[i] = ci;
+        V[i] = cv;
+        if (!fired[i] && cv >= th) {
+            spk[i] = 1.0f;
+            fired[i] = 1;
+            ft[i] = (float)t;
+        } else {
+            spk[i] = 0.0f;
+        }
+    }
+}
+
+int orc_culif_stepnet_forward(const orc_culif_layer* layers, int n_layers, int N, const float* data,
+                              int T, float** layer_outs, float* final_out, int32_t* pred, int nthreads) {
+    if (n_layers <= 0 || N <= 0 || T <= 0 || layers[0].kind != ORC_CULIF_RAW_CONV) return -1;
+    for (int l = 0; l < n_layers; ++l) {
+        const orc_culif_layer* L = &layers[l];
+        if (L->kind < ORC_CULIF_RAW_CONV || L->kind > ORC_CULIF_FC || (l > 0 && L->kind == ORC_CULIF_RAW_CONV))
+            return -1;
+        if (L->kind != ORC_CULIF_POOL && !L->w) return -1;
+        if (L->kind == ORC_CULIF_FC_REC && !L->w_rec) return -1;
+        if (l > 0) {
+            const int64_t prev = culif_out_elems(&layers[l - 1], N) / N;
+            const int64_t need = (int64_t)L->C_in * L->H_in * L->W_in;
+            if (prev != need) return -1;
+        }
+    }
+    float** cur = (float**)calloc(n_layers, sizeof(float*));
+    float** I = (float**)calloc(n_layers, sizeof(float*));
+    float** V = (float**)calloc(n_layers, sizeof(float*));
+    float** spk = (float**)calloc(n_layers, sizeof(float*));
+    float** ft = (float**)calloc(n_layers, sizeof(float*));
+    unsigned char** fired = (unsigned char**)calloc(n_layers, sizeof(void*));
+    int rc = (!cur || !I || !V || !spk || !ft || !fired) ? -2 : 0;
+    for (int l = 0; l < n_layers && rc == 0; ++l) {
+        const int64_t n = culif_out_elems(&layers[l], N);
+        cur[l] = (float*)calloc(n, sizeof(float));
+        I[l] = (float*)calloc(n, sizeof(float));
+        V[l] = (float*)calloc(n, sizeof(float));
+        spk[l] = (float*)calloc(n, sizeof(float));
+        ft[l] = (float*)malloc(sizeof(float) * n);
+        fired[l] = (unsigned char*)calloc(n, 1);
+        if (!cur[l] || !I[l] || !V[l] || !spk[l] || !ft[l] || !fired[l]) rc = -2;
+        else
+            for (int64_t i = 0; i < n; ++i) ft[l][i] = ORC_INF;
+    }
+    for (int t = 0; t < T && rc == 0; ++t) {
+        const float* in = NULL;
+        for (int l = 0; l < n_layers; ++l) {
+            const orc_culif_layer* L = &layers[l];
+            const int64_t n = culif_out_elems(L, N);
+            switch (L->kind) {
+                case ORC_CULIF_RAW_CONV: s3_conv(L, N, data, 1, T, t, cur[l], nthreads); break;
+                case ORC_CULIF_CONV: s3_conv(L, N, in, 0, T, t, cur[l], nthreads); break;
+                case ORC_CULIF_POOL: s3_pool(L, N, in, cur[l], nthreads); break;
+                case ORC_CULIF_FC: s3_fc(in, L->w, cur[l], N, L->C_in, L->C_out, 0, nthreads); break;
+                default: /* FC_REC: spk[l] still holds step t-1 */
+                    s3_fc(in, L->w, cur[l], N, L->C_in, L->C_out, 0, nthreads);
+                    s3_fc(spk[l], L->w_rec, cur[l], N, L->C_out, L->C_out, 1, nthreads);
+                    break;
+            }
+            s3_neuron(cur[l], I[l], V[l], spk[l], fired[l], ft[l], n, L->decay, L->th, t);
+            in = spk[l];
+        }
+    }
+    if (rc == 0) {
+        const orc_culif_layer* last = &layers[n_layers - 1];
+        const int64_t n = culif_out_elems(last, N);
+        for (int l = 0; l < n_layers; ++l)
+            if (layer_outs && layer_outs[l])
+                memcpy(layer_outs[l], ft[l], sizeof(float) * (size_t)culif_out_elems(&layers[l], N));
+        if (final_out) memcpy(final_out, ft[n_layers - 1], sizeof(float) * (size_t)n);
+        if (pred) orc_readout_t3(ft[n_layers - 1], N, (int)(n / N), pred);
+    }
+    for (int l = 0; l < n_layers; ++l) {
+        if (cur) free(cur[l]);
+        if (I) free(I[l]);
+        if (V) free(V[l]);
+        if (spk) free(spk[l]);
+        if (ft) free(ft[l]);
+        if (fired) free(fired[l]);
+    }
+    free(cur); free(I); free(V); free(spk); free(ft); free(fired);
+    return rc;
+}

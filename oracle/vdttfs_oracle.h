@@ -189,6 +189,33 @@ void orc_culif_fc(const int32_t* bcin, const float* btin, const int32_t* boff, f
  * in[t] for t in [0,T); returns first t with V>=th or INF. */
 float orc_culif_neuron_steps(const float* in, int T, float decay, float th);
 
+/* ---- step-by-step CuLIF baseline (T3S =
+ *      task3_dvsgesture/stepbystep_cuda/snn_dvs_stepbystep.cu) ----
+ * For t = 0..T-1 (T3S:220-252), every layer in order: the layer's input
+ * current from that step's input (raw events data[...][t] for the first
+ * layer, else the previous layer's 0/1 spike map), then the CuIF neuron
+ * I = fma(I, decay, cur); V = V + I; spike once at V >= th (T3S:119-140).
+ *   RAW_CONV / CONV (T3S:41-68): 3x3 pad 1, OIHW, sum = fma(in, w, sum) over
+ *     c_in, ky, kx in that order (in-bounds taps only);
+ *   POOL (T3S:70-94): max of the 2x2 window, from -1e9;
+ *   FC (T3S:96-109): sum = fma(in[i], W[o][i], sum) over i ascending;
+ *   FC_REC (T3S:243-247): FC over the input plus, added after, the FC of
+ *     the layer's own spikes of step t-1 through W_rec[o][j].
+ * Kinds as ORC_CULIF_*.  layer_outs[i] (may be NULL, or entries NULL)
+ * receive each layer's first-spike steps (NCHW, 9999 = none), final_out the
+ * last layer's, pred the T3V/T3S readout (argmin from class 0).  Returns 0,
+ * or -1 for an inconsistent table, -2 when out of memory. */
+enum { ORC_CULIF_RAW_CONV = 0, ORC_CULIF_CONV = 1, ORC_CULIF_POOL = 2, ORC_CULIF_FC_REC = 3, ORC_CULIF_FC = 4 };
+typedef struct orc_culif_layer {
+    int kind;
+    int C_in, H_in, W_in, C_out; /* FC: C_in = input features, H_in = W_in = 1 */
+    const float* w;
+    const float* w_rec;
+    float decay, th;
+} orc_culif_layer;
+int orc_culif_stepnet_forward(const orc_culif_layer* layers, int n_layers, int N, const float* data,
+                              int T, float** layer_outs, float* final_out, int32_t* pred, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,3 +92,100 @@ def test_small_vgg_t2s(gpu_ctx_factory):
     o = out.reshape(B, 10)
     assert np.any(o != layers[-1].bias[None, :])
     assert len(np.unique(o[:, 0])) > 1
+
+
+# ---- T3S: the step-by-step CuLIF baseline ----------------------------------
+def _t3s_run(ctx, layers, B, data):
+    sn = vdttfs.CulifStepNet(ctx, layers, B)
+    try:
+        d = ctx.to_device(data)
+        p = ctx.empty(B, np.int32)
+        sn.forward(d, p)
+        ctx.synchronize()
+        out, steps = sn.output()
+        pred = p.download()
+        d.free()
+        p.free()
+    finally:
+        sn.close()
+    return out, pred, steps
+
+
+def _odd_culif_net(rng, T):
+    """Channel counts that are not multiples of 4 (one output per thread) and
+    a 4x4 map (a wave spans several c_out planes)."""
+    from vdttfs.core import CulifLayerSpec
+
+    def kw(*shape):
+        return (rng.standard_normal(shape) * np.sqrt(2.0 / np.prod(shape[1:]))).astype(np.float32)
+
+    d, th = 0.6, 0.5
+    return [CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, 8, 8, 3, kw(3, 2, 3, 3), None, d, th),
+            CulifLayerSpec(vdttfs.CULIF_CONV, 3, 8, 8, 5, kw(5, 3, 3, 3), None, d, th),
+            CulifLayerSpec(vdttfs.CULIF_POOL, 5, 8, 8, 5, None, None, d, th),
+            CulifLayerSpec(vdttfs.CULIF_CONV, 5, 4, 4, 6, kw(6, 5, 3, 3), None, d, th),
+            CulifLayerSpec(vdttfs.CULIF_POOL, 6, 4, 4, 6, None, None, d, th),
+            CulifLayerSpec(vdttfs.CULIF_FC_REC, 24, 1, 1, 7, kw(7, 24), kw(7, 7), d, th),
+            CulifLayerSpec(vdttfs.CULIF_FC, 7, 1, 1, 3, kw(3, 7), None, d, th)]
+
+
+@pytest.mark.parametrize("net", ["culif7-8x8", "odd-channels"])
+def test_culif_t3s_every_layer_vs_oracle(gpu_ctx_factory, net):
+    """Random (non-dyadic) weights: each prefix of the table ends at layer k,
+    so its output is layer k's first-spike map; all equal the oracle's T3S
+    restatement bit for bit, and so do the predictions."""
+    from test_culif_step_oracle import events
+
+    print(f"T3S small CuLIF net {net} vs oracle, every layer", flush=True)
+    rng = np.random.default_rng(7)
+    N, T = 3, 32
+    w = models.culif7(H=8, W=8, T=T, delta=8, n_classes=5, th=0.6)
+    layers = w.layers if net == "culif7-8x8" else _odd_culif_net(rng, T)
+    data = events(rng, N, T, density=0.15)
+    ctx = gpu_ctx_factory(w.consts)
+    ref = oracle.culif_stepnet_forward(layers, data, N, T, keep_layers=True)
+    for k in range(1, len(layers) + 1):
+        out, pred, steps = _t3s_run(ctx, layers[:k], N, data)
+        assert steps == T
+        np.testing.assert_array_equal(out, ref["outs"][k - 1], err_msg=f"layer {k - 1}")
+        assert np.any(out < 9999.0), f"layer {k - 1} never fires"
+    np.testing.assert_array_equal(pred, ref["pred"])
+
+
+def test_culif_t3s_equals_engine_on_exact_sums(gpu_ctx_factory):
+    """Weights and event counts in quarter units make every input current
+    exact, so the time-driven baseline and the event-driven engine must give
+    the same last-layer first spikes and predictions."""
+    from test_culif_step_oracle import events, small_net
+
+    print("T3S vs CuLIF engine on exact sums", flush=True)
+    rng = np.random.default_rng(3)
+    N, T = 4, 32
+    layers = small_net(rng, 0.5, 1.0)
+    data = events(rng, N, T)
+    ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=8))
+    out, pred, _ = _t3s_run(ctx, layers, N, data)
+    net = vdttfs.CulifNet(ctx, layers, N)
+    try:
+        d = ctx.to_device(data)
+        p = ctx.empty(N, np.int32)
+        net.forward(d, p)
+        ctx.synchronize()
+        eng = net.layer_output(len(layers) - 1)
+        np.testing.assert_array_equal(out, eng.ravel())
+        np.testing.assert_array_equal(pred, p.download())
+    finally:
+        net.close()
+
+
+def test_culif_t3s_config4_shapes(gpu_ctx_factory):
+    """The config 4 table at a 32x32 map, B=4, T=32, against the oracle."""
+    print("T3S config 4 table at 32x32 vs oracle", flush=True)
+    w = models.culif7(H=32, W=32, T=32)
+    B = 4
+    data = models.dvs_events(w, B)
+    ctx = gpu_ctx_factory(w.consts)
+    out, pred, _ = _t3s_run(ctx, w.layers, B, data)
+    ref = oracle.culif_stepnet_forward(w.layers, data, B, w.consts.T)
+    np.testing.assert_array_equal(out, ref["final"])
+    np.testing.assert_array_equal(pred, ref["pred"])

@@ -204,6 +204,29 @@ int launch_step_pool(vdttfs_ctx* ctx, const uint8_t* s_in, uint8_t* s_out, uint8
                      int W_in, int C);
 int launch_step_fill(vdttfs_ctx* ctx, float* p, int64_t n, float v);
 
+// Step-by-step CuLIF baseline (T3S semantics): one layer of the time-driven
+// network, NCHW maps.  kind as VDTTFS_CULIF_*; in/out counts per sample:
+// conv C_out*H*W, pool C*(H/2)*(W/2), FC C_out.
+struct Step3Layer {
+    int kind;
+    int C_in, H, W, C_out;
+    const float* weight;      // conv OIHW [C_out][C_in][3][3], FC [in][out] (transposed at creation)
+    const float* weight_rec;  // FC_REC [j][out] (transposed)
+    float* I;
+    float* V;
+    float* s;            // 0/1 spikes of the step (FC_REC: of step t-1 until its neuron runs)
+    uint8_t* fired;
+    float* ft;           // first-spike steps
+    float* cur;          // FC_REC: input current of the step; RAW_CONV: the step's raw events
+    int64_t n;           // neurons
+    float decay, th;
+};
+// Layer checks of vdttfs_culif_net_create (kinds, chained shapes, weights).
+int validate_culif_table(const vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n);
+// One step t of layer L from its input in (RAW_CONV: the event tensor
+// [N][C_in][H][W][T]; else the previous layer's spikes of step t).
+int launch_step3_layer(vdttfs_ctx* ctx, const Step3Layer& L, const float* in, int N, int T, int t);
+
 // shape validation shared by the entry points
 int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s);
 

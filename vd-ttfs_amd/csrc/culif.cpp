@@ -360,6 +360,12 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
 
 }  // namespace
 
+namespace vdttfs {
+int validate_culif_table(const vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n) {
+    return validate(ctx, layers, n);
+}
+}  // namespace vdttfs
+
 extern "C" {
 
 // ---- drop-in entry points (reference layouts) ----------------------------

@@ -1,6 +1,8 @@
 // Step-by-step (time-driven) baseline network (T1S / T2S main loops,
 // T1S:222-244 and T2S:329-352): encode once, then for every global step the
 // input spikes of that step and every layer in order, then the readout.
+// T3S mode (snn_dvs_stepbystep.cu:220-252) steps the CuLIF layer table over
+// the dense event tensor.
 // Weights are uploaded once; spike maps, membrane potentials and fire-once
 // latches live on the device for the batch.
 #include <cmath>
@@ -34,6 +36,9 @@ struct vdttfs_stepnet {
     uint8_t* s0 = nullptr;
     float* out = nullptr;
     int64_t out_elems = 0;
+    // T3S mode: the CuLIF layers and every buffer they own
+    std::vector<Step3Layer> L3;
+    std::vector<void*> bufs3;
 };
 
 namespace {
@@ -47,7 +52,10 @@ void release(vdttfs_stepnet* net) {
     for (StepNetLayer& l : net->L)
         for (void* p : {(void*)l.W, (void*)l.bias, (void*)l.spk, (void*)l.fired, (void*)l.vmem})
             if (p) (void)hipFree(p);
-    for (void* p : {(void*)net->tin, (void*)net->s0, (void*)net->out})
+    for (void* p : {(void*)net->tin, (void*)net->s0})
+        if (p) (void)hipFree(p);
+    if (net->mode != VDTTFS_STEP_T3 && net->out) (void)hipFree(net->out);  // T3S: out is a layer's ft
+    for (void* p : net->bufs3)
         if (p) (void)hipFree(p);
     delete net;
 }
@@ -181,9 +189,122 @@ int forward_impl(vdttfs_stepnet* net, const float* d_img, int32_t* d_pred) {
     return VDTTFS_OK;
 }
 
+// T3S (snn_dvs_stepbystep.cu:173-214): per layer, the CuIF state and the
+// fire-once latch of every neuron, its 0/1 spikes and first-spike steps.
+int create3_impl(vdttfs_stepnet* net, const vdttfs_culif_layer* layers, int n) {
+    const int B = net->B;
+    auto alloc = [&](void** p, size_t bytes) -> int {
+        VD_TRY(dmalloc(p, bytes));
+        net->bufs3.push_back(*p);
+        return VDTTFS_OK;
+    };
+    auto upload3 = [&](const float** dst, const float* src, size_t elems) -> int {
+        float* d = nullptr;
+        VD_TRY(alloc((void**)&d, elems * 4));
+        VD_HIP(hipMemcpy(d, src, elems * 4, hipMemcpyHostToDevice));
+        *dst = d;
+        return VDTTFS_OK;
+    };
+    net->L3.resize(n);
+    for (int i = 0; i < n; ++i) {
+        const vdttfs_culif_layer& d = layers[i];
+        Step3Layer& l = net->L3[i];
+        l = Step3Layer{};
+        l.kind = d.kind;
+        l.C_in = d.C_in;
+        l.H = d.H_in;
+        l.W = d.W_in;
+        l.C_out = d.C_out;
+        l.decay = d.decay;
+        l.th = d.th;
+        const bool fc = d.kind == VDTTFS_CULIF_FC || d.kind == VDTTFS_CULIF_FC_REC;
+        if (fc)
+            l.n = (int64_t)B * d.C_out;
+        else if (d.kind == VDTTFS_CULIF_POOL)
+            l.n = (int64_t)B * d.C_in * (d.H_in / 2) * (d.W_in / 2);
+        else
+            l.n = (int64_t)B * d.C_out * d.H_in * d.W_in;
+        VD_TRY(alloc((void**)&l.I, (size_t)l.n * 4));
+        VD_TRY(alloc((void**)&l.V, (size_t)l.n * 4));
+        VD_TRY(alloc((void**)&l.s, (size_t)l.n * 4));
+        VD_TRY(alloc((void**)&l.ft, (size_t)l.n * 4));
+        VD_TRY(alloc((void**)&l.fired, (size_t)l.n));
+        if (d.kind == VDTTFS_CULIF_POOL) continue;
+        if (!fc) {
+            VD_TRY(upload3(&l.weight, d.weight, (size_t)d.C_out * d.C_in * 9));
+            if (d.kind == VDTTFS_CULIF_RAW_CONV)  // the step's raw events
+                VD_TRY(alloc((void**)&l.cur, (size_t)B * d.C_in * d.H_in * d.W_in * 4));
+            continue;
+        }
+        // FC weights transposed to [in][out]: a wave's threads are
+        // consecutive outputs, so each step of their (unchanged, i-ascending)
+        // sums reads one contiguous row instead of 64 rows far apart
+        std::vector<float> tw((size_t)d.C_out * d.C_in);
+        for (int o = 0; o < d.C_out; ++o)
+            for (int i2 = 0; i2 < d.C_in; ++i2) tw[(size_t)i2 * d.C_out + o] = d.weight[(size_t)o * d.C_in + i2];
+        VD_TRY(upload3(&l.weight, tw.data(), tw.size()));
+        if (d.kind == VDTTFS_CULIF_FC_REC) {
+            std::vector<float> tr((size_t)d.C_out * d.C_out);
+            for (int o = 0; o < d.C_out; ++o)
+                for (int j = 0; j < d.C_out; ++j) tr[(size_t)j * d.C_out + o] = d.weight_rec[(size_t)o * d.C_out + j];
+            VD_TRY(upload3(&l.weight_rec, tr.data(), tr.size()));
+            VD_TRY(alloc((void**)&l.cur, (size_t)l.n * 4));
+        }
+    }
+    net->out = net->L3.back().ft;
+    net->out_elems = net->L3.back().n;
+    net->steps = net->ctx->c.T;
+    return VDTTFS_OK;
+}
+
+// T3S main loop (T3S:220-252), then its first-spike readout (T3S:274-279,
+// argmin from class 0).
+int forward3_impl(vdttfs_stepnet* net, const float* d_data, int32_t* d_pred) {
+    vdttfs_ctx* ctx = net->ctx;
+    for (Step3Layer& l : net->L3) {
+        VD_TRY(launch_step_fill(ctx, l.I, l.n, 0.0f));
+        VD_TRY(launch_step_fill(ctx, l.V, l.n, 0.0f));
+        VD_TRY(launch_step_fill(ctx, l.s, l.n, 0.0f));
+        VD_TRY(launch_step_fill(ctx, l.ft, l.n, kInfTime));
+        VD_HIP(hipMemsetAsync(l.fired, 0, (size_t)l.n, ctx->stream));
+    }
+    const int T = net->steps;
+    for (int t = 0; t < T; ++t) {
+        const float* in = d_data;
+        for (const Step3Layer& l : net->L3) {
+            VD_TRY(launch_step3_layer(ctx, l, in, net->B, T, t));
+            in = l.s;
+        }
+    }
+    if (d_pred) VD_TRY(launch_readout(ctx, net->out, net->B, (int)(net->out_elems / net->B), d_pred, 2));
+    return VDTTFS_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int vdttfs_stepnet_create_culif(vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n_layers, int B,
+                                vdttfs_stepnet** out) {
+    VD_TRY(check_ctx(ctx));
+    if (!out || !layers || n_layers <= 0 || B <= 0)
+        return set_error(VDTTFS_E_INVALID, "stepnet_create_culif: bad argument");
+    *out = nullptr;
+    VD_TRY(validate_culif_table(ctx, layers, n_layers));
+    vdttfs_stepnet* net = new (std::nothrow) vdttfs_stepnet();
+    if (!net) return set_error(VDTTFS_E_NOMEM, "stepnet_create_culif: out of memory");
+    net->ctx = ctx;
+    net->B = B;
+    net->mode = VDTTFS_STEP_T3;
+    net->img_elems = (int64_t)layers[0].C_in * layers[0].H_in * layers[0].W_in * ctx->c.T;
+    const int rc = create3_impl(net, layers, n_layers);
+    if (rc != VDTTFS_OK) {
+        release(net);
+        return rc;
+    }
+    *out = net;
+    return VDTTFS_OK;
+}
 
 int vdttfs_stepnet_create(vdttfs_ctx* ctx, const vdttfs_layer_desc* layers, int n_layers, int B,
                           int64_t img_elems, int encode_mode, float tc_in, float td_in, int mode,
@@ -225,6 +346,7 @@ int vdttfs_stepnet_destroy(vdttfs_stepnet* net) {
 int vdttfs_stepnet_forward(vdttfs_stepnet* net, const float* d_img, int32_t* d_pred) {
     if (!net || !d_img) return set_error(VDTTFS_E_INVALID, "stepnet_forward: null argument");
     VD_TRY(check_ctx(net->ctx));
+    if (net->mode == VDTTFS_STEP_T3) return forward3_impl(net, d_img, d_pred);
     return forward_impl(net, d_img, d_pred);
 }
 

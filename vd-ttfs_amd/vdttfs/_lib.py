@@ -27,7 +27,7 @@ LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM = 0, 1, 2, 3
 ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES = 0, 1, 2
 READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
-STEP_T1, STEP_T2 = 1, 2
+STEP_T1, STEP_T2, STEP_T3 = 1, 2, 3
 PATH_AUTO, PATH_BINS, PATH_DENSE, PATH_FUSED = 0, 1, 2, 3
 
 
@@ -172,6 +172,7 @@ SIGNATURES = {
     "vdttfs_stepnet_destroy": [_vp],
     "vdttfs_stepnet_forward": [_vp, _vp, _vp],
     "vdttfs_stepnet_output": [_vp, C.POINTER(_vp), C.POINTER(_i64), C.POINTER(_i)],
+    "vdttfs_stepnet_create_culif": [_vp, C.POINTER(CulifLayer), _i, _i, C.POINTER(_vp)],
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
     "vdttfs_net_set_windows": [_vp, _vp, _i],

@@ -17,7 +17,7 @@ import numpy as np
 from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_TIME,  # noqa: F401
                    LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES,
                    READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
-                   CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2, LayerPlan, PATH_AUTO, PATH_BINS, PATH_DENSE,
+                   CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2, STEP_T3, LayerPlan, PATH_AUTO, PATH_BINS, PATH_DENSE,
                    PATH_FUSED)
 
 
@@ -395,6 +395,27 @@ class StepNet:
         h = np.empty(n.value, np.float32)
         check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), p, h.nbytes))
         return h, steps.value
+
+
+class CulifStepNet(StepNet):
+    """The step-by-step CuLIF baseline (T3S semantics) over the same layer
+    table as CulifNet (vdttfs_stepnet_create_culif); forward takes the dense
+    event tensor [B][C][H][W][T], output() gives the last layer's first-spike
+    steps."""
+
+    def __init__(self, ctx: Context, layers: list, B: int):
+        self.ctx = ctx
+        self.layers = layers
+        self.B = B
+        for l in layers:
+            if l.weight is not None:
+                l.weight = np.ascontiguousarray(l.weight, np.float32)
+            if l.weight_rec is not None:
+                l.weight_rec = np.ascontiguousarray(l.weight_rec, np.float32)
+        arr = (CulifLayer * len(layers))(*[l.to_c() for l in layers])
+        h = C.c_void_p()
+        check(lib().vdttfs_stepnet_create_culif(ctx.handle, arr, len(layers), B, C.byref(h)))
+        self.handle = h
 
 
 @dataclass
