@@ -594,7 +594,8 @@ def bench_ttfs(args) -> int:
             "kernel": "integrator = a layer's k_stream_dense (conv, C_in <= 64, 32 <= C_out <= 64: "
                       "list built in LDS), k_merge_dense + k_stream (other conv, C_in <= 64) or "
                       "k_bucketize + k_merge + k_stream (wider conv, FC); layers with C_out < 32 "
-                      "stream with k_stream_narrow; a launch is one layer's integrate, achieved = "
+                      "stream with k_stream_narrow, or with k_conv_small (no list) when the receptive "
+                      "field has <= 32 elements; a launch is one layer's integrate, achieved = "
                       "fused algorithmic bytes of a step / integrator time of a step",
             "algorithmic_bytes_per_step": b_int,
             "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),

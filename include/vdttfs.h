@@ -257,7 +257,10 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  *           (merge straight from the spike map; conv layers with <= 9 taps,
  *           C_in <= 64, or narrow layers with <= 25 taps), VDTTFS_PATH_FUSED
  *           (merge and integrate in one kernel, the list kept in LDS; dense
- *           layers with C_out <= 64, T <= 64, gather 1)
+ *           layers with C_out <= 64, T <= 64, gather 1), VDTTFS_PATH_REG (no
+ *           list: each lane keeps its receptive field in registers; conv
+ *           layers with K_h*K_w*C_in <= 32, C_out <= 64, T <= 64; gather 1,
+ *           ppw 64 / C_out; counting forwards run it as DENSE or FUSED)
  *   gather: 1 one c_out per lane; 2 two events per 16-byte load (C_out a
  *           multiple of 4 and <= 128); 4 four c_out per lane (C_out a
  *           multiple of 4)
@@ -273,6 +276,7 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
 #define VDTTFS_PATH_BINS  1
 #define VDTTFS_PATH_DENSE 2
 #define VDTTFS_PATH_FUSED 3
+#define VDTTFS_PATH_REG   4
 typedef struct vdttfs_layer_plan {
     int32_t path, gather, ppw;
 } vdttfs_layer_plan;

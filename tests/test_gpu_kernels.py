@@ -106,6 +106,13 @@ LAYER_CASES = [
     # the integrating kernel (Task 1 alpha-by-bin, valid conv; Task 2 same conv)
     ("t1-conv3x3-lds-list", 64, 0.0, 16, False, False, 3, 11, 9, 48, 40, 3),
     ("t2-conv3x3-lds-list-c3", 64, 32.0, 8, True, False, 4, 12, 10, 3, 64, 3),
+    # K_h * K_w * C_in <= 32, C_out <= 64, T <= 64: receptive field in
+    # registers, 64 / C_out pixels per wave (the two cases above take it too)
+    ("t1-conv2x2-reg-c8-o40", 64, 0.0, 16, False, False, 3, 9, 9, 8, 40, 2),
+    ("t2-conv3x3-reg-c2-o20", 64, 32.0, 8, True, False, 3, 10, 10, 2, 20, 3),
+    ("t2-conv1x1-reg-c32-o32", 64, 32.0, 8, True, False, 2, 6, 6, 32, 32, 1),
+    ("t1-conv3x3-reg-T48", 48, 0.0, 16, False, False, 3, 10, 10, 3, 16, 3),
+    ("t2-conv3x3-reg-T16", 16, 8.0, 4, True, False, 2, 8, 8, 3, 64, 3),
 ]
 
 
@@ -176,7 +183,7 @@ def test_integrate_paths_bitexact(gpu_ctx_factory, case):
     np.testing.assert_array_equal(d_out3.download(), exp)
 
 
-@pytest.mark.parametrize("shape", ["conv", "fc"])
+@pytest.mark.parametrize("shape", ["conv", "fc", "conv-small"])
 def test_integrate_theta_not_monotone(gpu_ctx_factory, shape):
     """Threshold tables the engine may not skip empty bins on: a shuffled
     theta (rises and falls), entries below 1e-5 and t_min > 0, next to the
@@ -186,8 +193,8 @@ def test_integrate_theta_not_monotone(gpu_ctx_factory, shape):
     tc = consts(64, 0.0, 8, True)
     ctx = gpu_ctx_factory(tc)
     is_fc = shape == "fc"
-    sp, Wt, bias, n_cols, shp = layer_inputs(rng, tc, is_fc, 6 if is_fc else 2, 6, 6,
-                                              40 if is_fc else 12, 64, 3)
+    c_in = 40 if is_fc else (3 if shape == "conv-small" else 12)  # conv-small: 27 elements, in registers
+    sp, Wt, bias, n_cols, shp = layer_inputs(rng, tc, is_fc, 6 if is_fc else 2, 6, 6, c_in, 64, 3)
     sp = np.where(rng.random(sp.size) < 0.7, np.float32(9999.0), sp).astype(np.float32)  # sparse: empty bins
     alpha, theta_mono = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
     theta_mix = rng.permutation(theta_mono).astype(np.float32)

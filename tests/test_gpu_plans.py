@@ -13,7 +13,7 @@ from vdttfs import models, tune
 
 pytestmark = pytest.mark.gpu
 
-BINS, DENSE, FUSED = vdttfs.PATH_BINS, vdttfs.PATH_DENSE, vdttfs.PATH_FUSED
+BINS, DENSE, FUSED, REG = vdttfs.PATH_BINS, vdttfs.PATH_DENSE, vdttfs.PATH_FUSED, vdttfs.PATH_REG
 
 
 def say(msg):
@@ -40,12 +40,18 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
         bad = [(18, FUSED, 0, 0),   # FC layers have no dense path
                (10, 0, 2, 0),       # two events per load cover <= 128 c_out
                (0, 0, 0, 9),        # at most 8 pixels per wave
-               (0, 4, 0, 0),        # unknown path
+               (0, 5, 0, 0),        # unknown path
                (4, DENSE, 0, 0),    # dense merge needs C_in <= 64
                (1, FUSED, 4, 0),    # the fused kernel gathers one c_out per lane
                (3, FUSED, 0, 0),    # ... and C_out <= 64
                (0, 0, 3, 0),        # gather is 1, 2 or 4
-               (2, BINS, 0, 0)]     # pools have no integrator
+               (2, BINS, 0, 0),     # pools have no integrator
+               (1, REG, 0, 0),      # 9 * 64 receptive elements do not fit in registers
+               (0, REG, 2, 0),      # the register path gathers one c_out per lane
+               (18, REG, 0, 0)]     # ... and is for conv layers
+        net.set_plan(0, REG)  # selectable on a wave-wide layer: the 27 elements fit
+        assert net.get_plan(0) == (REG, 1, 1)
+        net.set_plan(0)
         net.set_plan(3, BINS, 1, 2)
         for layer, path, gather, ppw in bad:
             with pytest.raises(vdttfs.VdttfsError):
@@ -60,7 +66,8 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
     ctx = gpu_ctx_factory(w.consts)
     net = make_net(ctx, w, 16)
     try:
-        assert net.get_plan(0) == (DENSE, 1, 10)   # C_out 6: 10 pixels per wave
+        assert net.get_plan(0) == (REG, 1, 10)     # C_out 6: 10 pixels per wave
+        assert net.get_plan(2) == (DENSE, 1, 4)    # 150 receptive elements: a list
         assert net.get_plan(6) == (BINS, 1, 6)     # FC 84 -> 10
         assert net.get_plan(4) == (BINS, 2, 1)     # FC 256 -> 120
         with pytest.raises(vdttfs.VdttfsError):
@@ -131,7 +138,7 @@ def test_every_plan_matches_oracle_lenet(gpu_ctx_factory):
     img = models.images_for(w, B)
     ref = oracle_ref(w, B, img)
     n = sweep_all_plans(gpu_ctx_factory(w.consts), w, B, img, ref, check_counts=True)
-    assert n[0] == 2 and n[6] == 1
+    assert n[0] == 3 and n[6] == 1
 
 
 def test_tuner_lenet(gpu_ctx_factory):
@@ -149,7 +156,7 @@ def test_tuner_lenet(gpu_ctx_factory):
     for L in r["layers"]:
         assert L["all_identical"] and L["best"] is not None
         assert L["best"]["ms"] <= min(c["ms"] for c in L["candidates"]) + 1e-12
-    assert r["plans"][1] is None and r["plans"][0]["path"] in ("bins", "dense")
+    assert r["plans"][1] is None and r["plans"][0]["path"] in ("bins", "dense", "reg")
 
 
 def test_committed_vgg_plans_bit_identical(gpu_ctx_factory):
@@ -175,5 +182,52 @@ def test_committed_vgg_plans_bit_identical(gpu_ctx_factory):
         ctx.synchronize()
         for i in range(len(w.layers)):
             assert np.array_equal(net.layer_output(i), ref[i]), f"layer {i}"
+    finally:
+        net.close()
+
+
+REG_CASES = [
+    # T, tfs, task2 (alpha by time, same pad), H, W, C_in, C_out, K
+    (64, 0.0, False, 9, 9, 8, 40, 2),      # 32 elements, one pixel per wave
+    (64, 32.0, True, 8, 7, 3, 64, 3),      # VGG-16 L0's shape
+    (64, 32.0, True, 6, 6, 32, 32, 1),     # 1x1, two pixels per wave
+    (48, 0.0, False, 10, 10, 3, 16, 3),    # T below 64
+    (16, 8.0, True, 8, 8, 3, 64, 3),       # short window, fire start
+    (64, 0.0, False, 12, 12, 1, 6, 5),     # LeNet conv1's shape (the built-in choice)
+]
+
+
+@pytest.mark.parametrize("case", REG_CASES, ids=[f"T{c[0]}-cin{c[5]}-cout{c[6]}-k{c[7]}" for c in REG_CASES])
+def test_register_path_forced_matches_oracle(gpu_ctx_factory, case):
+    """A one-layer network forced onto the register path (and on its
+    built-in path) equals the oracle's one-layer network bit for bit."""
+    import zlib
+
+    T, tfs, task2, H, W, C_in, C_out, K = case
+    say(f"register path {case}")
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    tc = vdttfs.TaskConsts(T=T, tfs=tfs, delta=8, vth=1.0, alpha_by_time=task2, conv_same_pad=task2)
+    ho, wo = (H, W) if task2 else (H - K + 1, W - K + 1)
+    kern = (rng.standard_normal((K, K, C_in, C_out)) * np.sqrt(2.0 / (K * K * C_in))).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.05).astype(np.float32)
+    layer = vdttfs.Layer(vdttfs.LAYER_CONV, H, W, C_in, ho, wo, C_out, K, K, kern, bias, T / 4.0, 0.0)
+    B = 3
+    n_in = B * H * W * C_in
+    t = np.floor(rng.random(n_in) * (T + tfs)).astype(np.float32)
+    t = np.where(rng.random(n_in) < 0.3, np.float32(9999.0), t).astype(np.float32)
+    ref = oracle.net_forward(oracle.Consts.from_task(tc), [layer], B, t, H * W * C_in, oracle.ENC_TIMES,
+                             T / 4.0, 0.0, oracle.READ_ARGMIN, same_pad=task2)["final"]
+    assert 0.02 < float(np.mean(ref < 9999.0)) < 0.98
+    ctx = gpu_ctx_factory(tc)
+    net = vdttfs.Net(ctx, [layer], B, H * W * C_in, vdttfs.ENCODE_TIMES, T / 4.0, 0.0, vdttfs.READOUT_ARGMIN)
+    try:
+        x = ctx.to_device(t)
+        for plan in ((0, 0, 0), (REG, 0, 0)):
+            net.set_plan(0, *plan)
+            net.forward(x)
+            ctx.synchronize()
+            got = net.layer_output(0)
+            np.testing.assert_array_equal(got, ref, err_msg=f"plan {net.get_plan(0)}")
+        assert net.get_plan(0)[0] == REG
     finally:
         net.close()

@@ -9,7 +9,7 @@ from vdttfs import models, tune
 
 
 def test_plan_records_round_trip():
-    for p in [(vdttfs.PATH_BINS, 4, 2), (vdttfs.PATH_DENSE, 2, 1), (vdttfs.PATH_FUSED, 1, 8)]:
+    for p in [(vdttfs.PATH_BINS, 4, 2), (vdttfs.PATH_DENSE, 2, 1), (vdttfs.PATH_FUSED, 1, 8), (vdttfs.PATH_REG, 1, 10)]:
         d = tune._plan_dict(p)
         assert (tune._path_id(d["path"]), d["gather"], d["ppw"]) == p
     assert tune._plan_dict((0, 0, 0))["path"] == "none"
@@ -44,4 +44,4 @@ def test_committed_vgg_plans_fit_the_benchmark():
         integ = l.kind in (vdttfs.LAYER_CONV, vdttfs.LAYER_FC)
         assert (p is not None) == integ
         if p:
-            assert p["path"] in ("bins", "dense", "fused") and p["gather"] in (1, 2, 4) and 1 <= p["ppw"] <= 8
+            assert p["path"] in ("bins", "dense", "fused", "reg") and p["gather"] in (1, 2, 4) and 1 <= p["ppw"] <= 64

@@ -9,7 +9,8 @@ Here Delta no longer sets the integrator's granularity: the engine sorts
 events into one-step bins and exits per bin, so its outputs and its time do
 not depend on Delta (Delta only defines the reference's E_proc work count).
 The sweep below confirms both.  The engine's own granularity knobs are per
-layer: how the merged event lists are built (bins, dense or fused), how many
+layer: how the merged event lists are built (bins, dense or fused) or whether
+the receptive field stays in registers with no list (reg), how many
 c_out a lane gathers per event (1, 2 events per load, or 4), and how many
 output pixels a wave integrates.  The tuner sweeps them per layer with the
 reference's procedure -- minimum of three timed rounds, outputs compared bit
@@ -33,7 +34,7 @@ import numpy as np
 
 from . import core, models
 
-PATHS = {core.PATH_BINS: "bins", core.PATH_DENSE: "dense", core.PATH_FUSED: "fused"}
+PATHS = {core.PATH_BINS: "bins", core.PATH_DENSE: "dense", core.PATH_FUSED: "fused", core.PATH_REG: "reg"}
 
 
 def _min_round_ms(ctx, net, x, d_pred, reps, rounds, per_layer):
