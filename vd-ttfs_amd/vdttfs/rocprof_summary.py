@@ -7,6 +7,7 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
   python -m vdttfs.rocprof_summary stats   DIR NAME            # --kernel-trace --stats
   python -m vdttfs.rocprof_summary layers  DIR NAME            # one forward, per layer
   python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME
+  python -m vdttfs.rocprof_summary counters DIR NAME           # occupancy, LDS conflicts
 
 ``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
 benchmark, and the same two counters over ``bench.py --copy-calibration``
@@ -145,6 +146,43 @@ def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str,
     return "\n".join(lines)
 
 
+def counters(d: str, name: str) -> str:
+    """Per kernel (non-counting dispatches, summed): waves, gathers and LDS
+    instructions per wave, LDS bank conflicts per LDS instruction, and
+    rocprofv3's OccupancyPercent (400 * SQ_WAVE_CYCLES / GRBM_GUI_ACTIVE /
+    CU_NUM / 32: resident waves as a share of 32 per CU over the dispatch),
+    weighted by dispatch duration."""
+    rows = _csv(d, name, "counter_collection")
+    by = collections.OrderedDict()
+    for r in rows:
+        k = int(r["Dispatch_Id"])
+        e = by.setdefault(k, {"name": short_name(r["Kernel_Name"]),
+                              "dur": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    agg = collections.OrderedDict()
+    for e in by.values():
+        n = e["name"]
+        if _COUNTING.match(n):
+            continue
+        a = agg.setdefault(n, collections.defaultdict(float))
+        a["dispatches"] += 1
+        a["dur"] += e["dur"]
+        for c in ("SQ_WAVES", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT"):
+            a[c] += e.get(c, 0.0)
+        a["OccupancyPercent"] += e.get("OccupancyPercent", 0.0) * e["dur"]
+    out = ["| kernel | dispatches | us | waves | gathers/wave | LDS instr/wave | bank conflicts/LDS instr "
+           "| occupancy % of 32 waves/CU |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for n, a in sorted(agg.items(), key=lambda kv: -kv[1]["dur"]):
+        w = max(a["SQ_WAVES"], 1.0)
+        lds = a["SQ_INSTS_LDS"]
+        out.append("| %s | %d | %.1f | %d | %.1f | %.1f | %s | %.1f |" % (
+            n, a["dispatches"], a["dur"], a["SQ_WAVES"], a["SQ_INSTS_VMEM_RD"] / w, lds / w,
+            ("%.3f" % (a["SQ_LDS_BANK_CONFLICT"] / lds)) if lds else "-",
+            a["OccupancyPercent"] / a["dur"]))
+    return "\n".join(out)
+
+
 def main(argv) -> int:
     if len(argv) < 2:
         print(__doc__)
@@ -156,6 +194,8 @@ def main(argv) -> int:
         print(layers(argv[2], argv[3]))
     elif cmd == "traffic":
         print(traffic(*argv[2:7]))
+    elif cmd == "counters":
+        print(counters(argv[2], argv[3]))
     else:
         print(__doc__)
         return 2
