@@ -549,6 +549,7 @@ def bench_ttfs(args) -> int:
     elapsed = time.perf_counter() - t0
     net.set_timing(False)
     integ_ms, integ_n, bkt_ms, bkt_n = net.read_timing()
+    layer_ms = net.read_layer_timing() / args.steps
     gpu_pred = d_pred.download()
 
     eproc, ebin, n_ev, n_cols = net.count(d_img)
@@ -605,6 +606,7 @@ def bench_ttfs(args) -> int:
             "integrator_launches_per_step": launches_per_step,
         },
         "bucketize_ms_per_step": bkt_ms / args.steps,
+        "layers_ms": {str(i): round(float(v), 4) for i, v in enumerate(layer_ms) if v > 0},
         "eproc_per_image": float(eproc.sum()) / B,
         "ebin_per_image": float(ebin.sum()) / B,
         "dense_macs_per_image": dense / B,
