@@ -23,6 +23,8 @@
 // k_integrate_generic: one thread per neuron, the reference loop nest over
 // either the reference bucket layout (drop-in) or the engine's bin layout
 // (narrow layers), with the chunk's delta[] in private memory.
+#include <atomic>
+
 #include "common.h"
 #include "wave.h"
 
@@ -1415,6 +1417,37 @@ int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float*
     return VDTTFS_OK;
 }
 
+// Waves of the gather's k_stream instantiation the device holds at once
+// (resident blocks per CU from the compiled kernel's registers, times CUs);
+// 0 if the runtime cannot tell.  Cached per device and gather width.
+int64_t stream_wave_capacity(const vdttfs_ctx* ctx, int gather) {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> blocks_per_cu[3][kMaxDev];
+    static std::atomic<int> cus[kMaxDev];
+    const int dev = ctx->device;
+    if (dev < 0 || dev >= kMaxDev) return 0;
+    const int gi = gather == 4 ? 2 : (gather == 2 ? 1 : 0);
+    int nb = blocks_per_cu[gi][dev].load(std::memory_order_relaxed);
+    int nc = cus[dev].load(std::memory_order_relaxed);
+    if (nb <= 0 || nc <= 0) {
+        hipError_t e;
+        if (gi == 2)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_stream<false, 4, false, 1>, 256, 0);
+        else if (gi == 1)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_stream<false, 2, false, 2>, 256, 0);
+        else
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_stream<false, 1, false, 1>, 256, 0);
+        if (e != hipSuccess || hipDeviceGetAttribute(&nc, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            nb <= 0 || nc <= 0) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        blocks_per_cu[gi][dev].store(nb, std::memory_order_relaxed);
+        cus[dev].store(nc, std::memory_order_relaxed);
+    }
+    return (int64_t)nb * 4 * nc;  // 4 waves per block
+}
+
 int plan_error(const IntegShape& sh, const char* what) {
     return set_error(VDTTFS_E_UNSUPPORTED, "plan: %s (layer %dx%dx%d -> %d, %dx%d taps%s)", what, sh.H_in, sh.W_in,
                      sh.C_in, sh.C_out, sh.K_h, sh.K_w, sh.is_fc ? ", fc" : "");
@@ -1482,14 +1515,29 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
     // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
     // (VGG-16 B=256 at 2, 4, 8 pixels per wave: 30.4K -> 29.3K, 26.0K, 20.0K
-    // images/s; the 2^18-pixel CuLIF conv3: 3.68 -> 3.88 ms)
+    // images/s; the 2^18-pixel CuLIF conv3: 3.68 -> 3.88 ms).  It also pays
+    // where one pixel per wave needs more than one but at most two rounds of
+    // resident waves and two pixels per wave fit in one (VGG-16's 4x4 layers:
+    // 8,192 waves against 5,120 resident, 0.42 -> 0.39 ms each): the second
+    // round would run mostly empty.
     if (req.ppw > kMaxPixPerWave) return plan_error(sh, "at most 8 pixels per wave");
-    p.ppw = req.ppw ? req.ppw : (n_pixels(sh) >= (INT64_C(1) << 20) ? 2 : 1);
     const bool fused = dense && fused_ok(ctx, sh, p.gather);
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
         return plan_error(sh, "fused path needs the dense limits, C_out <= 64, T <= 64 and gather 1");
     p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
+    if (req.ppw) {
+        p.ppw = req.ppw;
+    } else {
+        const int64_t n_pix = n_pixels(sh);
+        p.ppw = n_pix >= (INT64_C(1) << 20) ? 2 : 1;
+        if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED) {  // k_stream's residency (the fused kernel's is LDS-bound)
+            const int vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
+            const int64_t n_cblk = p.gather == 2 ? 1 : (sh.C_out + 64 * vec - 1) / (64 * vec);
+            const int64_t cap = stream_wave_capacity(ctx, p.gather);
+            if (cap > 0 && n_pix * n_cblk > cap && (n_pix + 1) / 2 * n_cblk <= cap) p.ppw = 2;
+        }
+    }
     *out = p;
     return VDTTFS_OK;
 }
