@@ -24,6 +24,7 @@
 // either the reference bucket layout (drop-in) or the engine's bin layout
 // (narrow layers), with the chunk's delta[] in private memory.
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "wave.h"
@@ -32,7 +33,7 @@ namespace vdttfs {
 namespace {
 
 constexpr int kBlockBins = 64;  // arrival bins handled per table / per VGPR of bin starts
-constexpr int kListPad = 16;    // zeroed entries after each pixel's merged list (two groups)
+constexpr int kListPad = 32;    // zeroed entries after each pixel's merged list (four groups)
 constexpr int kMergeWaves = 4;
 
 // ---------------------------------------------------------------------------
@@ -456,21 +457,27 @@ struct PairGather {
 
 
 // List reader: groups of 8 merged events (row, alpha) as wave-uniform
-// SGPRs, one s_load_dwordx16 per group, read one group ahead (the list is
-// zero-padded by two groups).
-struct ScalarList {
+// SGPRs, one s_load_dwordx16 per group, read NA groups ahead; take() is
+// called for consecutive groups (j, j + 8, ...) until the next start().  The
+// list is zero-padded by four groups, so reads stay in the pixel's region.
+template <int NA>
+struct ScalarListN {
     const int2* L;
-    Group8 ahead;
+    Group8 ahead[NA];
     __device__ __forceinline__ void start(const void* L_, int j, const StreamArgs&) {
         L = static_cast<const int2*>(L_);
-        ahead = *reinterpret_cast<const Group8*>(L + j);
+#pragma unroll
+        for (int q = 0; q < NA; ++q) ahead[q] = *reinterpret_cast<const Group8*>(L + j + 8 * q);
     }
     __device__ __forceinline__ Group8 take(int j) {
-        const Group8 g = ahead;
-        ahead = *reinterpret_cast<const Group8*>(L + j + 8);
+        const Group8 g = ahead[0];
+#pragma unroll
+        for (int q = 0; q + 1 < NA; ++q) ahead[q] = ahead[q + 1];
+        ahead[NA - 1] = *reinterpret_cast<const Group8*>(L + j + 8 * NA);
         return g;
     }
 };
+using ScalarList = ScalarListN<1>;
 
 // Integrates one output pixel for one c_out block (lane = VEC c_out) from its
 // merged event list and writes the first-spike times.  CULIF selects the
@@ -478,7 +485,7 @@ struct ScalarList {
 // delta_t, fire at carry >= theta[t] >= 1e-5, t >= t_min) or the CuLIF neuron
 // of T3V (I = fma(I, decay, in_t); V += I; fire at V >= th).  CuLIF events
 // carry alpha = 1, so fma(w, 1, acc) is exactly the reference's acc + w.
-template <bool COUNT, bool CULIF, class G, class LR = ScalarList, int VEC = G::OWN>
+template <bool COUNT, bool CULIF, class G, class LR = ScalarList, int NG = 1, int VEC = G::OWN>
 __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restrict__ out,
                                              const void* __restrict__ L,
                                              const int32_t* __restrict__ BS,
@@ -572,51 +579,66 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         // groups of 8 (row, alpha) pairs, read one group (chunk) ahead
         LR lr;
         lr.start(L, j, a);
+        // NG groups of 8 per step: their gathers are issued together
+        constexpr int GE = 8 * NG;
         while (j < blk_end) {
-            const int n = (blk_end - j) < 8 ? (blk_end - j) : 8;
-            const Group8 grp = lr.take(j);
-            const int2* e = grp.v;
+            const int n = (blk_end - j) < GE ? (blk_end - j) : GE;
+            Group8 grp[NG];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(e[g].x), "s"(e[g].y));
-            Vf<VEC> w[8];
+            for (int q = 0; q < NG; ++q) grp[q] = lr.take(j + 8 * q);
 #pragma unroll
-            for (int g = 0; g < 8; ++g)
+            for (int q = 0; q < NG; ++q)
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) w[g].v[v] = 0.0f;
-            gather_w.group(grp.v, w, live);
+                for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(grp[q].v[g].x), "s"(grp[q].v[g].y));
+            Vf<VEC> w[NG][8];
+#pragma unroll
+            for (int q = 0; q < NG; ++q)
+#pragma unroll
+                for (int g = 0; g < 8; ++g)
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) w[q][g].v[v] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NG; ++q) gather_w.group(grp[q].v, w[q], live);
+#define VD_EV(i) grp[(i) / 8].v[(i) % 8]
+#define VD_W(i) w[(i) / 8][(i) % 8]
             if (bend >= j + n) {
-                // the whole group belongs to the open bin
-                if (n == 8) {
+                // the whole step belongs to the open bin
+                if (n == GE) {
 #pragma unroll
-                    for (int g = 0; g < 8; ++g)
+                    for (int i = 0; i < GE; ++i)
 #pragma unroll
                         for (int v = 0; v < VEC; ++v)
-                            acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
+                            acc[v] = __builtin_fmaf(VD_W(i).v[v], __int_as_float(VD_EV(i).y), acc[v]);
                 } else {
 #pragma unroll
-                    for (int g = 0; g < 8; ++g)
-                        if (g < n)
+                    for (int i = 0; i < GE; ++i)
+                        if (i < n)
 #pragma unroll
                             for (int v = 0; v < VEC; ++v)
-                                acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
+                                acc[v] = __builtin_fmaf(VD_W(i).v[v], __int_as_float(VD_EV(i).y), acc[v]);
                 }
             } else {
 #pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    if (g >= n) break;
-                    while (bend <= j + g) {
-                        VD_FINALIZE(bcur, acc);
-                        if (done) goto stream_done;
+                for (int q = 0; q < NG; ++q) {
 #pragma unroll
-                        for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-                        ++bcur;
-                        bend = VD_BIN_START(bcur + 1);
+                    for (int g = 0; g < 8; ++g) {
+                        if (8 * q + g >= n) break;
+                        while (bend <= j + 8 * q + g) {
+                            VD_FINALIZE(bcur, acc);
+                            if (done) goto stream_done;
+#pragma unroll
+                            for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+                            ++bcur;
+                            bend = VD_BIN_START(bcur + 1);
+                        }
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v)
+                            acc[v] = __builtin_fmaf(w[q][g].v[v], __int_as_float(grp[q].v[g].y), acc[v]);
                     }
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v)
-                        acc[v] = __builtin_fmaf(w[g].v[v], __int_as_float(e[g].y), acc[v]);
                 }
             }
+#undef VD_EV
+#undef VD_W
             j += n;
         }
         // close the block's remaining bins (the open one and trailing empty ones)
@@ -653,8 +675,13 @@ __device__ __forceinline__ void stream_one(const StreamArgs& a, float* __restric
         g.r = rsrc;
         const int c0 = GlobalGather<VEC>::c0(cb, lane);
         g.voff = (c0 < a.C_out ? c0 : 0) * 4;  // C_out is a multiple of VEC
-        stream_pixel<COUNT, CULIF, GlobalGather<VEC>, LR>(a, out, L, BS, theta, pix, cb, g, cnt_proc,
-                                                          cnt_bin);
+        // one c_out per lane: two groups of gathers in flight (16 events),
+        // the scalar list read two groups ahead
+        constexpr int NG = VEC == 1 ? 2 : 1;
+        using LRN = typename std::conditional<NG == 2 && std::is_same<LR, ScalarList>::value, ScalarListN<2>,
+                                              LR>::type;
+        stream_pixel<COUNT, CULIF, GlobalGather<VEC>, LRN, NG>(a, out, L, BS, theta, pix, cb, g, cnt_proc,
+                                                               cnt_bin);
     } else {
         static_assert(VEC == 2 && EPI == 2, "PairGather owns 2 c_out per lane");
         PairGather g;
