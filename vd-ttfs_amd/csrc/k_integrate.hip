@@ -16,7 +16,8 @@
 //  k_stream - one wave64 per (output pixel, c_out block); lanes are c_out, so
 //             each event is wave-uniform: the list is read through the scalar
 //             cache 8 events at a time and every weight gather is one
-//             coalesced row segment (dword or dwordx4 per lane).  Bins are
+//             coalesced row segment (dword or dwordx4 per lane); with one
+//             c_out per lane two groups of 8 gathers are in flight.  Bins are
 //             closed between fmas; lanes that fired stop fetching and the wave
 //             leaves once its ballot of live lanes is empty.
 //
