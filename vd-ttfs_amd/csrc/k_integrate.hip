@@ -916,11 +916,13 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
 // k_stream_narrow: layers with C_out < 32 (LeNet's 6-, 16- and 10-wide
 // layers), where one pixel per wave would leave most lanes idle.  A wave
 // packs P = 64 / C_out pixels, lane = (pixel p, c_out c); each lane walks its
-// pixel's merged list (the k_merge output, (bin, tap, cin) order) bin by bin,
-// gathering W[row + c] per event, four events in flight, and closes every
-// bin in order with the neuron of the layer, as k_stream does.  Lanes of one
-// pixel read the same list entries; lanes of different pixels diverge only
-// in how many events a bin holds.  E_proc / E_bin count per lane with the
+// pixel's merged list (the k_merge output, (bin, tap, cin) order) through a
+// window of 8 entries and their gathers W[row + c].  Bins close in lockstep,
+// in order, with the neuron of the layer, as in k_stream: each adds the
+// window's events that fall in it, in list order, and the window moves on
+// only when some lane's open bin runs past it -- one list load and one round
+// of gathers per 8 events rather than per bin.  Lanes of one pixel read the
+// same list entries.  E_proc / E_bin count per lane with the
 // same rules as k_stream (a neuron counts a bin's events while it was alive
 // at the start of the chunk / of the bin).
 template <bool COUNT, bool CULIF>
@@ -951,32 +953,47 @@ __global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __re
         const float v_th = (!CULIF && lane < nb) ? theta[t0 + lane] : 0.0f;
         bool done = false;
         for (int b8 = 0; b8 < nb && !done; b8 += 8) {
+            const int ng = (nb - b8) < 8 ? (nb - b8) : 8;  // uniform
             int ends[8];  // bin ends of the next eight bins, loaded together
 #pragma unroll
-            for (int g = 0; g < 8; ++g) ends[g] = (ok && b8 + g < nb) ? BS[t0 + b8 + g + 1] : 0;
+            for (int g = 0; g < 8; ++g) ends[g] = (ok && g < ng) ? BS[t0 + b8 + g + 1] : j;
+            // A window of 8 list entries per lane (the list is padded past its
+            // end, so the loads stay in the pixel's region) serves every bin
+            // it covers: bins close in lockstep, each adding the window's
+            // events that fall in it, in list order; the window moves on only
+            // when some lane's open bin runs past it.
+            int s_ = j;   // first event of the lane's open bin
+            int wj = j;   // window start
+            int2 e[8];
+            float w[8];
+            bool need = true;  // uniform
+            float acc = 0.0f;
+            for (int g = 0; g < ng;) {  // uniform
+                int be = ends[0];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                const int b = b8 + g;
-                if (b >= nb || done) break;  // uniform
-                const int t = t0 + b;
-                const int e_end = ends[g];
-                const int e_beg = j;
-                float acc = 0.0f;
-                while (__ballot(j < e_end)) {
-                    int2 e[4];
-                    float w[4];
+                for (int q = 1; q < 8; ++q) be = g == q ? ends[q] : be;
+                if (need) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) e[q] = (j + q < e_end) ? L[j + q] : make_int2(0, 0);
+                    for (int q = 0; q < 8; ++q) e[q] = L[wj + q];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    for (int q = 0; q < 8; ++q)
                         w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, e[q].x + voff, 0, 0));
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (j + q < e_end) acc = __builtin_fmaf(w[q], __int_as_float(e[q].y), acc);
-                    j = (j + 4 < e_end) ? j + 4 : (j < e_end ? e_end : j);
+                    need = false;
                 }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int idx = wj + q;
+                    acc = (idx >= s_ && idx < be) ? __builtin_fmaf(w[q], __int_as_float(e[q].y), acc) : acc;
+                }
+                if (__ballot(be > wj + 8)) {  // some lane's bin continues past the window
+                    wj = be > wj + 8 ? wj + 8 : be;
+                    need = true;
+                    continue;
+                }
+                const int b = b8 + g;
+                const int t = t0 + b;
                 if (COUNT) {
-                    const unsigned long long n = (unsigned long long)(e_end - e_beg);
+                    const unsigned long long n = (unsigned long long)(be - s_);
                     if (alive) cnt_bin += n;
                     if (alive_chunk) cnt_proc += n;
                 }
@@ -997,8 +1014,14 @@ __global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __re
                 }
                 const bool chunk_end = ((t + 1) % D) == 0;
                 if (COUNT && chunk_end) alive_chunk = alive;
-                if (__ballot(alive) == 0 && (!COUNT || chunk_end)) done = true;
+                acc = 0.0f;
+                s_ = be;
+                ++g;
             }
+            j = s_;
+            // counting forwards keep going to the end of the chunk of the
+            // last firing (their counts stop with the alive flags)
+            if (__ballot(COUNT ? (alive || alive_chunk) : alive) == 0) done = true;
         }
         if (done) break;
     }
