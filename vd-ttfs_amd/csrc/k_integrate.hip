@@ -1499,6 +1499,24 @@ int64_t stream_wave_capacity(const vdttfs_ctx* ctx, int gather) {
     return (int64_t)nb * 4 * nc;  // 4 waves per block
 }
 
+// Compute units of the context's device (0 if the runtime cannot tell),
+// cached per device.
+int64_t cu_count(const vdttfs_ctx* ctx) {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cus[kMaxDev];
+    const int dev = ctx->device;
+    if (dev < 0 || dev >= kMaxDev) return 0;
+    int nc = cus[dev].load(std::memory_order_relaxed);
+    if (nc <= 0) {
+        if (hipDeviceGetAttribute(&nc, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || nc <= 0) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        cus[dev].store(nc, std::memory_order_relaxed);
+    }
+    return nc;
+}
+
 int plan_error(const IntegShape& sh, const char* what) {
     return set_error(VDTTFS_E_UNSUPPORTED, "plan: %s (layer %dx%dx%d -> %d, %dx%d taps%s)", what, sh.H_in, sh.W_in,
                      sh.C_in, sh.C_out, sh.K_h, sh.K_w, sh.is_fc ? ", fc" : "");
@@ -1562,6 +1580,12 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         p.gather = req.gather;
     } else {
         p.gather = (sh.C_out % 4 == 0 && sh.C_out > 64) ? (sh.C_out <= 128 ? 2 : 4) : 1;
+        // an FC layer's pixels are its batch: where four c_out per lane would
+        // leave fewer waves than the device has SIMDs, one c_out per lane
+        // (4x the c_out blocks) is faster (VGG-16's 512 -> 512 FC at B=256:
+        // 512 waves, 0.072 -> 0.060 ms; the 2x2 conv L14's 2,048 keep four)
+        const int64_t simds = 4 * cu_count(ctx);
+        if (p.gather == 4 && sh.is_fc && simds > 0 && n_pixels(sh) * ((sh.C_out + 255) / 256) < simds) p.gather = 1;
     }
     // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
     // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
