@@ -2,14 +2,15 @@
 """Benchmark: VGG-16 TTFS-SNN inference (config 3) on one MI355X.
 
 One step = one batch of 256 synthetic images through the whole network:
-encode -> 13 conv layers (bucketize + integrate) with 5 min-pools -> FC
+encode -> 13 conv layers (list build + integrate) with 5 min-pools -> FC
 512->512 -> 512->10 membrane-potential readout -> argmax, inputs already
 resident in HBM.  Prints ONE JSON line (stdout) with images/s, the
 integrator's roofline position and a same-host CPU baseline of the
 reference algorithm (oracle/, timed on a bounded sample).
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-host-scope]
   python bench.py --copy-calibration   # known-size copy for FETCH/WRITE_SIZE scaling
+  python bench.py --gather-probe       # the gather roof: footprint x width sweep
 
 The other synthetic workloads print one line each in the same format
 (parity cases of the same engine, not the headline):
@@ -17,22 +18,40 @@ The other synthetic workloads print one line each in the same format
   python bench.py --workload lenet5     # config 2: LeNet-5, B=1024 (config 1 = its B=1 CPU leg)
   python bench.py --workload culif7     # config 4: 7-layer CuLIF on 2x128x128 events, B=64
   python bench.py --workload fc-sweep   # config 5: FC 4096x4096, B=512, density/T'/delta sweep
-  python bench.py --workload vgg16-timedriven | lenet5-timedriven
-                                        # the reference's step-by-step GPU baseline (T2S / T1S)
-                                        # on configs 3 / 2, with the event-driven speedup
+  python bench.py --workload fc-point   # config 5's headline point alone (density 5%, T'=64, delta=16)
+  python bench.py --workload vgg16-timedriven | lenet5-timedriven | culif7-timedriven
+                                        # the reference's step-by-step GPU baseline (T2S / T1S / T3S)
 
-roofline.traffic is the integrator's HBM bytes per launch measured with
-rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs and written to
-profiles/integrator_vgg16_b256_traffic.md (by python -m
-vdttfs.rocprof_summary traffic); it is reported only when that file's
-workload line matches the configuration being run, else null.
+Three rooflines are reported for the integrator (a layer's list build +
+stream, the dominant kernel family):
+
+* roofline.achieved / frac / traffic -- HBM: the FETCH_SIZE + WRITE_SIZE
+  bytes that rocprofv3 counted for the integrator kernels of one forward
+  (profiles/integrator_<workload>_traffic.md, written by python -m
+  vdttfs.rocprof_summary traffic) over the live HIP-event integrator time,
+  against 8 TB/s.  The counters belong to one build of the kernels: the
+  profile's WORKLOAD line carries a hash of the integrator sources, and a
+  profile of other sources is not used (traffic and frac are then null).
+* roofline.algorithmic_hbm_* -- the bytes the algorithm must move through
+  HBM in one fused pass per layer (input map, weights, bias, output map)
+  over the same time.
+* roofline.gathered -- the weight bytes the stream kernels gather per
+  integrated synapse (4 B per event under the per-bin exit the kernels run,
+  E_bin) over the same time, against the gather roof that
+  vdttfs_probe_gather measures live on the same GPU (weights resident in
+  one XCD's L2): this is the ceiling the stream kernels are bound by.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
+import re
+import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -44,60 +63,57 @@ import numpy as np  # noqa: E402
 
 METRIC = "images/sec/GPU for VGG-16 TTFS bs=256; integrator % of HBM peak"
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "integrator_vgg16_b256_traffic.md")
 COPY_FLOATS = 1 << 28  # 1 GiB read + 1 GiB written per calibration dispatch
+CSRC = os.path.join(ROOT, "vd-ttfs_amd", "csrc")
+# the sources that decide the integrator's dispatches and their memory traffic
+INTEG_SOURCES = ("k_integrate.hip", "k_bucketize.hip", "net.cpp", "capi.cpp", "k_culif.hip", "culif.cpp")
+# gather-roof probe: rows uniformly random over a footprint that fits one XCD's 4 MB L2
+PROBE_L2_BYTES = 2 << 20
+PROBE_WAVES, PROBE_EVENTS, PROBE_REPS = 32768, 512, 5
+MI355X_CUS, MI355X_GHZ = 256, 2.4
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(w, eproc, n_ev, n_cols, B):
-    """Fused bytes per integrating layer, B_int + 4*N_cols*C_in: the dense
-    input map read once, 4*E_proc (one fp32 weight per integrated synapse),
-    8*N_ev (event lists) + 4*OS*N_cols (chunk offsets), 4*C_out (bias) and
-    4*N_out (first-spike write).  Conv layers build their event lists straight
-    from the dense map; FC layers bucketize first -- either way the layer's
-    whole integrate (bucketize + merge + stream) is priced and timed."""
-    OS = w.consts.num_chunks + 1
-    total = 0
-    per_layer = []
-    for i, l in enumerate(w.layers):
-        if l.kind not in (0, 1):
-            per_layer.append(0)
-            continue
-        n_out = B * l.H_out * l.W_out * l.C_out
-        cin_col = l.C_in if l.kind == 0 else l.H_in * l.W_in * l.C_in
-        b = (4 * int(eproc[i]) + 8 * int(n_ev[i]) + 4 * OS * int(n_cols[i]) + 4 * l.C_out + 4 * n_out
-             + 4 * int(n_cols[i]) * cin_col)
-        per_layer.append(b)
-        total += b
-    return total, per_layer
+def sources_hash() -> str:
+    h = hashlib.sha1()
+    for name in INTEG_SOURCES:
+        with open(os.path.join(CSRC, name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:10]
 
 
-def workload_key(B, consts) -> str:
-    return f"vgg16 B={B} T={consts.T} delta={consts.delta} tfs={consts.tfs:g}"
+def traffic_file(tag: str) -> str:
+    return os.path.join(ROOT, "profiles", f"integrator_{tag}_traffic.md")
 
 
-def measured_traffic(key: str):
-    """(bytes per step, launches per step) from the committed counter summary."""
+def measured_traffic(tag: str, key: str):
+    """{per_step, launches, layers: [(fetch, write)]} from the committed counter
+    summary of workload `tag`, or None when it is missing or belongs to
+    another configuration or build."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(tag)) as f:
             text = f.read()
     except OSError:
         return None
     wl = per_step = launches = None
+    layers = []
     for line in text.splitlines():
         line = line.strip().strip("`")
         if line.startswith("WORKLOAD="):
             wl = line[len("WORKLOAD="):].strip()
+        elif line.startswith("LAYER_TRAFFIC "):
+            kv = dict(t.split("=", 1) for t in line.split()[1:])
+            layers.append((float(kv["fetch"]), float(kv["write"])))
         elif line.startswith("TRAFFIC_PER_STEP_BYTES="):
             kv = dict(t.split("=", 1) for t in line.split())
             per_step = float(kv["TRAFFIC_PER_STEP_BYTES"])
             launches = int(kv["LAUNCHES_PER_STEP"])
     if wl != key or per_step is None:
         return None
-    return per_step, launches
+    return {"per_step": per_step, "launches": launches, "layers": layers}
 
 
 def copy_calibration() -> int:
@@ -115,47 +131,463 @@ def copy_calibration() -> int:
     return 0
 
 
-def cpu_baseline(w, img, gpu_pred, threads_all, n1=16, nall=None):
-    import oracle
+def probe_point(ctx, vec: int, footprint: int, waves=PROBE_WAVES, n_ev=PROBE_EVENTS, reps=PROBE_REPS):
+    ms = ctx.probe_gather(vec, footprint, n_ev, waves, reps)
+    wave_gathers = waves * n_ev
+    return {"vec": vec, "bytes_per_wave_gather": 256 * vec, "footprint_bytes": footprint, "ms": ms,
+            "GBps": wave_gathers * 256.0 * vec / (ms * 1e-3) / 1e9,
+            "G_wave_gathers_per_s": wave_gathers / (ms * 1e-3) / 1e9,
+            "clk_per_wave_gather_per_cu": MI355X_CUS * MI355X_GHZ * 1e9 * ms * 1e-3 / wave_gathers}
+
+
+def gather_roofs(ctx):
+    """Live gather roofs (GB/s) for 256-byte (dword) and 1 KB (dwordx4) wave-gathers."""
+    return {1: probe_point(ctx, 1, PROBE_L2_BYTES), 4: probe_point(ctx, 4, PROBE_L2_BYTES)}
+
+
+def gather_probe(args) -> int:
+    """The probe sweep behind profiles/gather_roof_probe.md."""
     import vdttfs
 
-    c = oracle.Consts.from_task(w.consts)
-    rmode = oracle.READ_ARGMAX if w.readout == vdttfs.READOUT_ARGMAX else oracle.READ_ARGMIN
+    ctx = vdttfs.Context(vdttfs.task2_consts(T=64, delta=8, tfs=32.0), 0)
+    rows = []
+    for fp, name in ((24 << 10, "L1 (24 KiB)"), (PROBE_L2_BYTES, "one XCD's L2 (2 MiB)"),
+                     (64 << 20, "beyond L2 (64 MiB)")):
+        for vec in (1, 2, 4):
+            r = probe_point(ctx, vec, fp)
+            r["footprint"] = name
+            rows.append(r)
+            log(f"probe {name:22s} vec={vec}: {r['GBps'] / 1e3:6.2f} TB/s, "
+                f"{r['G_wave_gathers_per_s']:6.1f} G wave-gathers/s, {r['clk_per_wave_gather_per_cu']:.2f} clk/CU")
+    ctx.close()
+    print(json.dumps({"gather_probe": rows, "waves": PROBE_WAVES, "events_per_wave": PROBE_EVENTS,
+                      "reps": PROBE_REPS, "cus": MI355X_CUS, "ghz": MI355X_GHZ}), flush=True)
+    return 0
 
-    def run(n, thr):
-        t0 = time.perf_counter()
-        r = oracle.net_forward(c, w.layers, n, img[:n], w.img_elems, oracle.ENC_LINEAR, w.tc_in,
-                               w.td_in, rmode, same_pad=bool(w.consts.conv_same_pad), nthreads=thr)
-        return time.perf_counter() - t0, r
 
-    # bounded sample, ~10-20 s of CPU work in all: n1 images on 1 thread and
-    # the whole batch on every thread the box grants
-    n1 = min(n1, len(gpu_pred))
-    run(1, 1)  # warm-up (page-in, OpenMP pool)
-    dt1, r1 = run(n1, 1)
-    nall = len(gpu_pred) if nall is None else min(nall, len(gpu_pred))
-    dta, ra = run(nall, threads_all)
-    match = bool(np.array_equal(ra["pred"], gpu_pred[:nall]) and np.array_equal(r1["pred"], gpu_pred[:n1]))
-    return {
-        "value": nall / dta,
-        "unit": "images/s",
-        "cores": threads_all,
-        "kind": "port",
-        "sample": f"{nall} images of the batch, whole network, {threads_all} OpenMP threads "
-                  f"({dta:.2f} s); 1 thread on the first {n1} images: {n1 / dt1:.3f} images/s",
-        "single_thread_value": n1 / dt1,
-        "pred_match_gpu": match,
-    }
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def threads_all() -> int:
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
+def median_time(fn, reps: int):
+    """(median seconds, all seconds, last result) of `reps` calls of fn."""
+    ts, r = [], None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        r = fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts, r
+
+
+def conv_pads(l, same: bool):
+    if l.kind != 0 or not same:
+        return 0, 0
+    return l.K_h // 2, l.K_w // 2
+
+
+def hbm_compulsory_bytes(l, B: int) -> int:
+    """What one fused pass over a conv / FC layer must move through HBM: the
+    input map once, the weights once, the bias and the output map."""
+    n_in = B * l.H_in * l.W_in * l.C_in
+    n_out = B * l.H_out * l.W_out * l.C_out
+    n_w = (l.K_h * l.K_w * l.C_in if l.kind == 0 else l.H_in * l.W_in * l.C_in) * l.C_out
+    return 4 * (n_in + n_w + l.C_out + n_out)
+
+
+def onehot(pred, n_cls: int) -> np.ndarray:
+    y = np.zeros((len(pred), n_cls), np.float32)
+    for i, p in enumerate(pred):
+        if p >= 0:
+            y[i, p] = 1
+    return y
+
+
+def host_scope(ctx, net, w, img, B: int, steps: int):
+    """The reference's timed scope with the engine (T2V:337-402): per batch a
+    synchronous H2D of the images from pageable host memory, the forward, a
+    D2H of the last layer's output and the host readout."""
+    from vdttfs._lib import check, lib
+
+    h_img = np.ascontiguousarray(img, np.float32)
+    d_img = ctx.to_device(h_img)
+    ptr, elems = net.layer_output_ptr(len(w.layers) - 1)
+    h_out = np.empty(elems, np.float32)
+    argmax = w.readout == 1
+    n_cls = elems // B
+
+    def step():
+        check(lib().vdttfs_h2d(ctx.handle, d_img.ptr, h_img.ctypes.data, h_img.nbytes))
+        net.forward(d_img, None)
+        check(lib().vdttfs_d2h(ctx.handle, h_out.ctypes.data, ptr, h_out.nbytes))
+        o = h_out.reshape(B, n_cls)
+        if argmax:  # T2V:389-396: strict > from -1e9, the first maximum wins
+            return np.argmax(o, axis=1)
+        # T1V:312-319: strict < from INF, the first minimum wins, -1 if nothing fired
+        p = np.argmin(o, axis=1)
+        p[o.min(axis=1) >= np.float32(9999.0)] = -1
+        return p
+
+    step()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        pred = step()
+    dt = (time.perf_counter() - t0) / steps
+    d_img.free()
+    return {"value": B / dt, "unit": "images/s", "ms_per_step": dt * 1e3,
+            "scope": "synchronous H2D of the batch (pageable) + forward + D2H of the last layer + host readout "
+                     "(T2V:337-402 with the engine's forward)"}, pred
+
+
+def dropin_scope(w, img, gpu_pred, B: int, reps: int = 4):
+    """T2V's batch loop call for call on the drop-in entry points, run by the
+    C++ driver (vd-ttfs_amd/bin/vdttfs_vgg --dropin) on synthetic assets in the
+    reference's file formats whose labels are the engine's predictions, so a
+    reported 100% means identical classes."""
+    from vdttfs import models
+
+    drv = os.path.join(ROOT, "vd-ttfs_amd", "bin", "vdttfs_vgg")
+    if not os.path.exists(drv):
+        return {"error": f"{drv} is not built (make -C vd-ttfs_amd)"}
+    c = w.consts
+    with tempfile.TemporaryDirectory() as d:
+        wp = os.path.join(d, "snn_weights_vgg.bin")
+        models.write_weights_blob(wp, w.layers)
+        dd = os.path.join(d, "cifar10_float")
+        os.makedirs(dd)
+        for i in range(B):
+            np.ascontiguousarray(img[i], np.float32).tofile(os.path.join(dd, f"{i}.bin"))
+        onehot(gpu_pred, 10).tofile(os.path.join(dd, "label_onehot"))
+        cmd = [drv, "--weights", wp, "--data", dd, "--n", str(B), "--batch", str(B), "--T", str(c.T),
+               "--tfs", f"{c.tfs:g}", "--delta", str(c.delta), "--encode", "linear", "--tc-in", repr(w.tc_in),
+               "--td-in", repr(w.td_in), "--dropin", "--reps", str(reps)]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"error": f"driver exit {r.returncode}: {(r.stdout + r.stderr)[-400:]}"}
+    secs = [float(x) for x in re.findall(r"Total Inference Time:\s+([0-9.eE+-]+) seconds", r.stdout)]
+    accs = re.findall(r"Final Accuracy:\s+([0-9.]+)%", r.stdout)
+    layers = {}
+    for m in re.finditer(r"^LAYER_MS i=(\d+) kind=(\w+) lut_ms=(\S+) launch_ms=(\S+)$", r.stdout, re.M):
+        layers[int(m.group(1))] = {"kind": m.group(2), "lut_ms": float(m.group(3)), "launch_ms": float(m.group(4))}
+    med = statistics.median(secs[1:]) if len(secs) > 1 else secs[0]
+    return {"value": B / med, "unit": "images/s", "ms_per_step": med * 1e3,
+            "runs_s": secs, "pred_match_engine": bool(accs) and all(float(a) == 100.0 for a in accs),
+            "layers": layers,
+            "scope": "vd-ttfs_amd/bin/vdttfs_vgg --dropin: per batch vdttfs_h2d, vdttfs_encode_linear + sync, "
+                     "per weighted layer vdttfs_update_luts + vdttfs_launch_layer_sync / "
+                     "vdttfs_launch_fc_vmem_sync, pools vdttfs_launch_pool_sync, vdttfs_d2h of the logits, "
+                     "host argmax (T2V:337-402 call for call); median of the runs after the first"}
+
+
+def work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr):
+    """Per integrating layer: time, E_proc / E_bin / E_noEE, skip rate, spike
+    densities, launch plan and the three roof positions."""
+    from vdttfs import workcount
+
+    eproc, ebin, n_ev, n_cols = counts
+    T, tfs = w.consts.T, w.consts.tfs
+    same = bool(w.consts.conv_same_pad)
+    d_enc = ctx.empty(B * w.img_elems)
+    ctx.encode_linear(d_img, d_enc)
+    x = d_enc.download()
+    d_enc.free()
+    rows, li = [], 0
+    for i, l in enumerate(w.layers):
+        out = net.layer_output(i)
+        if l.kind in (0, 1):
+            fc = l.kind == 1
+            ph, pw = conv_pads(l, same)
+            cin = l.H_in * l.W_in * l.C_in if fc else l.C_in
+            e_noee, nev = workcount.no_exit_synapses(
+                x, B, 1 if fc else l.H_in, 1 if fc else l.W_in, cin, 1 if fc else l.H_out, 1 if fc else l.W_out,
+                l.C_out, 1 if fc else l.K_h, 1 if fc else l.K_w, ph, pw, fc, tfs, T)
+            ms = float(layer_ms[i])
+            path, gather, ppw = net.get_plan(i)
+            roof = roofs[1] if gather == 1 else roofs[4]
+            gb = 4.0 * float(ebin[i])
+            row = {"layer": i, "kind": "fc" if fc else "conv",
+                   "shape": f"{l.C_in}->{l.C_out} @ {l.H_in}x{l.W_in}" + ("" if fc else f", {l.K_h}x{l.K_w}"),
+                   "plan": {"path": ["auto", "bins", "dense", "fused", "reg"][path], "gather": gather, "ppw": ppw},
+                   "ms": ms, "eproc": int(eproc[i]), "ebin": int(ebin[i]), "e_noee": e_noee,
+                   "skip_rate": 1.0 - float(eproc[i]) / max(1, e_noee),
+                   "n_ev": int(n_ev[i]), "n_ev_host_equal": nev == int(n_ev[i]),
+                   "in_density": nev / float(x.size), "out_fired": float(np.mean(out < 9999.0)),
+                   "gathered_GBps": gb / (ms * 1e-3) / 1e9,
+                   "gather_roof_GBps": roof["GBps"],
+                   "gather_frac": gb / (ms * 1e-3) / 1e9 / roof["GBps"],
+                   "algorithmic_hbm_bytes": hbm_compulsory_bytes(l, B)}
+            if tr and li < len(tr["layers"]):
+                hb = tr["layers"][li][0] + tr["layers"][li][1]
+                row["hbm_bytes"] = hb
+                row["hbm_GBps"] = hb / (ms * 1e-3) / 1e9
+                row["hbm_frac"] = row["hbm_GBps"] / HBM_PEAK_GBS
+            rows.append(row)
+            li += 1
+        x = out
+    return rows
+
+
+def parity_summary(ctx, w, B, gpu_outs, gpu_pred, ref):
+    """BASELINE.md's parity columns: buckets bit-exact (the reference layout of
+    the widest layer input, GPU vdttfs_bucketize against the oracle), per-layer
+    mismatched first-spike times, class mismatches and the readout's largest
+    relative error, all 256 images."""
+    import oracle
+
+    mism, vmem_err = [], 0.0
+    for i, (l, g, o) in enumerate(zip(w.layers, gpu_outs, ref["outs"])):
+        if l.kind == 3:
+            vmem_err = max(vmem_err, float(np.max(np.abs(g - o) / (np.abs(o) + 1e-3))))
+            mism.append(0)
+        else:
+            mism.append(int(np.count_nonzero(g != o)))
+    # the widest conv input: the layer whose input has the most elements
+    cands = [(i, l) for i, l in enumerate(w.layers) if l.kind == 0]
+    i, l = max(cands, key=lambda il: il[1].H_in * il[1].W_in * il[1].C_in)
+    x = gpu_outs[i - 1] if i > 0 else None
+    if x is None:
+        return {"error": "first layer is the widest; no GPU input map kept"}
+    n_cols = B * l.H_in * l.W_in
+    c = oracle.Consts.from_task(w.consts)
+    cin, tin, off = oracle.bucketize(c, x, n_cols, l.C_in)
+    OS = w.consts.num_chunks + 1
+    d_x = ctx.to_device(x)
+    d_cin, d_tin = ctx.empty(n_cols * l.C_in, np.int32), ctx.empty(n_cols * l.C_in, np.float32)
+    d_off = ctx.empty(n_cols * OS, np.int32)
+    ctx.bucketize(d_x, n_cols, l.C_in, d_cin, d_tin, d_off)
+    g_off, g_cin, g_tin = d_off.download(), d_cin.download(), d_tin.download()
+    for a in (d_x, d_cin, d_tin, d_off):
+        a.free()
+    valid = np.arange(l.C_in)[None, :] < off.reshape(n_cols, OS)[:, -1:]
+    bk = bool(np.array_equal(g_off, off) and
+              np.array_equal(g_cin.reshape(n_cols, -1)[valid], cin.reshape(n_cols, -1)[valid]) and
+              np.array_equal(g_tin.reshape(n_cols, -1)[valid].view(np.uint32),
+                             tin.reshape(n_cols, -1)[valid].view(np.uint32)))
+    return {"images": B, "buckets_bitexact": bk, "bucket_check": f"layer {i} input, {n_cols} columns x {l.C_in}",
+            "mismatched_spike_times_per_layer": mism, "pred_mismatches": int(np.count_nonzero(gpu_pred != ref["pred"])),
+            "max_vmem_rel_err": vmem_err, "ties": [] if sum(mism) == 0 else "see mismatched_spike_times_per_layer"}
+
+
+def cpu_baseline(w, img, gpu_pred, thr: int, n1: int, reps: int = 3):
+    """The oracle (the reference algorithm in C, OpenMP over neurons with one
+    barrier per layer) on the host: the whole batch on every thread the box
+    grants and a prefix on one thread, each the median of `reps` timed runs
+    after a warm-up; then one untimed run that keeps every layer for the
+    parity summary."""
+    import oracle
+    import vdttfs
+
+    c = oracle.Consts.from_task(w.consts)
+    rmode = oracle.READ_ARGMAX if w.readout == vdttfs.READOUT_ARGMAX else oracle.READ_ARGMIN
+    same = bool(w.consts.conv_same_pad)
+    B = len(gpu_pred)
+
+    def run(n, t, keep=False):
+        return oracle.net_forward(c, w.layers, n, img[:n], w.img_elems, oracle.ENC_LINEAR, w.tc_in, w.td_in,
+                                  rmode, same_pad=same, keep_layers=keep, nthreads=t)
+
+    run(1, 1)  # warm-up (page-in, OpenMP pool)
+    n1 = min(n1, B)
+    ta, ta_all, ra = median_time(lambda: run(B, thr), reps)
+    t1, t1_all, r1 = median_time(lambda: run(n1, 1), reps)
+    ref = run(B, thr, keep=True)
+    match = bool(np.array_equal(ra["pred"], gpu_pred) and np.array_equal(r1["pred"], gpu_pred[:n1]))
+    return {
+        "value": B / ta,
+        "unit": "images/s",
+        "cores": thr,
+        "kind": "port",
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
+        "sample": f"the whole batch of {B} images, whole network, {thr} OpenMP threads, median of {reps} "
+                  f"({', '.join(f'{t:.2f}' for t in ta_all)} s); 1 thread on the first {n1} images, median of "
+                  f"{reps} ({', '.join(f'{t:.2f}' for t in t1_all)} s): {n1 / t1:.3f} images/s",
+        "single_thread_value": n1 / t1,
+        "pred_match_gpu": match,
+    }, ref
+
+
+def bench_ttfs(args) -> int:
+    """Configs 3 (VGG-16, the headline) and 2 (LeNet-5)."""
+    import vdttfs
+    from vdttfs import models
+
+    vgg = args.workload == "vgg16"
+    B = args.batch or (256 if vgg else 1024)
+    if vgg:
+        w = models.vgg16(delta=args.delta or 8)
+        metric = METRIC
+        workload = "VGG-16 TTFS-SNN, config 3 (3x32x32, 13 conv + FC 512-512-10)"
+        tag = f"vgg16_b{B}"
+    else:
+        w = models.lenet5(delta=args.delta or 16)
+        metric = f"images/sec/GPU for LeNet-5 TTFS bs={B}; integrator % of HBM peak"
+        workload = "LeNet-5 TTFS-SNN, config 2 (1x28x28, conv 6/16 + FC 256-120-84-10)"
+        tag = f"lenet5_b{B}"
+    src = sources_hash()
+    key = (f"{'vgg16' if vgg else 'lenet5'} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs:g} "
+           f"plans={'tuned' if args.plans else 'built-in'} src={src}")
+    img = models.images_for(w, B)
+    ctx = vdttfs.Context(w.consts, 0)
+    net = vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
+    if args.plans:
+        from vdttfs import tune
+        tune.apply_plans(net, tune.load_plans(args.plans, w, B))
+    d_img = ctx.to_device(img)
+    d_pred = ctx.empty(B, np.int32)
+    log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
+        f"params={w.n_params} plans={args.plans or 'built-in'} key={key}")
+
+    for _ in range(args.warmup):
+        net.forward(d_img, d_pred)
+    ctx.synchronize()
+    # throughput: K forwards, no instrumentation inside the timed region
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        net.forward(d_img, d_pred)
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    gpu_pred = d_pred.download()
+    log(f"bench: {args.steps} forwards in {elapsed * 1e3:.2f} ms")
+
+    # a separate pass with HIP events around each layer's integrate (on the
+    # library's own stream) for the per-layer and integrator times
+    net.read_timing()
+    net.read_layer_timing()
+    net.set_timing(True)
+    for _ in range(args.steps):
+        net.forward(d_img, d_pred)
+    net.set_timing(False)
+    integ_ms, integ_n, bkt_ms, bkt_n = net.read_timing()
+    layer_ms = net.read_layer_timing() / args.steps
+    integ_ms_step = (integ_ms + bkt_ms) / args.steps
+    launches_per_step = integ_n / args.steps
+
+    counts = net.count(d_img)
+    eproc, ebin, n_ev, n_cols = counts
+    net.forward(d_img, d_pred)
+    ctx.synchronize()
+    roofs = gather_roofs(ctx)
+    tr = measured_traffic(tag, key)
+    rows = work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr)
+    gpu_outs = [net.layer_output(i) for i in range(len(w.layers))]
+
+    ms_step = elapsed * 1000.0 / args.steps
+    integ_s = integ_ms_step * 1e-3
+    alg = sum(r["algorithmic_hbm_bytes"] for r in rows)
+    gathered = sum(4.0 * r["ebin"] for r in rows)
+    # time the layers would take at their gather roof, over the time they took
+    t_roof = sum(4.0 * r["ebin"] / (r["gather_roof_GBps"] * 1e9) for r in rows)
+    dense = 0
+    for l in w.layers:
+        if l.kind == 0:
+            dense += B * l.H_out * l.W_out * l.C_out * l.K_h * l.K_w * l.C_in
+        elif l.kind == 1:
+            dense += B * l.C_out * l.H_in * l.W_in * l.C_in
+    hbm = tr["per_step"] / integ_s / 1e9 if tr else None
+    out = {
+        "metric": metric,
+        "value": B / (ms_step * 1e-3),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded splitmix64 U[0,1) images, Kaiming-normal weights (random init)",
+        "config": {"workload": workload, "key": key,
+                   "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
+                   "seed": w.seed, "parallelism": "none (one GPU)",
+                   "plans": os.path.relpath(args.plans, ROOT) if args.plans else "built-in"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": hbm,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": hbm / HBM_PEAK_GBS if tr else None,
+            "traffic": tr["per_step"] / tr["launches"] if tr else None,
+            "kernel": "integrator = one layer's list build + stream: k_stream_dense (conv, C_in <= 64, "
+                      "32 <= C_out <= 64: list built in LDS), k_merge_dense + k_stream (other conv, "
+                      "C_in <= 64) or k_bucketize + k_merge + k_stream (wider conv, FC); layers with C_out < 32 "
+                      "stream with k_stream_narrow, or with k_conv_small when the receptive field has <= 32 "
+                      "elements.  A launch is one layer's integrate; achieved = rocprofv3 FETCH_SIZE + "
+                      "WRITE_SIZE bytes of the integrator dispatches of one forward / the live HIP-event "
+                      "integrator time of a forward",
+            "traffic_per_step": tr["per_step"] if tr else None,
+            "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
+                               f"no counter summary for {key} in profiles/"),
+            "integrator_ms_per_step": integ_ms_step,
+            "integrator_ms_per_launch": integ_ms_step / max(launches_per_step, 1),
+            "integrator_launches_per_step": launches_per_step,
+            "algorithmic_hbm_bytes_per_launch": alg / max(launches_per_step, 1),
+            "algorithmic_hbm_GBps": alg / integ_s / 1e9,
+            "algorithmic_hbm_frac": alg / integ_s / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_hbm_model": "per layer 4 B x (input map + weights + bias + output map): one fused pass",
+            "gathered": {
+                "bytes_per_step": gathered,
+                "achieved_GBps": gathered / integ_s / 1e9,
+                "roof_GBps_dword": roofs[1]["GBps"],
+                "roof_GBps_dwordx4": roofs[4]["GBps"],
+                "frac": t_roof / integ_s,
+                "model": "4 B per integrated synapse under the per-bin exit the kernels run (E_bin); roof = "
+                         "vdttfs_probe_gather with weights in one XCD's L2, dword rows for layers gathering one "
+                         "c_out per lane, dwordx4 rows for the others; frac = (time at each layer's roof) / "
+                         "(integrator time)",
+                "probe": roofs,
+            },
+        },
+        "layers": rows,
+        "bucketize_ms_per_step": bkt_ms / args.steps,
+        "eproc_per_image": float(eproc.sum()) / B,
+        "ebin_per_image": float(ebin.sum()) / B,
+        "e_noee_per_image": float(sum(r["e_noee"] for r in rows)) / B,
+        "early_exit_skip_rate": 1.0 - float(eproc.sum()) / max(1, sum(r["e_noee"] for r in rows)),
+        "dense_macs_per_image": dense / B,
+        "retained_events_per_image": float(n_ev.sum()) / B,
+    }
+    if not args.no_host_scope:
+        hs, hpred = host_scope(ctx, net, w, img, B, args.steps)
+        hs["pred_match_device"] = bool(np.array_equal(hpred, gpu_pred))
+        out["with_h2d_d2h"] = hs
+        if vgg:
+            ds = dropin_scope(w, img, gpu_pred, B)
+            if "layers" in ds:
+                for r in rows:
+                    d = ds["layers"].get(r["layer"])
+                    if d:
+                        r["dropin_launch_ms"] = d["launch_ms"]
+                        r["dropin_over_engine"] = d["launch_ms"] / r["ms"] if r["ms"] > 0 else None
+                ds.pop("layers")
+            out["reference_scope_dropin"] = ds
+    if not args.no_cpu:
+        cb, ref = cpu_baseline(w, img, gpu_pred, threads_all(), n1=8 if vgg else 256)
+        out["cpu_baseline"] = cb
+        out["x_cpu_all_cores"] = out["value"] / cb["value"]
+        out["parity"] = parity_summary(ctx, w, B, gpu_outs, gpu_pred, ref)
+    net.close()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def bench_culif(args) -> int:
     """Config 4: 7-layer CuLIF SNN on a synthetic 2x128x128 event stream."""
     import vdttfs
-    from vdttfs import models
+    from vdttfs import models, workcount
 
     B = args.batch or 64
     w = models.culif7(delta=args.delta or 32)
@@ -165,37 +597,60 @@ def bench_culif(args) -> int:
     net = vdttfs.CulifNet(ctx, w.layers, B)
     d_ev = ctx.to_device(ev)
     d_pred = ctx.empty(B, np.int32)
-    log(f"bench: {w.name} B={B} T={T} delta={D} params={w.n_params}")
+    src = sources_hash()
+    tag, key = f"culif7_b{B}", f"culif7 B={B} T={T} delta={D} src={src}"
+    log(f"bench: {w.name} B={B} T={T} delta={D} params={w.n_params} key={key}")
     for _ in range(args.warmup):
         net.forward(d_ev, d_pred)
-    ctx.synchronize()
-    net.read_timing()
-    net.set_timing(True)
     ctx.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         net.forward(d_ev, d_pred)
     ctx.synchronize()
     elapsed = time.perf_counter() - t0
+    gpu_pred = d_pred.download()
+    net.read_timing()
+    net.set_timing(True)
+    for _ in range(args.steps):
+        net.forward(d_ev, d_pred)
     net.set_timing(False)
     ms_layers, _ = net.read_timing()
     ms_layers = ms_layers / args.steps
-    gpu_pred = d_pred.download()
     eproc, ebin, n_ev, n_cols = net.count(d_ev)
-    OS = T // D + 1
+    net.forward(d_ev, d_pred)
+    ctx.synchronize()
+    roofs = gather_roofs(ctx)
+    tr = measured_traffic(tag, key)
     conv = [i for i, l in enumerate(w.layers) if l.kind == vdttfs.CULIF_CONV]
-    b_conv = 0
-    for i in conv:
+    rows, alg, gathered, t_roof = [], 0, 0.0, 0.0
+    for li, i in enumerate(conv):
         l = w.layers[i]
-        n_out = B * l.H_in * l.W_in * l.C_out
-        # fused form: the dense input map is read by bucketize, the rest is B_int
-        b_conv += (4 * int(eproc[i]) + 8 * int(n_ev[i]) + 4 * OS * int(n_cols[i]) + 4 * l.C_out
-                   + 4 * n_out + 4 * int(n_cols[i]) * l.C_in)
-    conv_ms = float(sum(ms_layers[i] for i in conv))
-    achieved = b_conv / (conv_ms * 1e-3) / 1e9
+        x = net.layer_output(i - 1, layout="nhwc")
+        e_noee, nev = workcount.no_exit_synapses(x, B, l.H_in, l.W_in, l.C_in, l.H_in, l.W_in, l.C_out, 3, 3, 1,
+                                                 1, False, 0.0, T)
+        ms = float(ms_layers[i])
+        roof = roofs[4] if (l.C_out % 4 == 0 and l.C_out > 64) else roofs[1]
+        gb = 4.0 * float(ebin[i])
+        n_in, n_out = B * l.H_in * l.W_in * l.C_in, B * l.H_in * l.W_in * l.C_out
+        hb = 4 * (n_in + 9 * l.C_in * l.C_out + n_out)
+        row = {"layer": i, "shape": f"{l.C_in}->{l.C_out} @ {l.H_in}x{l.W_in}, 3x3", "ms": ms,
+               "eproc": int(eproc[i]), "ebin": int(ebin[i]), "e_noee": e_noee,
+               "skip_rate": 1.0 - float(eproc[i]) / max(1, e_noee), "n_ev": int(n_ev[i]),
+               "n_ev_host_equal": nev == int(n_ev[i]), "in_density": nev / float(x.size),
+               "gathered_GBps": gb / (ms * 1e-3) / 1e9, "gather_roof_GBps": roof["GBps"],
+               "gather_frac": gb / (ms * 1e-3) / 1e9 / roof["GBps"], "algorithmic_hbm_bytes": hb}
+        if tr and li < len(tr["layers"]):
+            row["hbm_bytes"] = tr["layers"][li][0] + tr["layers"][li][1]
+            row["hbm_frac"] = row["hbm_bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+        rows.append(row)
+        alg += hb
+        gathered += gb
+        t_roof += gb / (roof["GBps"] * 1e9)
+    conv_s = sum(r["ms"] for r in rows) * 1e-3
     l0 = w.layers[0]
     raw_bytes = B * l0.C_in * l0.H_in * l0.W_in * T * 4 + B * l0.C_out * l0.H_in * l0.W_in * 4
     ms_step = elapsed * 1000.0 / args.steps
+    hbm = tr["per_step"] / conv_s / 1e9 if tr else None
     out = {
         "metric": f"samples/sec/GPU for CuLIF-7 DVS bs={B}; conv integrator % of HBM peak",
         "value": B / (ms_step * 1e-3),
@@ -211,46 +666,51 @@ def bench_culif(args) -> int:
         "data": "synthetic: moving Gaussian blob events (sigma 12 px, density 0.03), Kaiming-normal "
                 "weights (random init)",
         "config": {"workload": "CuLIF-7 SNN, config 4 (2x128x128 events, conv 64/128/128, "
-                               "recurrent FC 131072-128, FC 128-11)",
+                               "recurrent FC 131072-128, FC 128-11)", "key": key,
                    "batch": B, "T": T, "delta": D, "decay": w.meta["decay"], "th": w.meta["th"],
                    "seed": w.seed, "parallelism": "none (one GPU)"},
         "roofline": {
             "bound": "hbm",
-            "achieved": achieved,
+            "achieved": hbm,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "conv layers after conv1 (C_in <= 64: k_merge_dense + k_stream<CuLIF>; "
-                      "wider: k_bucketize + k_merge + k_stream<CuLIF>); achieved = fused "
-                      "algorithmic bytes of those layers / their HIP-event time",
-            "algorithmic_bytes_per_step": b_conv,
-            "conv_ms_per_step": conv_ms,
+            "frac": hbm / HBM_PEAK_GBS if tr else None,
+            "traffic": tr["per_step"] / tr["launches"] if tr else None,
+            "kernel": "conv layers after conv1 (C_in <= 64: k_merge_dense + k_stream<CuLIF>; wider: "
+                      "k_bucketize + k_merge + k_stream<CuLIF>); achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                      "bytes of their dispatches / their live HIP-event time",
+            "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
+                               f"no counter summary for {key} in profiles/"),
+            "conv_ms_per_step": conv_s * 1e3,
+            "algorithmic_hbm_bytes_per_launch": alg / max(1, len(rows)),
+            "algorithmic_hbm_frac": alg / conv_s / 1e9 / HBM_PEAK_GBS,
+            "gathered": {"bytes_per_step": gathered, "achieved_GBps": gathered / conv_s / 1e9,
+                         "roof_GBps_dwordx4": roofs[4]["GBps"], "frac": t_roof / conv_s,
+                         "model": "4 B per synapse under the per-bin exit (E_bin); roof = vdttfs_probe_gather, "
+                                  "weights in one XCD's L2"},
         },
         "layers_ms": [round(float(x), 4) for x in ms_layers],
+        "conv_layers": rows,
         "conv1_raw_dense_GBps": raw_bytes / (float(ms_layers[0]) * 1e-3) / 1e9,
         "eproc_per_sample": float(eproc.sum()) / B,
         "ebin_per_sample": float(ebin.sum()) / B,
+        "early_exit_skip_rate": 1.0 - float(sum(r["eproc"] for r in rows)) / max(1, sum(r["e_noee"] for r in rows)),
     }
     if not args.no_cpu:
         import oracle
 
         thr = threads_all()
-
-        def run(n, t):
-            t0 = time.perf_counter()
-            _, pred = oracle.culif_net_forward(w.layers, ev[:n], n, T, D, t)
-            return time.perf_counter() - t0, pred
-
-        run(1, thr)  # warm-up
-        dt1, p1 = run(1, 1)
         nall = min(8, B)
-        dta, pa = run(nall, thr)
+        oracle.culif_net_forward(w.layers, ev[:1], 1, T, D, thr)  # warm-up
+        ta, ta_all, (_, pa) = median_time(lambda: oracle.culif_net_forward(w.layers, ev[:nall], nall, T, D, thr), 3)
+        t1, t1_all, (_, p1) = median_time(lambda: oracle.culif_net_forward(w.layers, ev[:1], 1, T, D, 1), 3)
         out["cpu_baseline"] = {
-            "value": nall / dta, "unit": "samples/s", "cores": thr, "kind": "port",
-            "sample": f"{nall} samples, whole network, {thr} OpenMP threads ({dta:.2f} s); "
-                      f"1 thread on 1 sample: {1.0 / dt1:.3f} samples/s",
-            "single_thread_value": 1.0 / dt1,
+            "value": nall / ta, "unit": "samples/s", "cores": thr, "kind": "port", "cpu_model": cpu_model(),
+            "host_cpus": os.cpu_count(),
+            "sample": f"{nall} samples, whole network, {thr} OpenMP threads, median of 3 "
+                      f"({', '.join(f'{t:.2f}' for t in ta_all)} s); 1 thread on 1 sample, median of 3: "
+                      f"{1.0 / t1:.3f} samples/s",
+            "single_thread_value": 1.0 / t1,
             "pred_match_gpu": bool(np.array_equal(pa, gpu_pred[:nall]) and p1[0] == gpu_pred[0]),
         }
         out["x_cpu_all_cores"] = out["value"] / out["cpu_baseline"]["value"]
@@ -262,58 +722,80 @@ def bench_culif(args) -> int:
     return 0
 
 
+FC_HEAD = (0.05, 64, 16)  # config 5's headline point: density, T', delta
+
+
+def fc_point(ctx, tc, layer, sp, B, reps, roofs):
+    """One config-5 point: a whole layer call (bucketize + merge + stream)
+    timed with HIP events on the library's stream."""
+    import vdttfs
+
+    cin = cout = 4096
+    Tp = tc.T
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_W, d_b = ctx.to_device(layer.kernel), ctx.to_device(layer.bias)
+    d_a, d_t = ctx.to_device(alpha), ctx.to_device(theta)
+    d_out = ctx.empty(B * cout)
+    d_in = ctx.to_device(sp)
+    call = lambda cnt=False: ctx.layer_forward(d_out, d_in, d_W, d_b, d_a, d_t, 0, B, 1, 1,  # noqa: E731
+                                               cin, 1, 1, cout, 1, 1, True, count=cnt)
+    call()
+    ctx.synchronize()
+    ctx.timer_begin()
+    for _ in range(reps):
+        call()
+    ms = ctx.timer_end() / reps
+    eproc, ebin = call(True)
+    for x in (d_W, d_b, d_a, d_t, d_out, d_in):
+        x.free()
+    n_ev = int(np.count_nonzero(sp < Tp))
+    e_noee = n_ev * cout
+    alg = 4 * (B * cin + cin * cout + cout + B * cout)
+    gb = 4.0 * ebin
+    roof = roofs[4]  # C_out = 4096: four c_out per lane (dwordx4)
+    return {"T_window": Tp, "delta": tc.delta, "ms": ms, "retained_density": n_ev / (B * cin),
+            "eproc": int(eproc), "ebin": int(ebin), "e_noee": e_noee,
+            "skip_rate": 1.0 - eproc / max(1, e_noee), "skip_rate_per_bin": 1.0 - ebin / max(1, e_noee),
+            "gathered_GBps": gb / (ms * 1e-3) / 1e9, "gather_frac": gb / (ms * 1e-3) / 1e9 / roof["GBps"],
+            "algorithmic_hbm_bytes": alg, "algorithmic_hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_fc_sweep(args) -> int:
     """Config 5: one FC 4096->4096 layer at B=512 over spike density, the
-    truncated window T' and delta.  Every point times one whole layer call
-    (bucketize + merge + stream) with HIP events on the library's stream."""
+    truncated window T' and delta (fc-point: the headline point alone, for
+    the counter profile)."""
     import vdttfs
     from vdttfs import models
 
     B = args.batch or 512
-    cin = cout = 4096
     layer = models.fc_sweep_layer()
-    dens = (0.01, 0.05, 0.2, 0.5)
-    spikes = {d: models.fc_sweep_spikes(5, B, cin, d) for d in dens}
+    point = args.workload == "fc-point"
+    dens = (FC_HEAD[0],) if point else (0.01, 0.05, 0.2, 0.5)
+    spikes = {d: models.fc_sweep_spikes(5, B, 4096, d) for d in dens}
     reps = max(1, min(args.steps, 10))
-    rows = []
-    for Tp in (16, 32, 64):
-        for D in (8, 16, 32):
-            tc = vdttfs.TaskConsts(T=Tp, tfs=0.0, delta=D, alpha_by_time=False)
-            ctx = vdttfs.Context(tc, 0)
-            alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
-            d_W, d_b = ctx.to_device(layer.kernel), ctx.to_device(layer.bias)
-            d_a, d_t = ctx.to_device(alpha), ctx.to_device(theta)
-            d_out = ctx.empty(B * cout)
-            OS = tc.num_chunks + 1
-            for d in dens:
-                sp = spikes[d]
-                d_in = ctx.to_device(sp)
-                call = lambda cnt=False: ctx.layer_forward(d_out, d_in, d_W, d_b, d_a, d_t, 0, B, 1, 1,  # noqa: E731
-                                                           cin, 1, 1, cout, 1, 1, True, count=cnt)
-                call()
-                ctx.synchronize()
-                ctx.timer_begin()
-                for _ in range(reps):
-                    call()
-                ms = ctx.timer_end() / reps
-                eproc, ebin = call(True)
-                n_ev = int(np.count_nonzero(sp < Tp))
-                b_int = 4 * eproc + 8 * n_ev + 4 * OS * B + 4 * cout + 4 * B * cout
-                b_fused = b_int + 4 * B * cin
-                gbs = b_fused / (ms * 1e-3) / 1e9
-                rows.append({"density": d, "retained_density": n_ev / (B * cin), "T_window": Tp,
-                             "delta": D, "ms": ms, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
-                             "eproc": int(eproc), "ebin": int(ebin),
-                             "skip_rate": 1.0 - eproc / max(1, n_ev * cout),
-                             "skip_rate_per_bin": 1.0 - ebin / max(1, n_ev * cout)})
-                d_in.free()
-            for x in (d_W, d_b, d_a, d_t, d_out):
-                x.free()
-            ctx.close()
-    head = next(r for r in rows if r["density"] == 0.05 and r["T_window"] == 64 and r["delta"] == 16)
+    grid = [(FC_HEAD[1], FC_HEAD[2])] if point else [(Tp, D) for Tp in (16, 32, 64) for D in (8, 16, 32)]
+    rows, head, roofs = [], None, None
+    for Tp, D in grid:
+        tc = vdttfs.TaskConsts(T=Tp, tfs=0.0, delta=D, alpha_by_time=False)
+        ctx = vdttfs.Context(tc, 0)
+        if roofs is None:
+            roofs = gather_roofs(ctx)
+        for d in dens:
+            r = fc_point(ctx, tc, layer, spikes[d], B, reps, roofs)
+            r["density"] = d
+            rows.append(r)
+            if (d, Tp, D) == FC_HEAD:
+                head = r
+        ctx.close()
+    src = sources_hash()
+    tag, key = f"fc4096_b{B}", f"fc4096 B={B} density={FC_HEAD[0]} T={FC_HEAD[1]} delta={FC_HEAD[2]} src={src}"
+    tr = measured_traffic(tag, key)
+    hbm = tr["per_step"] / (head["ms"] * 1e-3) / 1e9 if tr else None
     out = {
-        "metric": f"integrator GB/s, FC 4096x4096 bs={B} (config 5 sweep; value at density 5%, T'=64, delta=16)",
-        "value": head["achieved_GBps"],
+        "metric": f"integrator GB/s, FC 4096x4096 bs={B} (config 5; value at density 5%, T'=64, delta=16)",
+        "value": hbm if hbm is not None else head["gathered_GBps"],
+        "value_kind": "HBM GB/s from rocprofv3 counters" if hbm is not None else
+                      "gathered GB/s (no counter summary for this build)",
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": reps,
@@ -325,12 +807,19 @@ def bench_fc_sweep(args) -> int:
         "dtype": "f32",
         "data": "synthetic: per (image, input) active with the given density, time uniform in "
                 "[0,64); Gaussian N(0, 2/4096) weights",
-        "config": {"workload": "FC 4096x4096 integrator sweep, config 5", "batch": B,
-                   "parallelism": "none (one GPU)"},
-        "roofline": {"bound": "hbm", "achieved": head["achieved_GBps"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac"], "traffic": None,
-                     "kernel": "one layer call = bucketize + k_merge + k_stream; fused algorithmic "
-                               "bytes B_int + 4*N_cols*C_in"},
+        "config": {"workload": "FC 4096x4096 integrator " + ("point" if point else "sweep") + ", config 5",
+                   "key": key, "batch": B, "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "achieved": hbm, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": hbm / HBM_PEAK_GBS if tr else None,
+                     "traffic": tr["per_step"] if tr else None,
+                     "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
+                                        f"no counter summary for {key} in profiles/"),
+                     "kernel": "one layer call = k_bucketize + k_merge<1> + k_stream (dwordx4, 4 c_out per lane); "
+                               "the 64 MiB weight matrix exceeds the 32 MB of aggregate L2",
+                     "algorithmic_hbm_bytes_per_launch": head["algorithmic_hbm_bytes"],
+                     "algorithmic_hbm_frac": head["algorithmic_hbm_frac"],
+                     "gathered": {"achieved_GBps": head["gathered_GBps"], "frac": head["gather_frac"],
+                                  "roof_GBps_dwordx4": roofs[4]["GBps"]}},
         "sweep": rows,
     }
     print(json.dumps(out), flush=True)
@@ -343,18 +832,22 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="vgg16",
-                    choices=["vgg16", "lenet5", "culif7", "fc-sweep", "vgg16-timedriven", "lenet5-timedriven",
-                             "culif7-timedriven"])
+                    choices=["vgg16", "lenet5", "culif7", "fc-sweep", "fc-point", "vgg16-timedriven",
+                             "lenet5-timedriven", "culif7-timedriven"])
     ap.add_argument("--batch", type=int, default=None,
                     help="default: 256 (vgg16), 1024 (lenet5), 64 (culif7), 512 (fc-sweep)")
     ap.add_argument("--delta", type=int, default=None,
                     help="default: 8 (vgg16), 16 (lenet5), 32 (culif7)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg (and the parity summary)")
+    ap.add_argument("--no-host-scope", action="store_true",
+                    help="skip the H2D/D2H-inclusive and drop-in (reference scope) legs")
     ap.add_argument("--plans", default=None,
                     help="vgg16/lenet5: per-layer launch plans written by python -m vdttfs.tune --out "
                          "(default: the library's built-in choice)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size copy used to scale FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--gather-probe", action="store_true",
+                    help="run only the gather-roof probe sweep (footprint x gather width)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (every image "
@@ -362,12 +855,14 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.gather_probe:
+        return gather_probe(args)
     if args.plans and args.workload not in ("vgg16", "lenet5"):
         print(f"--plans applies to the vgg16 and lenet5 engine workloads, not {args.workload}", file=sys.stderr)
         return 2
     if args.workload == "culif7":
         return bench_culif(args)
-    if args.workload == "fc-sweep":
+    if args.workload in ("fc-sweep", "fc-point"):
         return bench_fc_sweep(args)
     if args.workload.endswith("-timedriven"):
         return bench_timedriven(args)
@@ -505,120 +1000,6 @@ def bench_timedriven_culif(args) -> int:
         "speedup_event_driven": ms_td / ms_ev,
         "prediction_agreement": float(np.mean(pred_td == pred_ev)),
     }
-    print(json.dumps(out), flush=True)
-    return 0
-
-
-def bench_ttfs(args) -> int:
-    """Configs 3 (VGG-16, the headline) and 2 (LeNet-5)."""
-    import vdttfs
-    from vdttfs import models
-
-    vgg = args.workload == "vgg16"
-    B = args.batch or (256 if vgg else 1024)
-    if vgg:
-        w = models.vgg16(delta=args.delta or 8)
-        metric = METRIC
-        workload = "VGG-16 TTFS-SNN, config 3 (3x32x32, 13 conv + FC 512-512-10)"
-    else:
-        w = models.lenet5(delta=args.delta or 16)
-        metric = f"images/sec/GPU for LeNet-5 TTFS bs={B}; integrator % of HBM peak"
-        workload = "LeNet-5 TTFS-SNN, config 2 (1x28x28, conv 6/16 + FC 256-120-84-10)"
-    img = models.images_for(w, B)
-    ctx = vdttfs.Context(w.consts, 0)
-    net = vdttfs.Net(ctx, w.layers, B, w.img_elems, vdttfs.ENCODE_LINEAR, w.tc_in, w.td_in, w.readout)
-    if args.plans:
-        from vdttfs import tune
-        tune.apply_plans(net, tune.load_plans(args.plans, w, B))
-    d_img = ctx.to_device(img)
-    d_pred = ctx.empty(B, np.int32)
-    log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
-        f"params={w.n_params} plans={args.plans or 'built-in'}")
-
-    for _ in range(args.warmup):
-        net.forward(d_img, d_pred)
-    ctx.synchronize()
-    net.read_timing()  # reset
-
-    net.set_timing(True)
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        net.forward(d_img, d_pred)
-    ctx.synchronize()
-    elapsed = time.perf_counter() - t0
-    net.set_timing(False)
-    integ_ms, integ_n, bkt_ms, bkt_n = net.read_timing()
-    layer_ms = net.read_layer_timing() / args.steps
-    gpu_pred = d_pred.download()
-
-    eproc, ebin, n_ev, n_cols = net.count(d_img)
-    b_int, per_layer = algorithmic_bytes(w, eproc, n_ev, n_cols, B)
-    ms_step = elapsed * 1000.0 / args.steps
-    # a layer's whole integrate: the bucketize pass (FC layers) + merge + stream
-    integ_ms_step = (integ_ms + bkt_ms) / args.steps
-    launches_per_step = integ_n / args.steps
-    achieved = b_int / (integ_ms_step * 1e-3) / 1e9
-    key = workload_key(B, w.consts) if vgg else f"{w.name} B={B} T={w.consts.T} delta={w.consts.delta}"
-    tr = measured_traffic(key)
-    dense = 0
-    for l in w.layers:
-        if l.kind == 0:
-            dense += B * l.H_out * l.W_out * l.C_out * l.K_h * l.K_w * l.C_in
-        elif l.kind == 1:
-            dense += B * l.C_out * l.H_in * l.W_in * l.C_in
-    out = {
-        "metric": metric,
-        "value": B / (ms_step * 1e-3),
-        "unit": "images/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded splitmix64 U[0,1) images, Kaiming-normal weights (random init)",
-        "config": {"workload": workload,
-                   "key": key,
-                   "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
-                   "seed": w.seed, "parallelism": "none (one GPU)",
-                   "plans": os.path.relpath(args.plans, ROOT) if args.plans else "built-in"},
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": (tr[0] / tr[1]) if tr else None,
-            "kernel": "integrator = a layer's k_stream_dense (conv, C_in <= 64, 32 <= C_out <= 64: "
-                      "list built in LDS), k_merge_dense + k_stream (other conv, C_in <= 64) or "
-                      "k_bucketize + k_merge + k_stream (wider conv, FC); layers with C_out < 32 "
-                      "stream with k_stream_narrow, or with k_conv_small (no list) when the receptive "
-                      "field has <= 32 elements; a launch is one layer's integrate, achieved = "
-                      "fused algorithmic bytes of a step / integrator time of a step",
-            "algorithmic_bytes_per_step": b_int,
-            "algorithmic_bytes_per_launch": b_int / max(launches_per_step, 1),
-            "traffic_per_step": tr[0] if tr else None,
-            "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if tr else None,
-            "integrator_ms_per_step": integ_ms_step,
-            "integrator_launches_per_step": launches_per_step,
-        },
-        "bucketize_ms_per_step": bkt_ms / args.steps,
-        "layers_ms": {str(i): round(float(v), 4) for i, v in enumerate(layer_ms) if v > 0},
-        "eproc_per_image": float(eproc.sum()) / B,
-        "ebin_per_image": float(ebin.sum()) / B,
-        "dense_macs_per_image": dense / B,
-        "retained_events_per_image": float(n_ev.sum()) / B,
-    }
-    if not args.no_cpu:
-        thr = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-        cb = cpu_baseline(w, img, gpu_pred, thr, n1=16 if vgg else 256)
-        out["cpu_baseline"] = cb
-        out["x_cpu_all_cores"] = out["value"] / cb["value"]
-    net.close()
-    ctx.close()
     print(json.dumps(out), flush=True)
     return 0
 

@@ -108,7 +108,12 @@ int vdttfs_bucketize(vdttfs_ctx* ctx, const float* d_in, int64_t n_cols, int c_i
 
 /* ---- k_conv_bucketed (T1V:83-162, T2V:84-170) -------------------------- */
 /* Consumes the reference bucket layout; writes first-spike times (INF if a
- * neuron never fires), NHWC with c_out fastest. */
+ * neuron never fires), NHWC with c_out fastest.  This is the reference-layout
+ * export path, kept for bit-exact checks of caller-made buckets: one thread
+ * per neuron, several times slower than vdttfs_layer_forward, which takes the
+ * dense map.  Buckets are expected from this context's constants; events
+ * outside their chunk's bins or the window, at cin >= C_in, and offsets past
+ * the column are skipped / clamped rather than read out of range. */
 int vdttfs_integrate(vdttfs_ctx* ctx, float* d_out, const int32_t* d_bkt_cin,
                      const float* d_bkt_tin, const int32_t* d_bkt_off, const float* d_kernel,
                      const float* d_bias, const float* d_lut_decay, const float* d_lut_th,
@@ -142,8 +147,12 @@ int vdttfs_readout_argmin(vdttfs_ctx* ctx, const float* d_out, int B, int C, int
 int vdttfs_readout_argmax(vdttfs_ctx* ctx, const float* d_out, int B, int C, int32_t* d_pred);
 
 /* ---- per-layer launch wrappers (T1V:222-240, T2V:250-287) -------------- */
-/* Synchronous like the reference: bucketize + integrate (+ sync) with the
- * context's bucket scratch.  t_min = max(0, ceilf(td)) as T1V:225. */
+/* Synchronous like the reference: one layer's bucketize + integrate, then a
+ * stream synchronisation.  Runs the engine's kernels (the same as
+ * vdttfs_layer_forward, with the built-in launch plan and context-owned
+ * scratch); the reference's wrapper fills file-static buckets its caller
+ * never reads, so only d_out is observable, and it is bit-identical.
+ * t_min = max(0, ceilf(td)) as T1V:225. */
 int vdttfs_launch_layer_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, int H_in,
                              int W_in, int C_in, int H_out, int W_out, int C_out, int K_h,
                              int K_w, float td, const float* d_kernel, const float* d_bias,
@@ -414,6 +423,18 @@ int vdttfs_culif_net_count(vdttfs_culif_net* net, const float* d_data, uint64_t*
  * first-spike steps (9999 = none) and T. */
 int vdttfs_stepnet_create_culif(vdttfs_ctx* ctx, const vdttfs_culif_layer* layers, int n_layers, int B,
                                 vdttfs_stepnet** out);
+
+/* ---- gather-roof probe (measurement; no reference counterpart) --------- */
+/* The integrator's weight-gather pattern alone: `waves` waves each stream
+ * n_ev wave-uniform random row offsets (scalar loads, 8 per group) and issue
+ * one buffer_load of 4*vec bytes per lane per row (vec 1, 2 or 4: 256, 512 or
+ * 1024 B per wave-gather) into a buffer of footprint_bytes; one fma per dword.
+ * Allocates and frees its own buffers, times `reps` launches after a warm-up
+ * on the context stream and returns the milliseconds per launch.  The rate
+ * n_ev * waves * 256 * vec bytes / time is the roof the stream kernels are
+ * held against (footprints inside one XCD's L2 model a layer's weights). */
+int vdttfs_probe_gather(vdttfs_ctx* ctx, int vec, int64_t footprint_bytes, int n_ev, int64_t waves, int reps,
+                        double* ms_per_launch);
 
 /* ---- synthetic workloads (counter-mode splitmix64; host) --------------- */
 /* u = (z>>40) * 2^-24 with z = mix(seed + 0x9E3779B97F4A7C15*(stream*2^40+i+1)). */

@@ -30,7 +30,8 @@ class OrcConsts(C.Structure):
 class OrcLayer(C.Structure):
     _fields_ = [("kind", C.c_int), ("H_in", C.c_int), ("W_in", C.c_int), ("C_in", C.c_int),
                 ("H_out", C.c_int), ("W_out", C.c_int), ("C_out", C.c_int), ("K_h", C.c_int),
-                ("K_w", C.c_int), ("pad", C.c_int), ("W", C.POINTER(C.c_float)),
+                ("K_w", C.c_int), ("pad_h", C.c_int), ("pad_w", C.c_int),
+                ("W", C.POINTER(C.c_float)),
                 ("bias", C.POINTER(C.c_float)), ("tc_fire", C.c_float), ("td", C.c_float)]
 
 
@@ -46,6 +47,17 @@ def lib():
         _lib.orc_net_forward.restype = C.c_int
         _lib.orc_culif_neuron_steps.restype = C.c_float
     return _lib
+
+
+def pads(pad, K_h, K_w):
+    """(pad_h, pad_w) of a conv: a pair is taken as given; an int p means the
+    same p on both axes, which only a square kernel may use (T2V:109-110 pads
+    rows by K_h/2 and columns by K_w/2)."""
+    if isinstance(pad, (tuple, list)):
+        return int(pad[0]), int(pad[1])
+    if pad and K_h != K_w:
+        raise ValueError(f"non-square {K_h}x{K_w} kernel: pass pad as (pad_h, pad_w)")
+    return int(pad), int(pad)
 
 
 def _p(a):
@@ -117,7 +129,9 @@ def bucketize(c: Consts, spikes, n_cols, c_in, nthreads=0):
 
 def integrate(c: Consts, cin, tin, off, W, bias, alpha, theta, t_min, B, H_in, W_in, C_in, H_out,
               W_out, C_out, K_h, K_w, pad, is_fc, no_early_exit=False, nthreads=0):
-    """Returns (first-spike times, E_proc, E_bin)."""
+    """Returns (first-spike times, E_proc, E_bin).  pad: int (square kernels)
+    or (pad_h, pad_w)."""
+    ph, pw = pads(pad, K_h, K_w)
     n = B * (1 if is_fc else H_out * W_out) * C_out
     out = np.empty(n, np.float32)
     ep = C.c_uint64()
@@ -133,13 +147,14 @@ def integrate(c: Consts, cin, tin, off, W, bias, alpha, theta, t_min, B, H_in, W
     lib().orc_integrate(C.byref(cc), _p(out), _p(cin), _p(tin), _p(off), _p(W), _p(bias),
                         _p(alpha), _p(theta), C.c_int(t_min), C.c_int(B), C.c_int(H_in),
                         C.c_int(W_in), C.c_int(C_in), C.c_int(H_out), C.c_int(W_out),
-                        C.c_int(C_out), C.c_int(K_h), C.c_int(K_w), C.c_int(pad), C.c_int(int(is_fc)),
+                        C.c_int(C_out), C.c_int(K_h), C.c_int(K_w), C.c_int(ph), C.c_int(pw), C.c_int(int(is_fc)),
                         C.c_int(int(no_early_exit)), C.byref(ep), C.byref(eb), C.c_int(nthreads))
     return out, ep.value, eb.value
 
 
 def integrate_timedriven(c: Consts, spikes, W, bias, alpha, theta, t_min, B, H_in, W_in, C_in,
                          H_out, W_out, C_out, K_h, K_w, pad, is_fc, nthreads=0):
+    ph, pw = pads(pad, K_h, K_w)
     n = B * (1 if is_fc else H_out * W_out) * C_out
     out = np.empty(n, np.float32)
     cc = c.c()
@@ -147,13 +162,14 @@ def integrate_timedriven(c: Consts, spikes, W, bias, alpha, theta, t_min, B, H_i
     lib().orc_integrate_timedriven(C.byref(cc), _p(out), _p(sp), _p(W), _p(bias), _p(alpha),
                                    _p(theta), C.c_int(t_min), C.c_int(B), C.c_int(H_in),
                                    C.c_int(W_in), C.c_int(C_in), C.c_int(H_out), C.c_int(W_out),
-                                   C.c_int(C_out), C.c_int(K_h), C.c_int(K_w), C.c_int(pad),
-                                   C.c_int(int(is_fc)), C.c_int(nthreads))
+                                   C.c_int(C_out), C.c_int(K_h), C.c_int(K_w), C.c_int(ph),
+                                   C.c_int(pw), C.c_int(int(is_fc)), C.c_int(nthreads))
     return out
 
 
 def integrate_margin(c: Consts, spikes, W, bias, alpha, theta, t_min, B, H_in, W_in, C_in, H_out,
                      W_out, C_out, K_h, K_w, pad, is_fc, nthreads=0):
+    ph, pw = pads(pad, K_h, K_w)
     n = B * (1 if is_fc else H_out * W_out) * C_out
     out = np.empty(n, np.float64)
     cc = c.c()
@@ -161,8 +177,8 @@ def integrate_margin(c: Consts, spikes, W, bias, alpha, theta, t_min, B, H_in, W
     lib().orc_integrate_margin(C.byref(cc), _p(out), _p(sp), _p(W), _p(bias), _p(alpha), _p(theta),
                                C.c_int(t_min), C.c_int(B), C.c_int(H_in), C.c_int(W_in),
                                C.c_int(C_in), C.c_int(H_out), C.c_int(W_out), C.c_int(C_out),
-                               C.c_int(K_h), C.c_int(K_w), C.c_int(pad), C.c_int(int(is_fc)),
-                               C.c_int(nthreads))
+                               C.c_int(K_h), C.c_int(K_w), C.c_int(ph), C.c_int(pw),
+                               C.c_int(int(is_fc)), C.c_int(nthreads))
     return out
 
 
@@ -203,10 +219,10 @@ def net_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td_in,
         k = f32(l.kernel) if l.kernel is not None else None
         b = f32(l.bias) if l.bias is not None else None
         keep += [k, b]
-        pad = l.K_h // 2 if (l.kind == ORC_CONV and same_pad) else 0
+        same = l.kind == ORC_CONV and same_pad
         fp = C.POINTER(C.c_float)
         arr[i] = OrcLayer(l.kind, l.H_in, l.W_in, l.C_in, l.H_out, l.W_out, l.C_out, l.K_h, l.K_w,
-                          pad, k.ctypes.data_as(fp) if k is not None else fp(),
+                          l.K_h // 2 if same else 0, l.K_w // 2 if same else 0, k.ctypes.data_as(fp) if k is not None else fp(),
                           b.ctypes.data_as(fp) if b is not None else fp(), l.tc_fire, l.td)
     outs = [np.empty(B * l.H_out * l.W_out * l.C_out, np.float32) for l in layers] if keep_layers else None
     outs_p = (C.POINTER(C.c_float) * n)(*[o.ctypes.data_as(C.POINTER(C.c_float)) for o in outs]) if outs else None
@@ -243,9 +259,9 @@ def stepnet_forward(c: Consts, layers, B, img, img_elems, encode_mode, tc_in, td
         k = f32(l.kernel) if l.kernel is not None else None
         b = f32(l.bias) if l.bias is not None else None
         keep += [k, b]
-        pad = l.K_h // 2 if (l.kind == ORC_CONV and same_pad) else 0
+        same = l.kind == ORC_CONV and same_pad
         arr[i] = OrcLayer(l.kind, l.H_in, l.W_in, l.C_in, l.H_out, l.W_out, l.C_out, l.K_h, l.K_w,
-                          pad, k.ctypes.data_as(fp) if k is not None else fp(),
+                          l.K_h // 2 if same else 0, l.K_w // 2 if same else 0, k.ctypes.data_as(fp) if k is not None else fp(),
                           b.ctypes.data_as(fp) if b is not None else fp(), l.tc_fire, l.td)
     last = layers[-1]
     final = np.empty(B * last.H_out * last.W_out * last.C_out, np.float32)

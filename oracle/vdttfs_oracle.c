@@ -134,7 +134,7 @@ void orc_integrate(const orc_consts* c, float* out,
                    const int32_t* bcin, const float* btin, const int32_t* boff,
                    const float* W, const float* bias, const float* alpha, const float* theta,
                    int t_min, int B, int H_in, int W_in, int C_in,
-                   int H_out, int W_out, int C_out, int K_h, int K_w, int pad, int is_fc,
+                   int H_out, int W_out, int C_out, int K_h, int K_w, int pad_h, int pad_w, int is_fc,
                    int no_early_exit, uint64_t* eproc, uint64_t* ebin, int nthreads) {
     const int T = c->T, D = c->delta, NC = orc_num_chunks(c), OS = NC + 1;
     const float tfs = c->tfs;
@@ -170,10 +170,10 @@ void orc_integrate(const orc_consts* c, float* out,
                 }
             } else {
                 for (int kh = 0; kh < K_h; ++kh) {
-                    int h_in = h_out - pad + kh;
+                    int h_in = h_out - pad_h + kh;
                     if (h_in < 0 || h_in >= H_in) continue;
                     for (int kw = 0; kw < K_w; ++kw) {
-                        int w_in = w_out - pad + kw;
+                        int w_in = w_out - pad_w + kw;
                         if (w_in < 0 || w_in >= W_in) continue;
                         int64_t col = ((int64_t)img * H_in + h_in) * W_in + w_in;
                         int s = boff[col * OS + tau], e = boff[col * OS + tau + 1];
@@ -230,7 +230,7 @@ void orc_integrate_timedriven(const orc_consts* c, float* out, const float* spik
                               const float* W, const float* bias, const float* alpha,
                               const float* theta, int t_min, int B, int H_in, int W_in,
                               int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
-                              int pad, int is_fc, int nthreads) {
+                              int pad_h, int pad_w, int is_fc, int nthreads) {
     const int T = c->T;
     const float tfs = c->tfs;
     const int64_t total = (int64_t)B * H_out * W_out * C_out;
@@ -244,10 +244,10 @@ void orc_integrate_timedriven(const orc_consts* c, float* out, const float* spik
             float acc = 0.0f;
             int kh_n = is_fc ? 1 : K_h, kw_n = is_fc ? 1 : K_w;
             for (int kh = 0; kh < kh_n; ++kh) {
-                int h_in = is_fc ? 0 : h_out - pad + kh;
+                int h_in = is_fc ? 0 : h_out - pad_h + kh;
                 if (h_in < 0 || h_in >= (is_fc ? 1 : H_in)) continue;
                 for (int kw = 0; kw < kw_n; ++kw) {
-                    int w_in = is_fc ? 0 : w_out - pad + kw;
+                    int w_in = is_fc ? 0 : w_out - pad_w + kw;
                     if (w_in < 0 || w_in >= (is_fc ? 1 : W_in)) continue;
                     int64_t col = is_fc ? img : ((int64_t)img * H_in + h_in) * W_in + w_in;
                     const float* src = spikes + col * (int64_t)C_in;
@@ -274,7 +274,7 @@ void orc_integrate_margin(const orc_consts* c, double* margin, const float* spik
                           const float* W, const float* bias, const float* alpha,
                           const float* theta, int t_min, int B, int H_in, int W_in,
                           int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
-                          int pad, int is_fc, int nthreads) {
+                          int pad_h, int pad_w, int is_fc, int nthreads) {
     const int T = c->T;
     const float tfs = c->tfs;
     const int64_t total = (int64_t)B * H_out * W_out * C_out;
@@ -290,10 +290,10 @@ void orc_integrate_margin(const orc_consts* c, double* margin, const float* spik
         /* scale first: sum |w*alpha| over the whole receptive field */
         int kh_n = is_fc ? 1 : K_h, kw_n = is_fc ? 1 : K_w;
         for (int kh = 0; kh < kh_n; ++kh) {
-            int h_in = is_fc ? 0 : h_out - pad + kh;
+            int h_in = is_fc ? 0 : h_out - pad_h + kh;
             if (h_in < 0 || h_in >= (is_fc ? 1 : H_in)) continue;
             for (int kw = 0; kw < kw_n; ++kw) {
-                int w_in = is_fc ? 0 : w_out - pad + kw;
+                int w_in = is_fc ? 0 : w_out - pad_w + kw;
                 if (w_in < 0 || w_in >= (is_fc ? 1 : W_in)) continue;
                 int64_t col = is_fc ? img : ((int64_t)img * H_in + h_in) * W_in + w_in;
                 const float* src = spikes + col * (int64_t)C_in;
@@ -313,10 +313,10 @@ void orc_integrate_margin(const orc_consts* c, double* margin, const float* spik
             float acc = 0.0f;
             double acc_d = 0.0;
             for (int kh = 0; kh < kh_n; ++kh) {
-                int h_in = is_fc ? 0 : h_out - pad + kh;
+                int h_in = is_fc ? 0 : h_out - pad_h + kh;
                 if (h_in < 0 || h_in >= (is_fc ? 1 : H_in)) continue;
                 for (int kw = 0; kw < kw_n; ++kw) {
-                    int w_in = is_fc ? 0 : w_out - pad + kw;
+                    int w_in = is_fc ? 0 : w_out - pad_w + kw;
                     if (w_in < 0 || w_in >= (is_fc ? 1 : W_in)) continue;
                     int64_t col = is_fc ? img : ((int64_t)img * H_in + h_in) * W_in + w_in;
                     const float* src = spikes + col * (int64_t)C_in;
@@ -486,7 +486,7 @@ int orc_net_forward(const orc_consts* c, const orc_layer* layers, int n_layers, 
                 orc_integrate(c, nxt, bcin, btin, boff, L->W, L->bias, alpha, theta, t_min, B,
                               is_fc ? 1 : L->H_in, is_fc ? 1 : L->W_in, cin,
                               is_fc ? 1 : L->H_out, is_fc ? 1 : L->W_out, L->C_out,
-                              is_fc ? 1 : L->K_h, is_fc ? 1 : L->K_w, L->pad, is_fc, 0, &ep, &eb,
+                              is_fc ? 1 : L->K_h, is_fc ? 1 : L->K_w, L->pad_h, L->pad_w, is_fc, 0, &ep, &eb,
                               nthreads);
                 if (eproc) eproc[l] = ep;
                 if (ebin) ebin[l] = eb;
@@ -638,10 +638,10 @@ int orc_stepnet_forward(const orc_consts* c, const orc_layer* layers, int n_laye
                                 }
                         } else {
                             for (int kh = 0; kh < L->K_h; ++kh) {
-                                int hi = ho - L->pad + kh;
+                                int hi = ho - L->pad_h + kh;
                                 if (hi < 0 || hi >= L->H_in) continue;
                                 for (int kw = 0; kw < L->K_w; ++kw) {
-                                    int wi = wo - L->pad + kw;
+                                    int wi = wo - L->pad_w + kw;
                                     if (wi < 0 || wi >= L->W_in) continue;
                                     const unsigned char* src =
                                         s_in + (((int64_t)im * L->H_in + hi) * L->W_in + wi) * L->C_in;

@@ -68,7 +68,8 @@ void orc_bucketize(const orc_consts* c, const float* in, int64_t n_cols, int c_i
                    int32_t* out_cin, float* out_tin, int32_t* out_off, int nthreads);
 
 /* k_conv_bucketed (T1V:83-162, T2V:84-170; E_proc as T2M:99-176).
- * pad = 0 gives T1V's valid conv; pad = K/2 with out-of-bounds skip gives T2V.
+ * pad_h = pad_w = 0 gives T1V's valid conv; pad_h = K_h/2, pad_w = K_w/2 with
+ * out-of-bounds taps skipped gives T2V's same conv (T2V:109-110, 136-141).
  * eproc: events integrated under the reference's chunk-granular exit.
  * ebin : events integrated under a per-bin exit (events with bin <= fire bin).
  * Either may be NULL. */
@@ -76,7 +77,7 @@ void orc_integrate(const orc_consts* c, float* out,
                    const int32_t* bcin, const float* btin, const int32_t* boff,
                    const float* W, const float* bias, const float* alpha, const float* theta,
                    int t_min, int B, int H_in, int W_in, int C_in,
-                   int H_out, int W_out, int C_out, int K_h, int K_w, int pad, int is_fc,
+                   int H_out, int W_out, int C_out, int K_h, int K_w, int pad_h, int pad_w, int is_fc,
                    int no_early_exit, uint64_t* eproc, uint64_t* ebin, int nthreads);
 
 /* Brute-force time-driven restatement of the same neuron: for every time bin
@@ -87,7 +88,7 @@ void orc_integrate_timedriven(const orc_consts* c, float* out, const float* spik
                               const float* W, const float* bias, const float* alpha,
                               const float* theta, int t_min, int B, int H_in, int W_in,
                               int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
-                              int pad, int is_fc, int nthreads);
+                              int pad_h, int pad_w, int is_fc, int nthreads);
 
 /* Decision margin in fp64 along the reference path: per neuron, the smallest
  * |carry - theta| / (|bias| + sum|w*alpha|) over every checked bin up to the
@@ -96,7 +97,7 @@ void orc_integrate_margin(const orc_consts* c, double* margin, const float* spik
                           const float* W, const float* bias, const float* alpha,
                           const float* theta, int t_min, int B, int H_in, int W_in,
                           int C_in, int H_out, int W_out, int C_out, int K_h, int K_w,
-                          int pad, int is_fc, int nthreads);
+                          int pad_h, int pad_w, int is_fc, int nthreads);
 
 /* k_pooling (T1V:164-181, T2V:192-209). */
 void orc_pool_min(const float* in, float* out, int B, int H_in, int W_in, int C, int nthreads);
@@ -119,7 +120,7 @@ enum { ORC_READ_ARGMIN = 0, ORC_READ_ARGMAX = 1, ORC_READ_T3 = 2 };
 
 typedef struct orc_layer {
     int kind;
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad;
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w;
     const float* W;
     const float* bias;
     float tc_fire, td;

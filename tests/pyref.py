@@ -105,7 +105,9 @@ def luts(T, vth, tc_i, td_i, tc_f, td_f):
 
 def integrate_dense(spikes, W, bias, alpha, theta, t_min, B, H_in, W_in, C_in, H_out, W_out, C_out,
                     K_h, K_w, pad, is_fc, T, tfs, alpha_by_time):
-    """First-spike time of every neuron, NHWC with c_out fastest."""
+    """First-spike time of every neuron, NHWC with c_out fastest.  pad: int
+    (both axes) or (pad_h, pad_w)."""
+    ph, pw = (pad if isinstance(pad, (tuple, list)) else (pad, pad))
     sp = np.asarray(spikes, np.float32).reshape(-1)
     Wf = np.asarray(W, np.float32).reshape(-1)
     out = []
@@ -123,7 +125,7 @@ def integrate_dense(spikes, W, bias, alpha, theta, t_min, B, H_in, W_in, C_in, H
                 acc = 0.0
                 for kh in range(1 if is_fc else K_h):
                     for kw in range(1 if is_fc else K_w):
-                        hi, wi = (0, 0) if is_fc else (ho - pad + kh, wo - pad + kw)
+                        hi, wi = (0, 0) if is_fc else (ho - ph + kh, wo - pw + kw)
                         if not is_fc and not (0 <= hi < H_in and 0 <= wi < W_in):
                             continue
                         col = img if is_fc else (img * H_in + hi) * W_in + wi

@@ -114,6 +114,16 @@ def test_vgg_driver_end_to_end(tmp_path):
     assert rc == 0, out
     assert out.count("-> Batch [") == 3, out
     assert re.search(r"Final Accuracy:\s+100%", out), out
+    # T2V's loop call for call on the drop-in entry points (update_luts,
+    # launch_layer_sync, launch_pool_sync, launch_fc_vmem_sync, host argmax),
+    # twice: the same classes, and one LAYER_MS line per layer
+    rc, out = run([drv("vdttfs_vgg"), "--weights", wp, "--data", d, "--n", str(N), "--batch", "10",
+                   "--T", "64", "--tfs", "32", "--delta", "8", "--encode", "linear",
+                   "--tc-in", str(w.tc_in), "--td-in", str(w.td_in), "--dropin", "--reps", "2"])
+    assert rc == 0, out
+    assert out.count("-> Batch [") == 6, out
+    assert len(re.findall(r"Final Accuracy:\s+100%", out)) == 2, out
+    assert len(re.findall(r"^LAYER_MS i=\d+ kind=\w+ lut_ms=\S+ launch_ms=\S+$", out, re.M)) == len(w.layers), out
 
 
 @pytest.mark.gpu

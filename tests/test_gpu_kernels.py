@@ -312,3 +312,50 @@ def test_pool_vmem_readout_encode(gpu_ctx_factory):
     # device logf may differ from glibc by an ulp: only ceil-boundary ties may move
     diff = np.flatnonzero(g != o)
     assert diff.size <= 2, diff
+
+
+def test_integrate_dropin_skips_foreign_events(gpu_ctx_factory):
+    """The drop-in integrator over caller buckets guards what the reference
+    leaves undefined (T2V:127-131 indexes delta[tb - base_t] and the weight
+    row unchecked): events appended to a column's last chunk that lie in
+    another chunk's bins, past the window, or at cin >= C_in are skipped, and
+    a last offset past the column is clamped.  The result equals the valid
+    buckets' output."""
+    say("drop-in integrate with foreign events")
+    rng = np.random.default_rng(4242)
+    T, tfs, delta = 64, 32.0, 8
+    tc = consts(T, tfs, delta, True)
+    ctx = gpu_ctx_factory(tc)
+    B, H, W, C_in, C_out, K = 2, 6, 6, 16, 64, 3
+    n_cols = B * H * W
+    t = rng.integers(0, T + 40, n_cols * C_in).astype(np.float32)
+    sp = np.where(rng.random(t.size) < 0.3, t, INF).astype(np.float32)
+    Wt = (rng.standard_normal(K * K * C_in * C_out) * 0.1).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.05).astype(np.float32)
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    shape = dict(B=B, H_in=H, W_in=W, C_in=C_in, H_out=H, W_out=W, C_out=C_out, K_h=K, K_w=K)
+    c = oracle.Consts.from_task(tc)
+    cin, tin, off = oracle.bucketize(c, sp, n_cols, C_in)
+    exp, _, _ = oracle.integrate(c, cin, tin, off, Wt, bias, alpha, theta, 0, pad=1, is_fc=False, **shape)
+    OS = tc.num_chunks + 1
+    NC = OS - 1
+    bad_c, bad_t, bad_o = cin.copy(), tin.copy(), off.copy()
+    foreign = [(C_in + 3, np.float32(tfs + T - 1)),   # cin past the input width
+               (2, np.float32(tfs + 1.0)),            # a bin of chunk 0
+               (5, np.float32(tfs + T + 7.0))]        # past the window
+    n_bad = 0
+    for col in range(n_cols):
+        n = int(off[col * OS + NC])
+        room = C_in - n
+        for k in range(min(room, len(foreign))):
+            bad_c[col * C_in + n + k], bad_t[col * C_in + n + k] = foreign[k]
+            n_bad += 1
+        bad_o[col * OS + NC] = n + min(room, len(foreign))
+        if room == 0:
+            bad_o[col * OS + NC] = C_in + 50  # clamped to the column
+    assert n_bad > n_cols
+    d_out = ctx.empty(exp.size, np.float32)
+    ctx.integrate(d_out, ctx.to_device(bad_c), ctx.to_device(bad_t), ctx.to_device(bad_o), ctx.to_device(Wt),
+                  ctx.to_device(bias), ctx.to_device(alpha), ctx.to_device(theta), 0, is_fc=False, **shape)
+    ctx.synchronize()
+    np.testing.assert_array_equal(d_out.download(), exp)

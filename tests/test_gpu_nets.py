@@ -84,37 +84,40 @@ def test_vgg16_config3_b16(gpu_ctx_factory):
     np.testing.assert_array_equal(counts[1], ref["ebin"])
 
 
-def test_vgg16_b256_delta_invariance_and_prefix(gpu_ctx_factory):
-    """Full benchmark size: outputs are bit-identical for every chunk width,
-    and the first images equal the oracle's (image b does not depend on B)."""
-    say("VGG-16 B=256 Delta invariance")
+def test_vgg16_b256_every_layer_vs_oracle(gpu_ctx_factory):
+    """Config 3 at the benchmark size: every layer's map of all 256 images,
+    the readout (1e-5 relative) and the classes equal the oracle's, and the
+    integrated-synapse counts too; outputs are bit-identical for every chunk
+    width."""
+    say("VGG-16 B=256 (config 3) every layer vs oracle")
     B = 256
-    finals = []
-    for delta in (8, 4, 16):
-        w = models.vgg16(delta=delta)
-        img = models.images_for(w, B)
-        ctx = gpu_ctx_factory(w.consts)
-        outs, pred, _ = run_engine(ctx, w, B, img)
-        finals.append((outs, pred))
-    for outs, pred in finals[1:]:
-        for a, b in zip(outs, finals[0][0]):
-            assert np.array_equal(a, b)
-        np.testing.assert_array_equal(pred, finals[0][1])
     w = models.vgg16()
-    ref = run_oracle(w, 4, models.images_for(w, 4))
-    np.testing.assert_array_equal(finals[0][1][:4], ref["pred"])
-    np.testing.assert_array_equal(finals[0][0][-1][:40], ref["final"])
+    img = models.images_for(w, B)
+    outs, pred, counts = run_engine(gpu_ctx_factory(w.consts), w, B, img, count=True)
+    ref = run_oracle(w, B, img)
+    check_layers(w, outs, ref)
+    np.testing.assert_array_equal(pred, ref["pred"])
+    np.testing.assert_array_equal(counts[0], ref["eproc"])
+    np.testing.assert_array_equal(counts[1], ref["ebin"])
+    for delta in (4, 16):
+        say(f"VGG-16 B=256 delta={delta}")
+        wd = models.vgg16(delta=delta)
+        outs_d, pred_d, _ = run_engine(gpu_ctx_factory(wd.consts), wd, B, models.images_for(wd, B))
+        for i, (a, b) in enumerate(zip(outs_d, outs)):
+            assert np.array_equal(a, b), f"layer {i} differs at delta={delta}"
+        np.testing.assert_array_equal(pred_d, pred)
 
 
 @pytest.mark.parametrize("density", [0.01, 0.05, 0.2, 0.5])
 def test_fc_sweep_config5(gpu_ctx_factory, density):
-    """Config 5 layer: B=512 on the GPU; the first 64 images against the
-    oracle, and bit-identical outputs across T'-preserving Delta choices."""
+    """Config 5 layer at every T' of the sweep (16, 32, 64): B=512 on the
+    GPU, the first 64 images against the oracle, and bit-identical outputs
+    across Delta in {8, 16, 32} (Delta > T' is one chunk cut at T')."""
     say(f"FC 4096x4096 sweep density={density}")
     B, cin, cout = 512, 4096, 4096
     layer = models.fc_sweep_layer()
     sp = models.fc_sweep_spikes(5, B, cin, density)
-    for Tp in (16, 64):
+    for Tp in (16, 32, 64):
         outs = []
         for delta in (8, 16, 32):  # delta > T' is one chunk cut at T' (T1V:152-153)
             tc = vdttfs.TaskConsts(T=Tp, tfs=0.0, delta=delta, alpha_by_time=False)

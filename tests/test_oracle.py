@@ -146,6 +146,30 @@ def test_integrate_matches_exact_bruteforce(T, tfs, delta, abt, is_fc, same):
     np.testing.assert_array_equal(got, exp)
 
 
+@pytest.mark.parametrize("K_h,K_w", [(1, 3), (3, 5), (5, 1)])
+def test_integrate_nonsquare_same_pad(K_h, K_w):
+    """Same padding is K_h/2 rows and K_w/2 columns (T2V:109-110); a
+    non-square kernel pins both axes against the exact brute force."""
+    rng = np.random.default_rng(77 + 10 * K_h + K_w)
+    T, tfs, delta = 16, 6.0, 4
+    B, H, W, C_in, C_out = 2, 5, 6, 3, 4
+    sp = rand_spikes(rng, B * H * W * C_in, T, extra_cases=False)
+    Wt = (rng.standard_normal(K_h * K_w * C_in * C_out) * 0.6).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.3).astype(np.float32)
+    alpha, theta = oracle.build_luts(T, 1.0, T / 4.0, 0.0, T / 4.0, 0.0)
+    c = oracle.Consts(T, tfs, delta, True)
+    shape = dict(B=B, H_in=H, W_in=W, C_in=C_in, H_out=H, W_out=W, C_out=C_out, K_h=K_h, K_w=K_w,
+                 pad=(K_h // 2, K_w // 2), is_fc=False)
+    got, _, _ = run_oracle(c, sp, Wt, bias, alpha, theta, B * H * W, shape, t_min=1)
+    exp = pyref.integrate_dense(sp, Wt, bias, alpha, theta, 1, T=T, tfs=tfs, alpha_by_time=True, **shape)
+    np.testing.assert_array_equal(got, exp)
+    # the network runner derives the same pads from the layer's kernel
+    td = oracle.integrate_timedriven(c, sp, Wt, bias, alpha, theta, 1, **shape)
+    np.testing.assert_array_equal(td, exp)
+    with pytest.raises(ValueError):
+        oracle.pads(1, K_h, K_w)
+
+
 @pytest.mark.parametrize("T,tfs,delta,abt,is_fc,same", CASES)
 def test_integrate_matches_timedriven(T, tfs, delta, abt, is_fc, same):
     rng = np.random.default_rng(1000 + T)

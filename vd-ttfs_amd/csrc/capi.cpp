@@ -330,8 +330,39 @@ static IntegShape make_shape(const vdttfs_ctx* ctx, int B, int H_in, int W_in, i
     s.C_out = C_out;
     s.K_h = is_fc ? 1 : K_h;
     s.K_w = is_fc ? 1 : K_w;
-    s.pad = (is_fc || !ctx->c.conv_same_pad) ? 0 : K_h / 2;
+    // T2V:109-110: same padding is K_h/2 rows and K_w/2 columns
+    const bool same = !is_fc && ctx->c.conv_same_pad;
+    s.pad_h = same ? K_h / 2 : 0;
+    s.pad_w = same ? K_w / 2 : 0;
     return s;
+}
+
+// One layer on the engine's kernels (list built in LDS, from the dense map
+// or from the bin-layout bucketize, then the wave-per-pixel stream) with the
+// built-in launch plan and context-owned scratch.  Scratch is sized for what
+// the layer's plan uses: the fused and register paths need no merged list.
+static int engine_layer(vdttfs_ctx* ctx, float* d_out, const float* d_in, const float* d_kernel,
+                        const float* d_bias, const float* d_lut_decay, const float* d_lut_th, int t_min,
+                        const IntegShape& s, unsigned long long* counters) {
+    LaunchPlan p;
+    VD_TRY(resolve_plan(ctx, s, LaunchPlan{}, &p));
+    const int64_t cols = s.is_fc ? s.B : (int64_t)s.B * s.H_in * s.W_in;
+    const int64_t n_pix = s.is_fc ? s.B : (int64_t)s.B * s.H_out * s.W_out;
+    const int64_t cap = merged_list_cap(s);
+    const bool dense = integrate_dense_ok(ctx, s) && p.path != VDTTFS_PATH_BINS;
+    const bool lds_list = p.path == VDTTFS_PATH_FUSED || (p.path == VDTTFS_PATH_REG && !counters);
+    if (!lds_list)
+        VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
+    if (dense)  // conv: merged lists straight from the dense map
+        return launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, (int2*)ctx->mrg_list, cap,
+                                      (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
+                                      counters, nullptr, &p);
+    VD_TRY(ensure_bin_scratch(ctx, (size_t)cols * s.C_in, (size_t)cols));
+    VD_TRY(launch_bucketize_bins(ctx, d_in, cols, s.C_in, d_lut_decay, (vd_event*)ctx->bin_ev,
+                                 (int32_t*)ctx->bin_off, nullptr));
+    return launch_integrate_bins(ctx, d_out, (const vd_event*)ctx->bin_ev, (const int32_t*)ctx->bin_off,
+                                 (int2*)ctx->mrg_list, cap, (int32_t*)ctx->mrg_bstart, d_kernel, d_bias,
+                                 d_lut_th, t_min, s, counters, nullptr, &p);
 }
 
 int vdttfs_integrate(vdttfs_ctx* ctx, float* d_out, const int32_t* d_bkt_cin,
@@ -360,26 +391,10 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
     VD_TRY(check_integ_shape(ctx, s));
     if (!d_out || !d_in || !d_kernel || !d_bias || !d_lut_decay || !d_lut_th)
         return set_error(VDTTFS_E_INVALID, "layer_forward: null buffer");
-    const int64_t cols = is_fc ? B : (int64_t)B * H_in * W_in;
-    const int64_t n_pix = is_fc ? B : (int64_t)B * H_out * W_out;
-    const int64_t cap = merged_list_cap(s);
-    VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     const bool count = eproc || ebin;
     if (count) VD_TRY(zero_counters(ctx));
-    if (integrate_dense_ok(ctx, s)) {
-        // conv: merged lists straight from the dense map
-        VD_TRY(launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, (int2*)ctx->mrg_list, cap,
-                                      (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
-                                      count ? ctx->d_counters : nullptr));
-    } else {
-        VD_TRY(ensure_bin_scratch(ctx, (size_t)cols * C_in, (size_t)cols));
-        VD_TRY(launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, (vd_event*)ctx->bin_ev,
-                                     (int32_t*)ctx->bin_off, nullptr));
-        VD_TRY(launch_integrate_bins(ctx, d_out, (const vd_event*)ctx->bin_ev,
-                                     (const int32_t*)ctx->bin_off, (int2*)ctx->mrg_list, cap,
-                                     (int32_t*)ctx->mrg_bstart, d_kernel, d_bias, d_lut_th, t_min, s,
-                                     count ? ctx->d_counters : nullptr));
-    }
+    VD_TRY(engine_layer(ctx, d_out, d_in, d_kernel, d_bias, d_lut_decay, d_lut_th, t_min, s,
+                        count ? ctx->d_counters : nullptr));
     if (count) {
         unsigned long long h[4];
         VD_TRY(read_counters(ctx, h));
@@ -415,7 +430,10 @@ int vdttfs_readout_argmax(vdttfs_ctx* ctx, const float* d_out, int B, int C, int
     return launch_readout(ctx, d_out, B, C, d_pred, 1);
 }
 
-// T1V:222-234 / T2V:250-274
+// T1V:222-234 / T2V:250-274.  The reference's wrapper runs k_bucketize into
+// file-static scratch, then k_conv_bucketed, then synchronises; its caller
+// never reads the buckets.  This one runs the engine's kernels on the same
+// dense map (same first-spike times, bit for bit), then synchronises.
 int vdttfs_launch_layer_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, int H_in, int W_in,
                              int C_in, int H_out, int W_out, int C_out, int K_h, int K_w, float td,
                              const float* d_kernel, const float* d_bias, const float* d_lut_decay,
@@ -423,15 +441,11 @@ int vdttfs_launch_layer_sync(vdttfs_ctx* ctx, const float* d_in, float* d_out, i
     VD_TRY(check_ctx(ctx));
     int t_min = (int)ceilf(td);
     if (t_min < 0) t_min = 0;
-    const int64_t cols = is_fc ? B : (int64_t)B * H_in * W_in;
     IntegShape s = make_shape(ctx, B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, is_fc);
     VD_TRY(check_integ_shape(ctx, s));
-    VD_TRY(ensure_ref_scratch(ctx, (size_t)cols * C_in, (size_t)cols));
-    VD_TRY(launch_bucketize_ref(ctx, d_in, cols, C_in, (int32_t*)ctx->ref_cin, (float*)ctx->ref_tin,
-                                (int32_t*)ctx->ref_off));
-    VD_TRY(launch_integrate_ref(ctx, d_out, (const int32_t*)ctx->ref_cin, (const float*)ctx->ref_tin,
-                                (const int32_t*)ctx->ref_off, d_kernel, d_bias, d_lut_decay, d_lut_th,
-                                t_min, B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, is_fc));
+    if (!d_out || !d_in || !d_kernel || !d_bias || !d_lut_decay || !d_lut_th)
+        return set_error(VDTTFS_E_INVALID, "launch_layer: null buffer");
+    VD_TRY(engine_layer(ctx, d_out, d_in, d_kernel, d_bias, d_lut_decay, d_lut_th, t_min, s, nullptr));
     VD_HIP(hipStreamSynchronize(ctx->stream));
     return VDTTFS_OK;
 }

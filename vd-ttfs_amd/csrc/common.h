@@ -99,7 +99,7 @@ struct CulifNeuron {
 };
 
 struct IntegShape {
-    int B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+    int B, H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w, is_fc;
 };
 // Entries per pixel of the merged event list (receptive events + padding).
 int merged_list_cap(const IntegShape& s);
@@ -194,7 +194,7 @@ struct StepLayer {
     const float* W;
     const float* bias;
     int64_t n;  // neurons: B * H_out * W_out * C_out
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w, is_fc;
 };
 int launch_step_input(vdttfs_ctx* ctx, const float* tin, uint8_t* s, int64_t n, int t);
 int launch_step_neuron(vdttfs_ctx* ctx, const StepLayer& L, const uint8_t* s_in, uint8_t* s_out, float* vmem,

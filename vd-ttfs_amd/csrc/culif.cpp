@@ -194,7 +194,8 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
                 VD_TRY(upload(&l.W, w));
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;
                 const int64_t n_pix = cols;
-                IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3, 1, 0};
+                IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3,
+                              /*pad_h=*/1, /*pad_w=*/1, /*is_fc=*/0};
                 l.list_cap = merged_list_cap(sh);
                 if (cols * d.C_in > max_ev) max_ev = cols * d.C_in;
                 if (cols > max_cols) max_cols = cols;
@@ -301,7 +302,8 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
                 break;
             case VDTTFS_CULIF_CONV: {
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;
-                IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3, 1, 0};
+                IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3,
+                              /*pad_h=*/1, /*pad_w=*/1, /*is_fc=*/0};
                 // narrow inputs build the merged lists from the dense map (the
                 // bin-layout bucketize then only counts retained events)
                 const bool dense = integrate_dense_ok(ctx, sh);

@@ -53,7 +53,7 @@ struct MergeArgs {
     int64_t n_pix;
     int64_t cap;
     int T;
-    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad, is_fc;
+    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad_h, pad_w, is_fc;
     int rowbytes;          // C_out * 4
 };
 
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
         int col = 0;
         if (lane < a.K_h * a.K_w) {
             const int kh = lane / a.K_w, kw = lane - kh * a.K_w;
-            const int hi = h_out - a.pad + kh, wi = w_out - a.pad + kw;
+            const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
             v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
             col = (img * a.H_in + hi) * a.W_in + wi;
         }
@@ -202,7 +202,7 @@ struct DenseMergeArgs {
     float tfs;
     int alpha_by_time;
     int nbits;             // bits of a bin index (ceil(log2 T))
-    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad;
+    int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad_h, pad_w;
     int rowbytes;          // C_out * 4
     float inv_cin;         // 1 / C_in
 };
@@ -230,7 +230,7 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
         int col = 0;
         if (lane < a.K_h * a.K_w) {
             const int kh = lane / a.K_w, kw = lane - kh * a.K_w;
-            const int hi = h_out - a.pad + kh, wi = w_out - a.pad + kw;
+            const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
             v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
             col = (img * a.H_in + hi) * a.W_in + wi;
         }
@@ -813,7 +813,7 @@ struct SmallArgs {
     int64_t n_pix;
     int T, t_min, alpha_by_time;
     float tfs;
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad;
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w;
     int nel;              // K_h * K_w * C_in
     int P;                // pixels per wave: 64 / C_out
 };
@@ -860,7 +860,7 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
         for (int e = 0; e < kSmallMaxEl; ++e) {
             av[e] = kInfTime;  // spike time until the second round
             if (e < a.nel) {   // uniform
-                const int hi = h_out - a.pad + kh, wi = w_out - a.pad + kw;
+                const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
                 const bool inb = pix_ok && hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
                 const int64_t idx = inb ? ((img * a.H_in + hi) * a.W_in + wi) * a.C_in + ci : 0;
                 const float t = a.in[idx];
@@ -1054,7 +1054,7 @@ struct GenArgs {
     int64_t total;
     int T, D, t_min, alpha_by_time;
     float tfs;
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w, is_fc;
 };
 
 template <bool BINS, int DMAX, bool COUNT>
@@ -1090,10 +1090,10 @@ __global__ __launch_bounds__(256) void k_integrate_generic(GenArgs a) {
             }
             const int base_t = tau * D;
             for (int kh = 0; kh < kh_n; ++kh) {
-                const int h_in = a.is_fc ? 0 : h_out - a.pad + kh;
+                const int h_in = a.is_fc ? 0 : h_out - a.pad_h + kh;
                 if (!a.is_fc && (h_in < 0 || h_in >= a.H_in)) continue;
                 for (int kw = 0; kw < kw_n; ++kw) {
-                    const int w_in = a.is_fc ? 0 : w_out - a.pad + kw;
+                    const int w_in = a.is_fc ? 0 : w_out - a.pad_w + kw;
                     if (!a.is_fc && (w_in < 0 || w_in >= a.W_in)) continue;
                     const int64_t col =
                         a.is_fc ? img : ((int64_t)img * a.H_in + h_in) * a.W_in + w_in;
@@ -1107,9 +1107,17 @@ __global__ __launch_bounds__(256) void k_integrate_generic(GenArgs a) {
                         s = a.off[col * OS + tau];
                         e = a.off[col * OS + tau + 1];
                     }
+                    // caller-made buckets (the drop-in) are not trusted to
+                    // match this context's T, Delta and TFS: offsets clamp to
+                    // the column, and events outside this chunk's bins, the
+                    // window or the input width are skipped below.  Buckets
+                    // made with the context's own constants never trigger
+                    // either guard, so their results are unchanged.
+                    s = s < 0 ? 0 : (s > a.C_in ? a.C_in : s);
+                    e = e < s ? s : (e > a.C_in ? a.C_in : e);
                     for (int p = s; p < e; ++p) {
                         int cin, tb;
-                        float al;
+                        float al, t_in = 0.0f;
                         if (BINS) {
                             const vd_event ev = a.ev[col * a.C_in + p];
                             cin = (int)(ev.key & 0xFFFFFFu);
@@ -1117,12 +1125,13 @@ __global__ __launch_bounds__(256) void k_integrate_generic(GenArgs a) {
                             al = ev.alpha;
                         } else {
                             cin = a.ref_cin[col * a.C_in + p];
-                            const float t_in = a.ref_tin[col * a.C_in + p];
+                            t_in = a.ref_tin[col * a.C_in + p];
                             tb = (int)floorf(t_in - a.tfs);
                             if (tb < 0) tb = 0;
-                            al = a.alpha[alpha_index(t_in, tb, a.alpha_by_time, T)];
                         }
                         const int di = tb - base_t;
+                        if ((unsigned)di >= (unsigned)D || tb >= T || (unsigned)cin >= (unsigned)a.C_in) continue;
+                        if (!BINS) al = a.alpha[alpha_index(t_in, tb, a.alpha_by_time, T)];
                         delta[di] = __builtin_fmaf(a.W[(wbase + cin) * a.C_out + c_out], al, delta[di]);
                         if (COUNT) nbin[di]++;
                     }
@@ -1193,7 +1202,7 @@ int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s) {
         if (s.H_in <= 0 || s.W_in <= 0 || s.H_out <= 0 || s.W_out <= 0 || s.K_h <= 0 || s.K_w <= 0)
             return set_error(VDTTFS_E_INVALID, "integrate: conv dims must be positive");
         // every receptive column of every output pixel must be addressable
-        if (s.pad == 0 && (s.H_out + s.K_h - 1 > s.H_in || s.W_out + s.K_w - 1 > s.W_in))
+        if (s.pad_h == 0 && s.pad_w == 0 && (s.H_out + s.K_h - 1 > s.H_in || s.W_out + s.K_w - 1 > s.W_in))
             return set_error(VDTTFS_E_INVALID,
                              "integrate: valid conv needs H_in >= H_out+K_h-1 (got %d < %d+%d-1)",
                              s.H_in, s.H_out, s.K_h);
@@ -1234,7 +1243,9 @@ int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const 
     g.C_out = C_out;
     g.K_h = is_fc ? 1 : K_h;
     g.K_w = is_fc ? 1 : K_w;
-    g.pad = (is_fc || !ctx->c.conv_same_pad) ? 0 : K_h / 2;
+    const bool same = !is_fc && ctx->c.conv_same_pad;  // T2V:109-110
+    g.pad_h = same ? K_h / 2 : 0;
+    g.pad_w = same ? K_w / 2 : 0;
     g.is_fc = is_fc;
     g.total = (int64_t)B * g.H_out * g.W_out * C_out;
     return launch_generic_d<false, false>(ctx, g);
@@ -1266,7 +1277,8 @@ int launch_integrate_generic_bins(vdttfs_ctx* ctx, float* out, const vd_event* e
     g.C_out = sh.C_out;
     g.K_h = sh.K_h;
     g.K_w = sh.K_w;
-    g.pad = sh.pad;
+    g.pad_h = sh.pad_h;
+    g.pad_w = sh.pad_w;
     g.is_fc = sh.is_fc;
     g.total = (int64_t)sh.B * (sh.is_fc ? 1 : (int64_t)sh.H_out * sh.W_out) * sh.C_out;
     return counters ? launch_generic_d<true, true>(ctx, g) : launch_generic_d<true, false>(ctx, g);
@@ -1451,7 +1463,8 @@ int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float*
     a.C_out = sh.C_out;
     a.K_h = sh.K_h;
     a.K_w = sh.K_w;
-    a.pad = sh.pad;
+    a.pad_h = sh.pad_h;
+    a.pad_w = sh.pad_w;
     a.nel = sh.K_h * sh.K_w * sh.C_in;
     a.P = 64 / sh.C_out;
     if (a.nel > kSmallMaxEl || sh.C_out > 64 || a.T > kSmallMaxBins)
@@ -1653,7 +1666,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     m.W_out = sh.W_out;
     m.K_h = sh.K_h;
     m.K_w = sh.K_w;
-    m.pad = sh.pad;
+    m.pad_h = sh.pad_h;
+    m.pad_w = sh.pad_w;
     m.is_fc = sh.is_fc;
     m.rowbytes = sh.C_out * 4;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
@@ -1692,7 +1706,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int nk_max = sh.K_h * sh.K_w;
     const int64_t n_pix = n_pixels(sh);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
-    if (!list || !bstart || list_cap < cap)
+    // the fused kernel keeps its lists in LDS; the others need the scratch
+    if (p.path != VDTTFS_PATH_FUSED && (!list || !bstart || list_cap < cap))
         return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
     DenseMergeArgs m{};
     m.list = list;
@@ -1714,7 +1729,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.W_out = sh.W_out;
     m.K_h = sh.K_h;
     m.K_w = sh.K_w;
-    m.pad = sh.pad;
+    m.pad_h = sh.pad_h;
+    m.pad_w = sh.pad_w;
     m.rowbytes = sh.C_out * 4;
     m.inv_cin = 1.0f / (float)sh.C_in;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;

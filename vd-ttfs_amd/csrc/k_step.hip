@@ -35,7 +35,7 @@ struct StepArgs {
     const float* bias;
     float* out;  // output layer: first-spike steps (T1S) or max(V + b) (T2S)
     int64_t n;
-    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad, is_fc;
+    int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w, is_fc;
     int mode;          // 1: T1S (psp = sum w; V = fma(psp, kv, V)); 2: T2S (psp = fma chain of w*kv; V += psp)
     int int_ok, fire_ok;
     int out_layer;     // 1: T1S output (records its first spike); 2: T2S output (keeps max V + b)
@@ -68,10 +68,10 @@ __global__ __launch_bounds__(256) void k_step_neuron(StepArgs a) {
                 const int ho = (int)((q / a.W_out) % a.H_out);
                 const int64_t img = q / ((int64_t)a.W_out * a.H_out);
                 for (int kh = 0; kh < a.K_h; ++kh) {
-                    const int hi = ho - a.pad + kh;
+                    const int hi = ho - a.pad_h + kh;
                     if (hi < 0 || hi >= a.H_in) continue;
                     for (int kw = 0; kw < a.K_w; ++kw) {
-                        const int wi = wo - a.pad + kw;
+                        const int wi = wo - a.pad_w + kw;
                         if (wi < 0 || wi >= a.W_in) continue;
                         const uint8_t* src = a.s_in + ((img * a.H_in + hi) * a.W_in + wi) * a.C_in;
                         const int64_t wb = (int64_t)(kh * a.K_w + kw) * a.C_in;
@@ -166,7 +166,8 @@ int launch_step_neuron(vdttfs_ctx* ctx, const StepLayer& L, const uint8_t* s_in,
     a.C_out = L.C_out;
     a.K_h = L.K_h;
     a.K_w = L.K_w;
-    a.pad = L.pad;
+    a.pad_h = L.pad_h;
+    a.pad_w = L.pad_w;
     a.is_fc = L.is_fc;
     a.mode = mode;
     a.int_ok = int_ok;

@@ -140,7 +140,9 @@ IntegShape integ_shape(const vdttfs_net* net, const NetLayer& l) {
     s.C_out = d.C_out;
     s.K_h = fc ? 1 : d.K_h;
     s.K_w = fc ? 1 : d.K_w;
-    s.pad = (fc || !net->ctx->c.conv_same_pad) ? 0 : d.K_h / 2;
+    const bool same = !fc && net->ctx->c.conv_same_pad;  // T2V:109-110
+    s.pad_h = same ? d.K_h / 2 : 0;
+    s.pad_w = same ? d.K_w / 2 : 0;
     return s;
 }
 
@@ -335,7 +337,9 @@ int create_impl(vdttfs_net* net, const vdttfs_layer_desc* layers, int n) {
         s.C_out = d.C_out;
         s.K_h = fc ? 1 : d.K_h;
         s.K_w = fc ? 1 : d.K_w;
-        s.pad = (fc || !c.conv_same_pad) ? 0 : d.K_h / 2;
+        const bool same = !fc && c.conv_same_pad;  // T2V:109-110
+        s.pad_h = same ? d.K_h / 2 : 0;
+        s.pad_w = same ? d.K_w / 2 : 0;
         VD_TRY(check_integ_shape(ctx, s));
         if (l.cols * l.cin_col > max_elems) max_elems = l.cols * l.cin_col;
         if (l.cols > max_cols) max_cols = l.cols;

@@ -97,7 +97,9 @@ int create_impl(vdttfs_stepnet* net, const vdttfs_layer_desc* layers, int n) {
         s.K_h = d.K_h;
         s.K_w = d.K_w;
         s.is_fc = d.kind != VDTTFS_LAYER_CONV;
-        s.pad = (s.is_fc || !c.conv_same_pad) ? 0 : d.K_h / 2;
+        const bool same = !s.is_fc && c.conv_same_pad;  // T2V:109-110
+        s.pad_h = same ? d.K_h / 2 : 0;
+        s.pad_w = same ? d.K_w / 2 : 0;
         VD_TRY(dmalloc((void**)&l.spk, (size_t)s.n));
         VD_TRY(dmalloc((void**)&l.fired, (size_t)s.n));
         if (d.kind == VDTTFS_LAYER_POOL) continue;

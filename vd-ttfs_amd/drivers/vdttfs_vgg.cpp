@@ -10,7 +10,125 @@
 //   vdttfs_vgg [--weights exported_models/snn_weights_vgg.bin]
 //              [--data dataset_downloaded/cifar10_float/] [--n 10000] [--batch 1000]
 //              [--T 80] [--tfs 40] [--delta 8] [--encode log|linear] [--tc-in 34.750164]
+//              [--dropin] [--reps 1]
+//
+// Default: the whole layer loop is one vdttfs_net_forward per batch (LUTs
+// resident, no host synchronisation inside the forward).  --dropin instead
+// runs T2V's batch loop call for call on the drop-in entry points (the
+// switch a maintainer makes in the reference program): per batch one H2D
+// of the images, encode + synchronise, and per weighted layer
+// vdttfs_update_luts (host expf, blocking upload) followed by
+// vdttfs_launch_layer_sync / vdttfs_launch_fc_vmem_sync, pools through
+// vdttfs_launch_pool_sync, then a D2H of the logits and the host argmax
+// (T2V:337-402).  It also prints each layer's host time (LAYER_MS lines).
+// --reps R repeats the whole inference R times and prints each run's time.
 #include "driver_util.h"
+
+namespace {
+
+struct DropinLayerTime {
+    double lut_s = 0, launch_s = 0;
+};
+
+// T2V:337-402 on the C ABI.  L: the topology built from the blob (pools
+// inserted), dev: the blob's layers on the device (vdttfs_load_weights).
+int run_dropin(vdttfs_ctx* ctx, const vdttfs_consts& c, const std::vector<vdttfs_layer_desc>& L,
+               const vdttfs_dev_layer* dev, int n_dev, bool linear, float tc_in, float td_in,
+               const std::vector<float>& imgs, const std::vector<float>& labels, int N, int B, int n_cls,
+               int rep, std::vector<DropinLayerTime>& lt) {
+    const int n_batches = (N + B - 1) / B;
+    DevBuf d_img(ctx, (size_t)B * 3072 * 4), d_s0(ctx, (size_t)B * 3072 * 4);
+    DevBuf d_decay(ctx, (size_t)(c.T + 1) * 4), d_th(ctx, (size_t)c.T * 4);
+    std::vector<DevBuf*> outs;
+    for (const vdttfs_layer_desc& d : L)
+        outs.push_back(new DevBuf(ctx, (size_t)B * d.H_out * d.W_out * d.C_out * 4));
+    std::vector<float> batch((size_t)B * 3072, 0.0f), h_out((size_t)B * n_cls);
+    int total_correct = 0;
+    using clk = std::chrono::steady_clock;
+    std::cout << ">>> Starting Full " << N << " Inference (drop-in, call for call; " << n_batches
+              << " batches of " << B << ")..." << std::endl;
+    const auto t0 = clk::now();
+    VD_CHECK(vdttfs_timer_begin(ctx));
+    for (int bi = 0; bi < n_batches; ++bi) {
+        const int s = bi * B, nb = std::min(B, N - s);
+        std::copy(imgs.begin() + (size_t)s * 3072, imgs.begin() + (size_t)(s + nb) * 3072, batch.begin());
+        VD_CHECK(vdttfs_h2d(ctx, d_img.p, batch.data(), batch.size() * 4));
+        if (linear)
+            VD_CHECK(vdttfs_encode_linear(ctx, d_img.as<float>(), d_s0.as<float>(), (int64_t)B * 3072));
+        else
+            VD_CHECK(vdttfs_encode_image(ctx, d_img.as<float>(), d_s0.as<float>(), (int64_t)B * 3072, tc_in,
+                                         td_in));
+        VD_CHECK(vdttfs_synchronize(ctx));
+        const float* cur = d_s0.as<float>();
+        float tc_i = tc_in, td_i = td_in;
+        int wi = 0;
+        for (size_t li = 0; li < L.size(); ++li) {
+            const vdttfs_layer_desc& d = L[li];
+            float* out = outs[li]->as<float>();
+            if (d.kind == VDTTFS_LAYER_POOL) {
+                const auto a = clk::now();
+                VD_CHECK(vdttfs_launch_pool_sync(ctx, cur, out, d.H_in, d.W_in, d.C_in, B));
+                lt[li].launch_s += seconds_since(a);
+            } else {
+                if (wi >= n_dev) {
+                    std::cerr << "weights file has fewer layers than the topology" << std::endl;
+                    return 1;
+                }
+                const vdttfs_dev_layer& w = dev[wi++];
+                auto a = clk::now();
+                VD_CHECK(vdttfs_update_luts(ctx, d_decay.as<float>(), d_th.as<float>(), tc_i, td_i, w.tc_fire,
+                                            w.td));
+                lt[li].lut_s += seconds_since(a);
+                a = clk::now();
+                if (d.kind == VDTTFS_LAYER_VMEM)
+                    VD_CHECK(vdttfs_launch_fc_vmem_sync(ctx, cur, out, d.H_in * d.W_in * d.C_in, d.C_out,
+                                                        w.d_kernel, w.d_bias, d_decay.as<float>(), B));
+                else if (d.kind == VDTTFS_LAYER_FC)
+                    VD_CHECK(vdttfs_launch_layer_sync(ctx, cur, out, 1, 1, d.H_in * d.W_in * d.C_in, 1, 1, d.C_out,
+                                                      1, 1, w.td, w.d_kernel, w.d_bias, d_decay.as<float>(),
+                                                      d_th.as<float>(), B, /*is_fc=*/1));
+                else
+                    VD_CHECK(vdttfs_launch_layer_sync(ctx, cur, out, d.H_in, d.W_in, d.C_in, d.H_out, d.W_out,
+                                                      d.C_out, d.K_h, d.K_w, w.td, w.d_kernel, w.d_bias,
+                                                      d_decay.as<float>(), d_th.as<float>(), B, /*is_fc=*/0));
+                lt[li].launch_s += seconds_since(a);
+                tc_i = w.tc_fire;
+                td_i = w.td;
+            }
+            cur = out;
+        }
+        VD_CHECK(vdttfs_d2h(ctx, h_out.data(), cur, h_out.size() * 4));
+        int bc = 0;
+        for (int k = 0; k < nb; ++k) {  // T2V:389-396: strict > from -1e9
+            float mv = -1e9f;
+            int pc = -1;
+            for (int i = 0; i < n_cls; ++i)
+                if (h_out[(size_t)k * n_cls + i] > mv) {
+                    mv = h_out[(size_t)k * n_cls + i];
+                    pc = i;
+                }
+            if (pc == onehot_class(&labels[(size_t)(s + k) * n_cls], n_cls)) ++bc;
+        }
+        total_correct += bc;
+        std::cout << "  -> Batch [" << bi + 1 << "/" << n_batches << "] Correct: " << bc << " / " << nb
+                  << std::endl;
+    }
+    double ms = 0;
+    VD_CHECK(vdttfs_timer_end(ctx, &ms));
+    const double wall = seconds_since(t0);
+    for (DevBuf* b : outs) delete b;
+    std::cout << "\n=======================================" << std::endl;
+    std::cout << "TIME-SORTED INPUT-GEN EARLY-EXIT COMPLETED (drop-in, run " << rep + 1 << ")" << std::endl;
+    std::cout << "Total Images Processed: " << N << std::endl;
+    std::cout << "Final Accuracy:         " << (float)total_correct / N * 100.0f << "%" << std::endl;
+    std::cout << "Total Inference Time:   " << ms / 1000.0 << " seconds" << std::endl;
+    std::cout << "Throughput:             " << N / (ms / 1000.0) << " images/sec" << std::endl;
+    std::cout << "Host wall time:         " << wall << " seconds" << std::endl;
+    std::cout << "=======================================" << std::endl;
+    return 0;
+}
+
+}  // namespace
 
 int main(int argc, char** argv) {
     const Args a(argc, argv);
@@ -85,6 +203,26 @@ int main(int argc, char** argv) {
 
     vdttfs_ctx* ctx = nullptr;
     VD_CHECK(vdttfs_create(&c, 0, &ctx));
+    const int reps = std::max(1, a.i("reps", 1));
+    if (a.s("dropin", "0") == "1") {
+        vdttfs_blob_free(blob);
+        vdttfs_dev_layer* dev = nullptr;
+        int n_dev = 0;
+        VD_CHECK(vdttfs_load_weights(ctx, weights.c_str(), &dev, &n_dev));
+        std::vector<DropinLayerTime> lt(L.size());
+        for (int r = 0; r < reps; ++r) {
+            if (r == reps - 1) lt.assign(L.size(), DropinLayerTime{});  // per-layer times of the last run
+            const int rc = run_dropin(ctx, c, L, dev, n_dev, linear, tc_in, td_in, imgs, labels, N, B, n_cls, r, lt);
+            if (rc) return rc;
+        }
+        static const char* kinds[] = {"conv", "fc", "pool", "vmem"};
+        for (size_t li = 0; li < L.size(); ++li)
+            std::cout << "LAYER_MS i=" << li << " kind=" << kinds[L[li].kind] << " lut_ms=" << lt[li].lut_s * 1e3
+                      << " launch_ms=" << lt[li].launch_s * 1e3 << std::endl;
+        VD_CHECK(vdttfs_free_weights(ctx, dev, n_dev));
+        vdttfs_destroy(ctx);
+        return 0;
+    }
     vdttfs_net* net = nullptr;
     VD_CHECK(vdttfs_net_create(ctx, L.data(), (int)L.size(), B, 3072,
                                linear ? VDTTFS_ENCODE_LINEAR : VDTTFS_ENCODE_LOG, tc_in, td_in,

@@ -203,6 +203,7 @@ SIGNATURES = {
     "vdttfs_culif_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_timer_begin": [_vp],
     "vdttfs_timer_end": [_vp, C.POINTER(C.c_double)],
+    "vdttfs_probe_gather": [_vp, _i, _i64, _i, _i64, _i, C.POINTER(C.c_double)],
 }
 
 _RESTYPES = {"vdttfs_last_error": C.c_char_p, "vdttfs_version": C.c_char_p}

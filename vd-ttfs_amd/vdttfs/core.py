@@ -160,6 +160,13 @@ class Context:
     def synchronize(self):
         check(lib().vdttfs_synchronize(self.handle))
 
+    def probe_gather(self, vec: int, footprint_bytes: int, n_ev: int = 512, waves: int = 32768,
+                     reps: int = 5) -> float:
+        """Milliseconds per launch of the gather-roof probe (vdttfs_probe_gather)."""
+        ms = C.c_double(0.0)
+        check(lib().vdttfs_probe_gather(self.handle, vec, footprint_bytes, n_ev, waves, reps, C.byref(ms)))
+        return ms.value
+
     # ---- the reference surface ----
     def update_LUTs(self, d_lut_decay: DeviceArray, d_lut_th: DeviceArray, tc_integ, td_integ,
                     tc_fire, td_fire):
@@ -305,6 +312,13 @@ class Net:
 
     def forward(self, d_img: DeviceArray, d_pred: DeviceArray | None = None):
         check(lib().vdttfs_net_forward(self.handle, d_img.ptr, d_pred.ptr if d_pred else None))
+
+    def layer_output_ptr(self, i: int):
+        """(device pointer, elements) of layer i's output map."""
+        p = C.c_void_p()
+        n = C.c_int64()
+        check(lib().vdttfs_net_layer_output(self.handle, i, C.byref(p), C.byref(n)))
+        return p, n.value
 
     def layer_output(self, i: int) -> np.ndarray:
         p = C.c_void_p()
@@ -474,8 +488,9 @@ class CulifNet:
         check(lib().vdttfs_culif_net_forward(self.handle, d_data.ptr, d_pred.ptr if d_pred else None))
 
     def layer_output(self, i: int, layout: str = "nchw") -> np.ndarray:
-        """Layer i's output as [B][C][H][W] (layout "nchw") whatever the engine
-        keeps internally."""
+        """Layer i's output as [B][C][H][W] (layout "nchw") or [B][H][W][C]
+        ("nhwc"), whatever the engine keeps internally; any other layout
+        returns the engine's own buffer."""
         p = C.c_void_p()
         n = C.c_int64()
         nhwc = C.c_int32()
@@ -484,6 +499,10 @@ class CulifNet:
         h = np.empty(n.value, np.float32)
         check(lib().vdttfs_d2h(self.ctx.handle, _ptr(h), p, h.nbytes))
         Cc, H, W = self.layers[i].out_shape
+        if layout == "nhwc":
+            if nhwc.value:
+                return h
+            return np.ascontiguousarray(h.reshape(self.B, Cc, H, W).transpose(0, 2, 3, 1)).reshape(-1)
         if nhwc.value:
             h = h.reshape(self.B, H, W, Cc).transpose(0, 3, 1, 2)
         return np.ascontiguousarray(h.reshape(self.B, Cc, H, W)) if layout == "nchw" else h

@@ -6,16 +6,23 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
 
   python -m vdttfs.rocprof_summary stats   DIR NAME            # --kernel-trace --stats
   python -m vdttfs.rocprof_summary layers  DIR NAME            # one forward, per layer
-  python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME
+  python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME \
+         [--workload KEY] [--first PREFIX]
   python -m vdttfs.rocprof_summary counters DIR NAME           # occupancy, LDS conflicts
 
 ``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
 benchmark, and the same two counters over ``bench.py --copy-calibration``
 (an elementwise copy of a known number of bytes).  Each counter is scaled by
 known_bytes / counted_bytes of the copy, then summed over the integrator
-dispatches (bucketize + merge + stream, or the generic integrator) of one
-non-counting forward.  The last line is machine-readable and is what
-bench.py reports as ``roofline.traffic``.
+dispatches (bucketize + merge + stream, the fused or register kernels, or the
+generic integrator) of one non-counting forward, per integrating layer and in
+total.  A forward starts at a dispatch whose name begins with PREFIX
+(default ``k_encode``: the engine's encoder; the config-5 layer call starts
+at ``k_bucketize``, the CuLIF network at ``k_culif_event_masks``).  The last
+lines are machine-readable: ``WORKLOAD=KEY`` (the bench.py configuration the
+counters belong to), one ``LAYER_TRAFFIC`` line per integrating layer, and
+``TRAFFIC_PER_STEP_BYTES``, which bench.py reports as ``roofline.traffic``
+when its own configuration key equals KEY.
 """
 from __future__ import annotations
 
@@ -26,7 +33,9 @@ import re
 import sys
 
 # every kernel of a layer's integrate: bucketize (FC layers), merge, stream
-INTEGRATOR = ("k_bucketize", "k_merge", "k_stream", "k_integrate_generic")
+INTEGRATOR = ("k_bucketize", "k_merge", "k_stream", "k_integrate_generic", "k_conv_small")
+# the dispatch that ends a layer's integrate (lists, if any, come before it)
+LAYER_END = ("k_stream", "k_integrate_generic", "k_conv_small")
 COPY_BYTES_DEFAULT = 1 << 30  # bench.py --copy-calibration moves 2^28 floats each way
 
 
@@ -53,13 +62,15 @@ def stats(d: str, name: str) -> str:
     return "\n".join(out)
 
 
-def _forwards(rows, key_start="Start_Timestamp"):
-    """Split dispatches (sorted by start) into forwards; each starts with an encoder."""
+def _forwards(rows, key_start="Start_Timestamp", first="k_encode"):
+    """Split dispatches (sorted by start) into forwards; each starts with a
+    dispatch named `first...` (the engine's encoder by default)."""
     rows = sorted(rows, key=lambda r: int(r[key_start]))
     fw, cur = [], None
     for r in rows:
         n = short_name(r["Kernel_Name"])
-        if n.startswith("k_encode"):
+        if n.startswith(first) and (cur is None or first != "k_bucketize" or any(
+                short_name(q["Kernel_Name"]).startswith(LAYER_END) for q in cur)):
             cur = []
             fw.append(cur)
         if cur is not None:
@@ -114,8 +125,8 @@ def _copy_factor(d: str, name: str, counter: str, known: int) -> float:
     return known / (big["_v"] * 1024.0)
 
 
-def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str,
-            copy_bytes: int = COPY_BYTES_DEFAULT) -> str:
+def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str, workload: str = "",
+            first: str = "k_encode", copy_bytes: int = COPY_BYTES_DEFAULT) -> str:
     ff = _copy_factor(cfdir, name, "FETCH_SIZE", copy_bytes)
     wf = _copy_factor(cwdir, name, "WRITE_SIZE", copy_bytes)
     lines = [f"copy calibration ({copy_bytes} B read + {copy_bytes} B written per dispatch): "
@@ -123,25 +134,32 @@ def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str,
     res = {}
     for counter, d, scale in (("FETCH_SIZE", fdir, ff), ("WRITE_SIZE", wdir, wf)):
         disp = _per_dispatch(d, name, counter)
-        fw = [f for f in _forwards(disp, key_start="Dispatch_Id") if not _is_counting(f)]
+        fw = [f for f in _forwards(disp, key_start="Dispatch_Id", first=first) if not _is_counting(f)]
         f = fw[-1]
         per = [(short_name(r["Kernel_Name"]), r["_v"] * 1024.0 * scale) for r in f]
         res[counter] = per
     lines.append("| # | kernel | FETCH bytes | WRITE bytes |")
     lines.append("|---:|---|---:|---:|")
     tf = tw = 0.0
-    n_integ = 0
+    layer_f = layer_w = 0.0
+    layers = []
     for i, ((n, fb), (_, wb)) in enumerate(zip(res["FETCH_SIZE"], res["WRITE_SIZE"])):
         lines.append("| %d | %s | %.4g | %.4g |" % (i, n, fb, wb))
         if n.startswith(INTEGRATOR):
             tf += fb
             tw += wb
-            if n.startswith(("k_stream", "k_integrate_generic")):
-                n_integ += 1
+            layer_f += fb
+            layer_w += wb
+            if n.startswith(LAYER_END):
+                layers.append((layer_f, layer_w))
+                layer_f = layer_w = 0.0
     lines.append("")
     lines.append(f"integrator (bucketize + merge + stream) per forward: FETCH {tf:.6g} B, WRITE {tw:.6g} B, "
-                 f"{n_integ} integrating layers")
-    lines.append(f"TRAFFIC_PER_STEP_BYTES={tf + tw:.0f} LAUNCHES_PER_STEP={n_integ} "
+                 f"{len(layers)} integrating layers")
+    lines.append(f"WORKLOAD={workload}")
+    for i, (fb, wb) in enumerate(layers):
+        lines.append(f"LAYER_TRAFFIC n={i} fetch={fb:.0f} write={wb:.0f}")
+    lines.append(f"TRAFFIC_PER_STEP_BYTES={tf + tw:.0f} LAUNCHES_PER_STEP={len(layers)} "
                  f"FETCH_SCALE={ff:.5f} WRITE_SCALE={wf:.5f}")
     return "\n".join(lines)
 
@@ -193,7 +211,9 @@ def main(argv) -> int:
     elif cmd == "layers":
         print(layers(argv[2], argv[3]))
     elif cmd == "traffic":
-        print(traffic(*argv[2:7]))
+        rest = argv[7:]
+        opts = dict(zip(rest[::2], rest[1::2]))
+        print(traffic(*argv[2:7], workload=opts.get("--workload", ""), first=opts.get("--first", "k_encode")))
     elif cmd == "counters":
         print(counters(argv[2], argv[3]))
     else:
