@@ -134,6 +134,24 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
                          int H_out, int W_out, int C_out, int K_h, int K_w, int is_fc,
                          uint64_t* eproc, uint64_t* ebin);
 
+/* ---- the layer path without device allocation ------------------------- */
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and results as vdttfs_layer_forward
+ * (without the work counters), with the layer's merged lists and bucket
+ * scratch in a 64 MiB device buffer that the library holds per GPU until the
+ * process ends, instead of context scratch grown with hipMalloc.  The call
+ * allocates and frees nothing.  A layer whose scratch exceeds 64 MiB fails
+ * with VDTTFS_E_UNSUPPORTED (the LDS-list and register paths need none; a
+ * 3x3 conv needs about (9*C_in + 32)*8 + 4*(T+1) bytes per output pixel).
+ * Every call on one GPU shares that GPU's buffer: calls that overlap on one
+ * GPU (two streams, two host threads, or two contexts on the same device)
+ * race and must be serialised by the caller. */
+int vdttfs_layer_forward_noalloc(vdttfs_ctx* ctx, float* d_out, const float* d_in, const float* d_kernel,
+                                 const float* d_bias, const float* d_lut_decay, const float* d_lut_th, int t_min,
+                                 int B, int H_in, int W_in, int C_in, int H_out, int W_out, int C_out, int K_h,
+                                 int K_w, int is_fc);
+
 /* ---- k_pooling (T1V:164-181, T2V:192-209) ------------------------------ */
 int vdttfs_pool_min(vdttfs_ctx* ctx, const float* d_in, float* d_out, int B, int H_in,
                     int W_in, int C);

@@ -1,0 +1,98 @@
+"""vdttfs_layer_forward_noalloc through the C ABI: the layer path on the
+library's static per-GPU scratch must give exactly what vdttfs_layer_forward
+(context scratch grown with hipMalloc) gives, on two calls in a row -- the
+second with a smaller input, so stale scratch from the first call cannot
+leak into it -- on every list path (fused, dense, bins, narrow, register,
+FC), and reject a layer whose scratch exceeds the buffer."""
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+import vdttfs
+from vdttfs import _lib
+
+pytestmark = pytest.mark.gpu
+INF = np.float32(9999.0)
+
+# name, task2, is_fc, (B, B2), H, W, C_in, C_out, K
+CASES = [
+    ("fused 32->64 3x3", True, False, (5, 2), 12, 12, 32, 64, 3),
+    ("dense 16->128 3x3", True, False, (4, 3), 16, 16, 16, 128, 3),
+    ("bins 130->256 3x3", True, False, (3, 1), 8, 8, 130, 256, 3),
+    ("narrow 6->16 5x5 valid", False, False, (40, 7), 12, 12, 6, 16, 5),
+    ("register 1->6 5x5 valid", False, False, (50, 9), 28, 28, 1, 6, 5),
+    ("fc 600->300", True, True, (40, 13), 1, 1, 600, 300, 1),
+]
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def layer(rng, tc, is_fc, B, H, W, C_in, C_out, K):
+    if is_fc:
+        ho = wo = 1
+        n_cols = B
+    else:
+        ho, wo = (H, W) if tc.conv_same_pad else (H - K + 1, W - K + 1)
+        n_cols = B * H * W
+    n_in = n_cols * C_in
+    t = np.floor(rng.random(n_in) * (tc.T + tc.tfs + 2)).astype(np.float32)
+    sp = np.where(rng.random(n_in) < 0.4, t, INF).astype(np.float32)
+    return sp, dict(B=B, H_in=H, W_in=W, C_in=C_in, H_out=ho, W_out=wo, C_out=C_out,
+                    K_h=1 if is_fc else K, K_w=1 if is_fc else K)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_matches_layer_forward(gpu_ctx_factory, case):
+    name, task2, is_fc, Bs, H, W, C_in, C_out, K = case
+    say(f"noalloc {name}")
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    tc = vdttfs.TaskConsts(T=64, tfs=32.0 if task2 else 0.0, delta=8, vth=1.0, alpha_by_time=task2,
+                           conv_same_pad=task2)
+    ctx = gpu_ctx_factory(tc)
+    fan = (1 if is_fc else K * K) * C_in
+    Wt = (rng.standard_normal(fan * C_out) * np.sqrt(2.0 / fan)).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.05).astype(np.float32)
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_W, d_b, d_a, d_t = ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha), ctx.to_device(theta)
+    L = vdttfs.lib()
+    for B in Bs:  # the second call has a smaller input
+        sp, sh = layer(rng, tc, is_fc, B, H, W, C_in, C_out, K)
+        n_out = B * sh["H_out"] * sh["W_out"] * C_out
+        d_in = ctx.to_device(sp)
+        d_ref = ctx.empty(n_out)
+        d_new = ctx.empty(n_out).fill(0xFF)
+        ctx.layer_forward(d_ref, d_in, d_W, d_b, d_a, d_t, 1, is_fc=is_fc, **sh)
+        args = [sh[k] for k in ("B", "H_in", "W_in", "C_in", "H_out", "W_out", "C_out", "K_h", "K_w")]
+        rc = L.vdttfs_layer_forward_noalloc(ctx.handle, d_new.ptr, d_in.ptr, d_W.ptr, d_b.ptr, d_a.ptr, d_t.ptr,
+                                             1, *args, int(is_fc))
+        assert rc == 0, _lib.last_error()
+        ctx.synchronize()
+        ref, new = d_ref.download(), d_new.download()
+        assert 0.02 < float(np.mean(ref < INF)) < 0.98, "degenerate case"
+        np.testing.assert_array_equal(new, ref, err_msg=f"{name} B={B}")
+        for a in (d_in, d_ref, d_new):
+            a.free()
+
+
+def test_noalloc_rejects_oversized_layer(gpu_ctx_factory):
+    """A 64->128 conv at 64x32x32 needs ~320 MB of merged lists: refused with
+    VDTTFS_E_UNSUPPORTED before any launch, the output left untouched."""
+    say("noalloc oversized layer")
+    tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
+    ctx = gpu_ctx_factory(tc)
+    B, H, W, C_in, C_out = 64, 32, 32, 64, 128
+    d_in = ctx.empty(B * H * W * C_in).fill(0)
+    d_out = ctx.empty(B * H * W * C_out).fill(0x7F)
+    d_W, d_b = ctx.empty(9 * C_in * C_out).fill(0), ctx.empty(C_out).fill(0)
+    d_a, d_t = ctx.empty(65).fill(0), ctx.empty(64).fill(0)
+    rc = vdttfs.lib().vdttfs_layer_forward_noalloc(ctx.handle, d_out.ptr, d_in.ptr, d_W.ptr, d_b.ptr, d_a.ptr,
+                                                    d_t.ptr, 0, B, H, W, C_in, H, W, C_out, 3, 3, 0)
+    assert rc == _lib.E_UNSUPPORTED
+    assert "scratch" in _lib.last_error()
+    out = d_out.download()
+    assert np.all(out.view(np.uint32) == 0x7F7F7F7F)

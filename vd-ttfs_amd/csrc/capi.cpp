@@ -153,6 +153,7 @@ int vdttfs_create(const vdttfs_consts* consts, int device, vdttfs_ctx** out) {
     if (device < 0 || device >= n)
         return set_error(VDTTFS_E_INVALID, "device %d out of range (%d devices)", device, n);
     VD_HIP(hipSetDevice(device));
+    VD_TRY(noalloc_setup(device));
     vdttfs_ctx* ctx = new (std::nothrow) vdttfs_ctx();
     if (!ctx) return set_error(VDTTFS_E_NOMEM, "context allocation failed");
     ctx->c = *consts;

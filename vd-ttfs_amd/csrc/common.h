@@ -230,4 +230,10 @@ int launch_step3_layer(vdttfs_ctx* ctx, const Step3Layer& L, const float* in, in
 // shape validation shared by the entry points
 int check_integ_shape(const vdttfs_ctx* ctx, const IntegShape& s);
 
+// The static scratch of vdttfs_layer_forward_noalloc (noalloc.hip): looks up
+// `device`'s copy once (hipGetSymbolAddress, `device` current); vdttfs_create
+// calls it for every context's device.
+int noalloc_setup(int device);
+size_t noalloc_scratch_bytes();
+
 }  // namespace vdttfs

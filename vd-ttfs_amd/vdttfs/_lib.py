@@ -151,6 +151,8 @@ SIGNATURES = {
                          _i, _i, _i, _i],
     "vdttfs_layer_forward": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
                              _i, _i, _i, _u64p, _u64p],
+    "vdttfs_layer_forward_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
+                                     _i, _i, _i],
     "vdttfs_pool_min": [_vp, _vp, _vp, _i, _i, _i, _i],
     "vdttfs_fc_vmem": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i],
     "vdttfs_readout_argmin": [_vp, _vp, _i, _i, _vp],

@@ -201,6 +201,13 @@ class Context:
                                          C.byref(eb) if count else None))
         return (ep.value, eb.value) if count else None
 
+    def layer_forward_noalloc(self, d_out, d_in, d_kernel, d_bias, d_alpha, d_theta, t_min, B, H_in, W_in,
+                              C_in, H_out, W_out, C_out, K_h, K_w, is_fc):
+        """vdttfs_layer_forward_noalloc: the layer path on the library's static scratch."""
+        check(lib().vdttfs_layer_forward_noalloc(self.handle, d_out.ptr, d_in.ptr, d_kernel.ptr, d_bias.ptr,
+                                                 d_alpha.ptr, d_theta.ptr, t_min, B, H_in, W_in, C_in, H_out,
+                                                 W_out, C_out, K_h, K_w, int(is_fc)))
+
     def pool_min(self, d_in, d_out, B, H_in, W_in, Cc):
         check(lib().vdttfs_pool_min(self.handle, d_in.ptr, d_out.ptr, B, H_in, W_in, Cc))
 
