@@ -7,7 +7,7 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
   python -m vdttfs.rocprof_summary stats   DIR NAME            # --kernel-trace --stats
   python -m vdttfs.rocprof_summary layers  DIR NAME            # one forward, per layer
   python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME \
-         [--workload KEY] [--first PREFIX]
+         [--workload KEY] [--first PREFIX] [--copy-name NAME]
   python -m vdttfs.rocprof_summary counters DIR NAME           # occupancy, LDS conflicts
 
 ``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
@@ -22,7 +22,8 @@ at ``k_bucketize``, the CuLIF network at ``k_culif_event_masks``).  The last
 lines are machine-readable: ``WORKLOAD=KEY`` (the bench.py configuration the
 counters belong to), one ``LAYER_TRAFFIC`` line per integrating layer, and
 ``TRAFFIC_PER_STEP_BYTES``, which bench.py reports as ``roofline.traffic``
-when its own configuration key equals KEY.
+when its own configuration key equals KEY.  --copy-name is the -o name of the
+calibration runs when it differs from NAME.
 """
 from __future__ import annotations
 
@@ -82,8 +83,11 @@ _COUNTING = re.compile(r"^(k_stream(_dense|_narrow)?<true|k_integrate_generic<\w
 
 
 def _is_counting(forward) -> bool:
-    """A forward run with the E_proc counters on (net.count), not a timed one."""
-    return any(_COUNTING.match(short_name(r["Kernel_Name"])) for r in forward)
+    """A forward run with the E_proc counters on (net.count), not a timed one;
+    or a stretch between two encoder dispatches with no integrating layer (an
+    encode on its own, as bench.py runs to read the first layer's input)."""
+    return (any(_COUNTING.match(short_name(r["Kernel_Name"])) for r in forward) or
+            not any(short_name(r["Kernel_Name"]).startswith(LAYER_END) for r in forward))
 
 
 def layers(d: str, name: str) -> str:
@@ -126,9 +130,9 @@ def _copy_factor(d: str, name: str, counter: str, known: int) -> float:
 
 
 def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str, workload: str = "",
-            first: str = "k_encode", copy_bytes: int = COPY_BYTES_DEFAULT) -> str:
-    ff = _copy_factor(cfdir, name, "FETCH_SIZE", copy_bytes)
-    wf = _copy_factor(cwdir, name, "WRITE_SIZE", copy_bytes)
+            first: str = "k_encode", copy_name: str = "", copy_bytes: int = COPY_BYTES_DEFAULT) -> str:
+    ff = _copy_factor(cfdir, copy_name or name, "FETCH_SIZE", copy_bytes)
+    wf = _copy_factor(cwdir, copy_name or name, "WRITE_SIZE", copy_bytes)
     lines = [f"copy calibration ({copy_bytes} B read + {copy_bytes} B written per dispatch): "
              f"FETCH_SIZE scale {ff:.4f}, WRITE_SIZE scale {wf:.4f}", ""]
     res = {}
@@ -213,7 +217,8 @@ def main(argv) -> int:
     elif cmd == "traffic":
         rest = argv[7:]
         opts = dict(zip(rest[::2], rest[1::2]))
-        print(traffic(*argv[2:7], workload=opts.get("--workload", ""), first=opts.get("--first", "k_encode")))
+        print(traffic(*argv[2:7], workload=opts.get("--workload", ""), first=opts.get("--first", "k_encode"),
+                      copy_name=opts.get("--copy-name", "")))
     elif cmd == "counters":
         print(counters(argv[2], argv[3]))
     else:
