@@ -215,7 +215,7 @@ constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 // tail zeroed) and its T+1 bin starts into `bs`, and returns the list length.
 // `cur` (T ints) and `kinfo` (2 * KMAX ints) are the wave's LDS scratch.  The
 // outputs are HBM (k_merge_dense) or the wave's LDS (k_stream_dense).
-template <int KMAX, class ListPtr, class BinPtr>
+template <int KMAX, int NB, class ListPtr, class BinPtr>
 __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo,
                                            ListPtr out, BinPtr bs) {
     const int lane = lane_id();
@@ -244,22 +244,53 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
     }
     for (int t = lane; t < a.T; t += 64) cur[t] = 0;
     wave_sync();
-    const int nel = nk * a.C_in;  // <= KMAX * 64
-    // element f of the pixel: tap k = f / C_in (the quotient's fractional
-    // part is >= 0.5 / 64, so the float product rounds it correctly), cin c
-    auto element = [&](int f, float& x, int& row) {
-        const int k = (int)(((float)f + 0.5f) * a.inv_cin);
-        const int c = f - k * a.C_in;
-        x = a.in[(int64_t)kinfo[k] * a.C_in + c];
-        row = kinfo[KMAX + k] + c;
+    const int nel = nk * a.C_in;  // <= KMAX * 64 (C_in <= 64)
+    // Elements f = chunk * 64 + lane are loaded a batch of NB chunks at a
+    // time, every load of a batch issued together, so the wave waits for one
+    // round of loads per batch rather than one per chunk.  Each element
+    // packs into one register: weight row (bits 16..), decay-LUT index (bits
+    // 8..15) and arrival bin (bits 0..7, 0xFF: no event; T <= 255 keeps bins
+    // and indices below 0xFF).  A pixel of at most NB chunks (every 3x3
+    // layer at NB = 9) keeps its batch in registers for pass 2; wider ones
+    // reload it.  NB = 1 serves pixels of at most 64 elements with the
+    // fewest registers.
+    static_assert(NB >= 1 && NB <= 9, "NB chunks per batch");
+    const int n_chunks = (nel + 63) >> 6;
+    int pk[NB];
+    auto load_batch = [&](int c0) {
+        float xs[NB];
+        int rows[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            xs[c] = kInfTime;
+            rows[c] = 0;
+            if (c0 + c < n_chunks) {  // uniform
+                // tap k = f / C_in (the quotient's fractional part is >=
+                // 0.5 / 64, so the float product rounds it correctly), cin ci
+                const int f = (c0 + c) * 64 + lane;
+                const bool in = f < nel;
+                const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
+                const int ci = f - k * a.C_in;
+                rows[c] = kinfo[KMAX + k] + ci;
+                const float v = a.in[in ? (int64_t)kinfo[k] * a.C_in + ci : 0];
+                xs[c] = in ? v : kInfTime;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const int b = arrival_bin(xs[c], a.tfs, a.T);
+            const int ai = b >= 0 ? alpha_index(xs[c], b, a.alpha_by_time, a.T) : 0;
+            pk[c] = (rows[c] << 16) | (ai << 8) | (b & 0xFF);
+        }
     };
     // pass 1: events per bin
-    for (int f0 = 0; f0 < nel; f0 += 64) {
-        float x = kInfTime;
-        int row = 0;
-        if (f0 + lane < nel) element(f0 + lane, x, row);
-        const int b = arrival_bin(x, a.tfs, a.T);
-        if (b >= 0) atomicAdd(&cur[b], 1);
+    for (int c0 = 0; c0 < n_chunks; c0 += NB) {
+        load_batch(c0);
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const int b = pk[c] & 0xFF;
+            if (c0 + c < n_chunks && b != 0xFF) atomicAdd(&cur[b], 1);
+        }
     }
     wave_sync();
     // bin starts: lane l scans bins 4l .. 4l+3
@@ -286,27 +317,31 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
     wave_sync();
     // pass 2: stable placement, chunk by chunk in (kh, kw, cin) order
     const uint64_t lt = lanemask_lt();
-    for (int f0 = 0; f0 < nel; f0 += 64) {
-        float x = kInfTime;
-        int row = 0;
-        if (f0 + lane < nel) element(f0 + lane, x, row);
-        const int b = arrival_bin(x, a.tfs, a.T);
-        const bool valid = b >= 0;
-        uint64_t m = __ballot(valid);
-        if (m == 0) continue;  // uniform
-        for (int bit = 0; bit < a.nbits; ++bit) {
-            const bool set = valid && ((b >> bit) & 1);
-            const uint64_t bb = __ballot(set);
-            m &= set ? bb : ~bb;
+    for (int c0 = 0; c0 < n_chunks; c0 += NB) {
+        if (n_chunks > NB) load_batch(c0);  // uniform; else the batch is still in registers
+        float al[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) al[c] = a.alpha[(pk[c] >> 8) & 0xFF];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const int b = pk[c] & 0xFF;
+            const bool valid = c0 + c < n_chunks && b != 0xFF;
+            uint64_t m = __ballot(valid);
+            if (m != 0) {  // uniform (also false for chunks past the end)
+                for (int bit = 0; bit < a.nbits; ++bit) {
+                    const bool set = valid && ((b >> bit) & 1);
+                    const uint64_t bb = __ballot(set);
+                    m &= set ? bb : ~bb;
+                }
+                if (valid) {
+                    const int pos = cur[b] + __popcll(m & lt);
+                    out[pos] = make_int2((pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
+                }
+                wave_sync();
+                if (valid && (m & lt) == 0) cur[b] += __popcll(m);
+                wave_sync();
+            }
         }
-        if (valid) {
-            const int pos = cur[b] + __popcll(m & lt);
-            const float al = a.alpha[alpha_index(x, b, a.alpha_by_time, a.T)];
-            out[pos] = make_int2(row * a.rowbytes, __float_as_int(al));
-        }
-        wave_sync();
-        if (valid && (m & lt) == 0) cur[b] += __popcll(m);
-        wave_sync();
     }
     // zeroed tail: the stream kernel reads whole groups of 8 entries
     for (int i = lane; i < kListPad; i += 64) out[total + i] = make_int2(0, 0);
@@ -320,7 +355,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs
     const int wave = uniform(threadIdx.x >> 6);
     const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
     if (pix >= a.n_pix) return;  // uniform per wave
-    (void)dense_build<KMAX>(a, pix, cur_all[wave], kinfo_all[wave], a.list + pix * a.cap,
+    (void)dense_build<KMAX, 9>(a, pix, cur_all[wave], kinfo_all[wave], a.list + pix * a.cap,
                             a.bstart + pix * (int64_t)(a.T + 1));
 }
 
@@ -532,6 +567,28 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         const float v_th = (!CULIF && lane < nb) ? theta[t0 + lane] : 0.0f;
         const int blk_end = BS[t0 + nb];
         asm volatile("" ::"v"(v_bs), "v"(v_th));  // complete these loads before streaming
+        // Empty bin runs in O(1) (the LUT neuron without counters): a bin with
+        // no event adds +0 to carry, which changes no comparison, so across
+        // a run of empty bins carry is constant.  With theta non-increasing
+        // over the block (checked here; NaN fails the check), "carry >=
+        // theta[t]" holds on a suffix of the run and "theta[t] >= 1e-5" on a
+        // prefix of the block (bins below th_end), so a neuron fires in the
+        // run iff it clears theta at the run's last bin it may fire in, and
+        // then at the first such bin -- a per-lane lower bound over the run.
+        // Otherwise the bins are closed one by one as before.  Only the
+        // one-c_out-per-lane streams take it: their layers are the sparse
+        // ones (VGG-16 L0: 27 events over 64 bins), while in the pair and
+        // dwordx4 streams empty bins are rare and the extra scalar registers
+        // cost a wave per SIMD (pair stream: 8 -> 7; VGG L2/L3 +15%).
+        constexpr bool FAST = !COUNT && !CULIF && VEC == 1;
+        bool mono = false;
+        int th_end = 0;
+        if (FAST) {
+            const float nxt = __shfl_down(v_th, 1, 64);
+            mono = __ballot(lane + 1 < nb && !(v_th >= nxt)) == 0;
+            const uint64_t low = __ballot(lane < nb && !(v_th >= 1e-5f));
+            th_end = low ? (int)__builtin_ctzll(low) : nb;
+        }
 
 #define VD_BIN_START(b) ((b) < nb ? __builtin_amdgcn_readlane(v_bs, (b)) : blk_end)
 #define VD_FINALIZE(b, acc_)                                                            \
@@ -571,6 +628,47 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
         }                                                                               \
         if (__ballot(live) == 0 && (!COUNT || chunk_end_)) done = true;                 \
     } while (0)
+
+        // bins [r0, r1) of the block are empty and every earlier bin is
+        // closed: fire the neurons that cross in the run (see FAST above)
+        auto skip_empty = [&](int r0, int r1) {
+            const int ta = r0 > a.t_min - t0 ? r0 : a.t_min - t0;
+            const int tb = r1 < th_end ? r1 : th_end;
+            if (ta >= tb) return;
+            const float th_last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), tb - 1));
+            bool any = false;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) any = any || (alive[v] && carry[v] >= th_last);
+            if (__ballot(any) == 0) return;
+            int n_it = 0;
+            while ((1 << n_it) < tb - ta) ++n_it;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                // first t in [ta, tb) with theta[t] <= carry (it exists where
+                // carry >= th_last); every lane runs the search, as
+                // ds_bpermute reads the source lanes' registers
+                int lo = ta, hi = tb - 1;
+                for (int it = 0; it < n_it; ++it) {
+                    const int mid = (lo + hi) >> 1;
+                    const float thm =
+                        __int_as_float(__builtin_amdgcn_ds_bpermute(mid << 2, __float_as_int(v_th)));
+                    const bool le = thm <= carry[v];
+                    hi = le ? mid : hi;
+                    lo = le ? lo : mid + 1;
+                }
+                if (alive[v] && carry[v] >= th_last) {
+                    res[v] = (float)(t0 + lo);
+                    alive[v] = false;
+                }
+            }
+            live = alive[0];
+#pragma unroll
+            for (int v = 1; v < VEC; ++v) live = live || alive[v];
+            if (__ballot(live) == 0) done = true;
+        };
+        // the block-relative bin holding merged event idx (blk_end > idx):
+        // the last bin whose start is at most idx
+        auto bin_of = [&](int idx) { return __popcll(__ballot(lane < nb && v_bs <= idx)) - 1; };
 
         int bcur = 0;                    // open bin of this block
         int bend = VD_BIN_START(1);      // merged end of the open bin
@@ -631,6 +729,13 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
                             for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
                             ++bcur;
                             bend = VD_BIN_START(bcur + 1);
+                            if (FAST && mono && bend <= j + 8 * q + g) {
+                                const int bn = bin_of(j + 8 * q + g);
+                                skip_empty(bcur, bn);
+                                if (done) goto stream_done;
+                                bcur = bn;
+                                bend = VD_BIN_START(bcur + 1);
+                            }
                         }
 #pragma unroll
                         for (int v = 0; v < VEC; ++v)
@@ -649,6 +754,10 @@ __device__ __forceinline__ void stream_pixel(const StreamArgs& a, float* __restr
 #pragma unroll
             for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
             ++bcur;
+            if (FAST && mono && bcur < nb) {  // every bin after the last event is empty
+                skip_empty(bcur, nb);
+                break;
+            }
         }
 #undef VD_FINALIZE
 #undef VD_BIN_START
@@ -769,7 +878,7 @@ __host__ __device__ inline int fused_wave_words(int nel_max, int T) {
     return (w + 3) & ~3;
 }
 
-template <bool COUNT, int VEC, bool CULIF, int EPI>
+template <bool COUNT, int VEC, bool CULIF, int EPI, int NB>
 __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamArgs a,
                                                       float* __restrict__ out,
                                                       const float* __restrict__ theta, int nel_max) {
@@ -784,7 +893,7 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
     for (int q = 0; q < a.ppw; ++q) {
         const int64_t pix = pix0 + q;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)dense_build<9>(m, pix, cur, kinfo, L, bs);
+        (void)dense_build<9, NB>(m, pix, cur, kinfo, L, bs);
         wave_sync();
         stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
         wave_sync();  // this pixel's list reads precede the next pixel's build
@@ -1754,9 +1863,18 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     if (p.path == VDTTFS_PATH_FUSED) {
         // C_out <= 64: build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
-#define VD_LAUNCH_FUSED(C, L)                                                                      \
-    hipLaunchKernelGGL((k_stream_dense<C, 1, L, 1>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), \
+        // pixels of at most 64 elements (VGG-16 L0: 27) build from one chunk
+        // in the fewest registers
+#define VD_LAUNCH_FUSED_NB(C, L, NB)                                                                      \
+    hipLaunchKernelGGL((k_stream_dense<C, 1, L, 1, NB>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), \
                        lds, ctx->stream, m, a, out, theta, nel_max)
+#define VD_LAUNCH_FUSED(C, L)                \
+    do {                                     \
+        if (nel_max <= 64)                   \
+            VD_LAUNCH_FUSED_NB(C, L, 1);     \
+        else                                 \
+            VD_LAUNCH_FUSED_NB(C, L, 9);     \
+    } while (0)
         if (culif) {
             if (counters)
                 VD_LAUNCH_FUSED(true, true);
@@ -1769,6 +1887,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
                 VD_LAUNCH_FUSED(false, false);
         }
 #undef VD_LAUNCH_FUSED
+#undef VD_LAUNCH_FUSED_NB
         VD_HIP(hipGetLastError());
         return VDTTFS_OK;
     }
