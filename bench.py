@@ -318,7 +318,8 @@ def work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr):
             gb = 4.0 * float(ebin[i])
             row = {"layer": i, "kind": "fc" if fc else "conv",
                    "shape": f"{l.C_in}->{l.C_out} @ {l.H_in}x{l.W_in}" + ("" if fc else f", {l.K_h}x{l.K_w}"),
-                   "plan": {"path": ["auto", "bins", "dense", "fused", "reg"][path], "gather": gather, "ppw": ppw},
+                   "plan": {"path": ["auto", "bins", "dense", "fused", "reg", "window"][path], "gather": gather,
+                            "ppw": ppw},
                    "ms": ms, "eproc": int(eproc[i]), "ebin": int(ebin[i]), "e_noee": e_noee,
                    "skip_rate": 1.0 - float(eproc[i]) / max(1, e_noee),
                    "n_ev": int(n_ev[i]), "n_ev_host_equal": nev == int(n_ev[i]),

@@ -287,7 +287,11 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  *           layers with C_out <= 64, T <= 64, gather 1), VDTTFS_PATH_REG (no
  *           list: each lane keeps its receptive field in registers; conv
  *           layers with K_h*K_w*C_in <= 32, C_out <= 64, T <= 64; gather 1,
- *           ppw 64 / C_out; counting forwards run it as DENSE or FUSED)
+ *           ppw 64 / C_out; counting forwards run it as DENSE or FUSED),
+ *           VDTTFS_PATH_WINDOW (bucketize, then one kernel merges each
+ *           pixel's column lists through a 64-entry register window and
+ *           streams them, no merged list in memory; conv layers with <= 9
+ *           taps and FC layers, C_out >= 32, T <= 64)
  *   gather: 1 one c_out per lane; 2 two events per 16-byte load (C_out a
  *           multiple of 4 and <= 128); 4 four c_out per lane (C_out a
  *           multiple of 4)
@@ -299,11 +303,12 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  * choice; an unsupported request fails with VDTTFS_E_UNSUPPORTED and leaves
  * the layer's plan unchanged.  get_plan returns the resolved plan the next
  * forward uses. */
-#define VDTTFS_PATH_AUTO  0
-#define VDTTFS_PATH_BINS  1
-#define VDTTFS_PATH_DENSE 2
-#define VDTTFS_PATH_FUSED 3
-#define VDTTFS_PATH_REG   4
+#define VDTTFS_PATH_AUTO   0
+#define VDTTFS_PATH_BINS   1
+#define VDTTFS_PATH_DENSE  2
+#define VDTTFS_PATH_FUSED  3
+#define VDTTFS_PATH_REG    4
+#define VDTTFS_PATH_WINDOW 5
 typedef struct vdttfs_layer_plan {
     int32_t path, gather, ppw;
 } vdttfs_layer_plan;

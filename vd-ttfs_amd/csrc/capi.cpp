@@ -341,7 +341,8 @@ static IntegShape make_shape(const vdttfs_ctx* ctx, int B, int H_in, int W_in, i
 // One layer on the engine's kernels (list built in LDS, from the dense map
 // or from the bin-layout bucketize, then the wave-per-pixel stream) with the
 // built-in launch plan and context-owned scratch.  Scratch is sized for what
-// the layer's plan uses: the fused and register paths need no merged list.
+// the layer's plan uses: the fused, window and register paths need no merged
+// list.
 static int engine_layer(vdttfs_ctx* ctx, float* d_out, const float* d_in, const float* d_kernel,
                         const float* d_bias, const float* d_lut_decay, const float* d_lut_th, int t_min,
                         const IntegShape& s, unsigned long long* counters) {
@@ -350,8 +351,9 @@ static int engine_layer(vdttfs_ctx* ctx, float* d_out, const float* d_in, const 
     const int64_t cols = s.is_fc ? s.B : (int64_t)s.B * s.H_in * s.W_in;
     const int64_t n_pix = s.is_fc ? s.B : (int64_t)s.B * s.H_out * s.W_out;
     const int64_t cap = merged_list_cap(s);
-    const bool dense = integrate_dense_ok(ctx, s) && p.path != VDTTFS_PATH_BINS;
-    const bool lds_list = p.path == VDTTFS_PATH_FUSED || (p.path == VDTTFS_PATH_REG && !counters);
+    const bool dense = integrate_dense_ok(ctx, s) && !plan_bins(p);
+    const bool lds_list = p.path == VDTTFS_PATH_FUSED || p.path == VDTTFS_PATH_WINDOW ||
+                          (p.path == VDTTFS_PATH_REG && !counters);
     if (!lds_list)
         VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     if (dense)  // conv: merged lists straight from the dense map

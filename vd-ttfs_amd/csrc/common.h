@@ -112,6 +112,8 @@ struct LaunchPlan {
     int path = 0, gather = 0, ppw = 0;
 };
 constexpr int kMaxPixPerWave = 8;
+// The plan's lists come from the bin-layout bucketize (the bins and window paths).
+inline bool plan_bins(const LaunchPlan& p) { return p.path == VDTTFS_PATH_BINS || p.path == VDTTFS_PATH_WINDOW; }
 // Fills every field of *out: a requested field is checked against the
 // layer's shape (VDTTFS_E_UNSUPPORTED when the kernels cannot run it), a zero
 // field takes the built-in choice.

@@ -382,6 +382,9 @@ struct StreamArgs {
     int ppw;               // consecutive output pixels per wave
     int w_bytes;
     float decay, th;  // CuLIF neuron (T3V:62-63): I = I*decay + in; V += I; fire at V >= th
+    // windowed merge (k_stream_window): the bin layout and its row scale
+    const vd_event* bev;
+    int b_cin, b_rowbytes;
 };
 
 // Block -> (c_out block, group of 4 output pixels).  Workgroups are dealt to
@@ -897,6 +900,226 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
         wave_sync();
         stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
         wave_sync();  // this pixel's list reads precede the next pixel's build
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_stream_window: k_merge and k_stream in one kernel for the bins path (the
+// layers whose columns were bucketized: conv with C_in > 64, FC), T <= 64.
+// Whole merged lists in LDS would cost occupancy (a 3x3 pixel of 512 inputs
+// is up to 37 KB), so each wave streams its pixel's merged list through a
+// window of 64 entries held one per lane in registers, with the next window
+// in a second register: when the stream passes a window, the following one
+// is built straight from the columns' bin-layout lists.  Merged position p
+// of event i of column k in bin t is D[k][t] + i with D[k][t] =
+// sum_{k'<k} O_k'[t+1] + sum_{k'>k} O_k'[t] (O_k = the column's bin offsets,
+// as in k_merge), so within a column positions increase with i and a window
+// [P0, P0 + 64) takes from each column one contiguous index range: from
+// where the previous window stopped to the index whose position reaches
+// P0 + 64, which the bin holding P0 + 64 and the closed form give.  Lane f
+// loads the window's f-th event (column-major), computes its position and
+// ds_permute moves the entry to lane p - P0.  Nothing goes through HBM but
+// the bucketize output; the per-pixel tables live in LDS.
+// Measured on VGG-16 B=256 against bucketize + k_merge + k_stream (layer
+// times include the bucketize): slower on every bins layer -- 128 -> 128 at
+// 16x16 0.92 -> 1.16 ms, the 8x8 and 4x4 layers +3..7%, the 2x2 layers and
+// the FC +5..10% -- as building a window costs the wave about as many
+// instructions as streaming it, where k_merge's work ran in a kernel of its
+// own with every lane busy.  So the built-in plan keeps the two kernels, and
+// this path is a plan the caller may select (VDTTFS_PATH_WINDOW).
+template <int KMAX>
+struct WinCtx {
+    int dtab[KMAX][kBlockBins];   // D[k][t]
+    int o[KMAX][kBlockBins + 1];  // O_k[t], t in [0, T]
+    int S[kBlockBins + 1];        // merged start of bin t, S[T] = list length
+    int col[KMAX], krow[KMAX];    // in-bounds columns in (kh, kw) order; first weight-row byte offset
+    int lo[KMAX];                 // first index of column k not yet windowed
+    int nk, total;
+};
+
+// Per pixel: the in-bounds columns, their bin offsets, D and S.  T <= 64.
+template <int KMAX>
+__device__ __forceinline__ void win_setup(const MergeArgs& m, int64_t pix, WinCtx<KMAX>& w) {
+    const int lane = lane_id();
+    int img, h_out = 0, w_out = 0;
+    if (m.is_fc) {
+        img = (int)pix;
+    } else {
+        w_out = (int)(pix % m.W_out);
+        const int64_t q = pix / m.W_out;
+        h_out = (int)(q % m.H_out);
+        img = (int)(q / m.H_out);
+    }
+    int nk;
+    if (m.is_fc) {
+        nk = 1;
+        if (lane == 0) {
+            w.col[0] = img;
+            w.krow[0] = 0;
+        }
+    } else {
+        bool v = false;
+        int col = 0;
+        if (lane < m.K_h * m.K_w) {
+            const int kh = lane / m.K_w, kw = lane - kh * m.K_w;
+            const int hi = h_out - m.pad_h + kh, wi = w_out - m.pad_w + kw;
+            v = hi >= 0 && hi < m.H_in && wi >= 0 && wi < m.W_in;
+            col = (img * m.H_in + hi) * m.W_in + wi;
+        }
+        const uint64_t mk = __ballot(v);
+        nk = __popcll(mk);
+        if (v) {
+            const int slot = __popcll(mk & lanemask_lt());
+            w.col[slot] = col;
+            w.krow[slot] = lane * m.C_in * m.rowbytes;
+        }
+    }
+    wave_sync();
+    const int T = m.T, osb = T + 1;
+    int lo[KMAX], hi[KMAX];
+    int S = 0, total = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        lo[k] = hi[k] = 0;
+        if (k < nk) {
+            const int32_t* ob = m.off + (int64_t)uniform(w.col[k]) * osb;
+            if (lane < T) {
+                lo[k] = ob[lane];
+                hi[k] = ob[lane + 1];
+            }
+            const int tk = ob[T];
+            total += tk;
+            S += lo[k];
+            if (lane < T) w.o[k][lane] = lo[k];
+            if (lane == 0) {
+                w.o[k][T] = tk;
+                w.lo[k] = 0;
+            }
+        }
+    }
+    int A = 0, P = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        if (k < nk) {
+            P += lo[k];
+            if (lane < T) w.dtab[k][lane] = A + (S - P);
+            A += hi[k];
+        }
+    }
+    if (lane < T) w.S[lane] = S;
+    if (lane == 0) {
+        w.S[T] = total;
+        w.nk = nk;
+        w.total = total;
+    }
+    wave_sync();
+}
+
+// List reader over the window (see k_stream_window): w0 holds merged entries
+// base + lane, w1 the next 64.  Windows are built in order, 64 positions at
+// a time, when the stream passes one; entries past the list are zero (row 0,
+// alpha 0), like the padding of the HBM lists.  Loading a window's events one
+// window ahead (so they arrive while w0 streams) was measured slower: it
+// costs registers (the dwordx4 stream 92 -> 97 VGPRs, 5 -> 4 waves per SIMD)
+// and the building, not the wait, is what costs here.
+template <int KMAX>
+struct WinList {
+    WinCtx<KMAX>* w;
+    const vd_event* ev;
+    int C_in, rowbytes, T;
+    int base;
+    int2 w0, w1;
+    __device__ __forceinline__ int2 fill(int P0) {
+        const int lane = lane_id();
+        const int total = uniform(w->total);
+        int2 e = make_int2(0, 0);
+        if (P0 >= total) return e;  // uniform
+        const int P1 = P0 + 64;
+        const int nk = uniform(w->nk);
+        int t1 = -1;
+        if (P1 < total) {  // the bin holding position P1: the last bin starting at or before it
+            const int sl = lane < T ? w->S[lane] : 0x7fffffff;
+            t1 = __popcll(__ballot(sl <= P1)) - 1;
+        }
+        int kk = 0, cbase = 0, lo_sel = 0, C = 0;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            if (k < nk) {
+                const int lo = uniform(w->lo[k]);
+                int hi;
+                if (t1 < 0) {
+                    hi = uniform(w->o[k][T]);
+                } else {
+                    const int ot = uniform(w->o[k][t1]), on = uniform(w->o[k][t1 + 1]);
+                    const int d = P1 - uniform(w->dtab[k][t1]) - ot;
+                    hi = ot + (d < 0 ? 0 : (d > on - ot ? on - ot : d));
+                }
+                if (lane >= C && lane < C + (hi - lo)) {  // lane takes column k's (lane - C)-th event
+                    kk = k;
+                    cbase = C;
+                    lo_sel = lo;
+                }
+                C += hi - lo;
+                // every lane read lo[k] above; a wave's LDS operations
+                // execute in program order
+                if (lane == 0) w->lo[k] = hi;
+            }
+        }
+        int pos = lane;  // lanes past the window's events carry the zero padding
+        if (lane < C) {
+            const int i = lo_sel + (lane - cbase);
+            const vd_event x = ev[(int64_t)w->col[kk] * C_in + i];
+            const int b = (int)(x.key >> 24);
+            pos = w->dtab[kk][b] + i - P0;
+            e = make_int2(w->krow[kk] + (int)(x.key & 0xFFFFFFu) * rowbytes, __float_as_int(x.alpha));
+        }
+        e.x = __builtin_amdgcn_ds_permute(pos << 2, e.x);
+        e.y = __builtin_amdgcn_ds_permute(pos << 2, e.y);
+        return e;
+    }
+    __device__ __forceinline__ void start(const void* L_, int j, const StreamArgs& a) {
+        w = static_cast<WinCtx<KMAX>*>(const_cast<void*>(L_));
+        ev = a.bev;
+        C_in = a.b_cin;
+        rowbytes = a.b_rowbytes;
+        T = a.T;
+        base = j;  // 0: T <= 64 is one bin block
+        w0 = fill(j);
+        w1 = fill(j + 64);
+    }
+    __device__ __forceinline__ Group8 take(int j) {
+        if (j - base >= 64) {  // uniform
+            base += 64;
+            w0 = w1;
+            w1 = fill(base + 64);
+        }
+        const int k = j - base;
+        Group8 g;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            g.v[i].x = __builtin_amdgcn_readlane(w0.x, k + i);
+            g.v[i].y = __builtin_amdgcn_readlane(w0.y, k + i);
+        }
+        return g;
+    }
+};
+
+template <bool COUNT, int VEC, bool CULIF, int EPI, int KMAX>
+__global__ __launch_bounds__(256) void k_stream_window(MergeArgs m, StreamArgs a, float* __restrict__ out,
+                                                       const float* __restrict__ theta) {
+    __shared__ WinCtx<KMAX> ctx_all[4];
+    const int wave = uniform(threadIdx.x >> 6);
+    int cb;
+    int64_t pg;
+    map_block(a.n_cblk, cb, pg);
+    WinCtx<KMAX>& w = ctx_all[wave];
+    const int64_t pix0 = (pg * 4 + wave) * a.ppw;
+    for (int q = 0; q < a.ppw; ++q) {
+        const int64_t pix = pix0 + q;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        win_setup<KMAX>(m, pix, w);
+        stream_one<COUNT, VEC, CULIF, EPI, WinList<KMAX>>(a, out, &w, w.S, theta, pix, cb);
+        wave_sync();  // this pixel's table reads precede the next pixel's setup
     }
 }
 
@@ -1490,6 +1713,56 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
     return VDTTFS_OK;
 }
 
+// The window path: bucketize output -> k_stream_window (merge + stream).
+int launch_stream_window(vdttfs_ctx* ctx, const MergeArgs& m, float* out, const vd_event* ev, const float* W,
+                         int64_t wbytes, const float* bias, const float* theta, int t_min, const IntegShape& sh,
+                         unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan& p) {
+    int vec, epi;
+    StreamArgs a = stream_args(ctx, out, nullptr, 0, nullptr, W, wbytes, bias, theta, t_min, sh, counters, culif,
+                               p, &vec, &epi);
+    a.bev = ev;
+    a.b_cin = sh.C_in;
+    a.b_rowbytes = sh.C_out * 4;
+    const int waves = 4;
+    const int64_t n_pg = (a.n_pix + waves * a.ppw - 1) / (waves * a.ppw);
+    const int64_t blocks = n_pg * a.n_cblk;
+    if (blocks <= 0) return VDTTFS_OK;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    if (m.T > kBlockBins || (!m.is_fc && m.K_h * m.K_w > 9))
+        return set_error(VDTTFS_E_UNSUPPORTED, "window path: T <= 64 and at most 9 taps");
+#define VD_LAUNCH_WIN(C, V, L, E, K)                                                                     \
+    hipLaunchKernelGGL((k_stream_window<C, V, L, E, K>), dim3((unsigned)blocks), dim3(64 * waves), 0,     \
+                       ctx->stream, m, a, out, theta)
+#define VD_LAUNCH_WIN_K(C, V, L, E)          \
+    do {                                     \
+        if (m.is_fc)                         \
+            VD_LAUNCH_WIN(C, V, L, E, 1);    \
+        else                                 \
+            VD_LAUNCH_WIN(C, V, L, E, 9);    \
+    } while (0)
+#define VD_LAUNCH_WIN_V(C, L)                \
+    do {                                     \
+        if (epi == 2)                        \
+            VD_LAUNCH_WIN_K(C, 2, L, 2);     \
+        else if (vec == 4)                   \
+            VD_LAUNCH_WIN_K(C, 4, L, 1);     \
+        else                                 \
+            VD_LAUNCH_WIN_K(C, 1, L, 1);     \
+    } while (0)
+    // the CuLIF engine always takes the built-in plan, which never asks for
+    // this path, so only the LUT neuron is instantiated
+    if (culif) return set_error(VDTTFS_E_UNSUPPORTED, "window path: LUT-threshold layers only");
+    if (counters)
+        VD_LAUNCH_WIN_V(true, false);
+    else
+        VD_LAUNCH_WIN_V(false, false);
+#undef VD_LAUNCH_WIN_V
+#undef VD_LAUNCH_WIN_K
+#undef VD_LAUNCH_WIN
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
 int launch_stream_narrow(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
                          const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
                          const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
@@ -1542,6 +1815,11 @@ bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     const int nel_max = sh.K_h * sh.K_w * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, ctx->c.T) * sizeof(int);
     return gather == 1 && sh.C_out <= 64 && ctx->c.T <= kBlockBins && lds <= kFusedMaxLds;
+}
+
+// k_stream_window's limits: one bin block, the per-pixel tables of <= 9 columns
+bool window_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    return ctx->c.T <= kBlockBins && (sh.is_fc || sh.K_h * sh.K_w <= 9);
 }
 
 // k_conv_small's limits (the receptive field and the bins fit in registers)
@@ -1647,7 +1925,7 @@ int plan_error(const IntegShape& sh, const char* what) {
 }  // namespace
 
 int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& req, LaunchPlan* out) {
-    if (req.path < 0 || req.path > VDTTFS_PATH_REG || req.gather < 0 || req.ppw < 0 || req.ppw > 64)
+    if (req.path < 0 || req.path > VDTTFS_PATH_WINDOW || req.gather < 0 || req.ppw < 0 || req.ppw > 64)
         return set_error(VDTTFS_E_INVALID, "plan: path %d, gather %d, ppw %d out of range", req.path,
                          req.gather, req.ppw);
     int64_t wbytes;
@@ -1682,7 +1960,8 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     }
     if (narrow) {  // one pixel per C_out lanes
         const int P = 64 / sh.C_out;
-        if (req.path == VDTTFS_PATH_FUSED || (req.gather && req.gather != 1) || (req.ppw && req.ppw != P))
+        if (req.path == VDTTFS_PATH_FUSED || req.path == VDTTFS_PATH_WINDOW || (req.gather && req.gather != 1) ||
+            (req.ppw && req.ppw != P))
             return plan_error(sh, "narrow layers take gather 1, 64 / C_out pixels per wave, paths bins or dense");
         p.path = req.path ? req.path : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS);
         if (p.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
@@ -1722,13 +2001,16 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
         return plan_error(sh, "fused path needs the dense limits, C_out <= 64, T <= 64 and gather 1");
+    if (req.path == VDTTFS_PATH_WINDOW && !window_ok(ctx, sh))
+        return plan_error(sh, "window path needs T <= 64 and at most 9 taps (or an FC layer)");
     p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
     if (req.ppw) {
         p.ppw = req.ppw;
     } else {
         const int64_t n_pix = n_pixels(sh);
         p.ppw = n_pix >= (INT64_C(1) << 20) ? 2 : 1;
-        if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED) {  // k_stream's residency (the fused kernel's is LDS-bound)
+        if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED && p.path != VDTTFS_PATH_WINDOW) {
+            // k_stream's residency (the fused and window kernels' is LDS-bound)
             const int vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
             const int64_t n_cblk = p.gather == 2 ? 1 : (sh.C_out + 64 * vec - 1) / (64 * vec);
             const int64_t cap = stream_wave_capacity(ctx, p.gather);
@@ -1745,7 +2027,7 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
                           unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
-    if (plan && plan->path && plan->path != VDTTFS_PATH_BINS)
+    if (plan && plan->path && !plan_bins(*plan))
         return set_error(VDTTFS_E_INVALID, "integrate_bins: the plan asks for a dense path");
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
@@ -1758,7 +2040,7 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     const int nk_max = sh.is_fc ? 1 : sh.K_h * sh.K_w;
     const int64_t n_pix = n_pixels(sh);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
-    if (!list || !bstart || list_cap < cap)
+    if (p.path != VDTTFS_PATH_WINDOW && (!list || !bstart || list_cap < cap))
         return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
     MergeArgs m{};
     m.list = list;
@@ -1779,6 +2061,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     m.pad_w = sh.pad_w;
     m.is_fc = sh.is_fc;
     m.rowbytes = sh.C_out * 4;
+    if (p.path == VDTTFS_PATH_WINDOW)
+        return launch_stream_window(ctx, m, out, ev, W, wbytes, bias, theta, t_min, sh, counters, culif, p);
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
     if (nk_max == 1)
@@ -1803,7 +2087,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
         return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
-    if (p.path == VDTTFS_PATH_BINS)
+    if (plan_bins(p))
         return set_error(VDTTFS_E_INVALID, "integrate_dense: the plan asks for the bins path");
     if (p.path == VDTTFS_PATH_REG) {
         if (!counters && !culif) return launch_conv_small(ctx, out, in, alpha, W, bias, theta, t_min, sh);

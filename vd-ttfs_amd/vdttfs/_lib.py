@@ -28,7 +28,7 @@ ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES = 0, 1, 2
 READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
 STEP_T1, STEP_T2, STEP_T3 = 1, 2, 3
-PATH_AUTO, PATH_BINS, PATH_DENSE, PATH_FUSED, PATH_REG = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_BINS, PATH_DENSE, PATH_FUSED, PATH_REG, PATH_WINDOW = 0, 1, 2, 3, 4, 5
 
 
 class VdttfsError(RuntimeError):

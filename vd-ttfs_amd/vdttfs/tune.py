@@ -34,7 +34,8 @@ import numpy as np
 
 from . import core, models
 
-PATHS = {core.PATH_BINS: "bins", core.PATH_DENSE: "dense", core.PATH_FUSED: "fused", core.PATH_REG: "reg"}
+PATHS = {core.PATH_BINS: "bins", core.PATH_DENSE: "dense", core.PATH_FUSED: "fused", core.PATH_REG: "reg",
+         core.PATH_WINDOW: "window"}
 
 
 def _min_round_ms(ctx, net, x, d_pred, reps, rounds, per_layer):
