@@ -292,9 +292,9 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  *           pixel's column lists through a 64-entry register window and
  *           streams them, no merged list in memory; conv layers with <= 9
  *           taps and FC layers, C_out >= 32, T <= 64)
- *   gather: 1 one c_out per lane; 2 two events per 16-byte load (C_out a
- *           multiple of 4 and <= 128); 4 four c_out per lane (C_out a
- *           multiple of 4)
+ *   gather: 1 one c_out per lane; 2 two events per 16-byte load, 128 c_out
+ *           per wave (C_out a multiple of 4); 4 four c_out per lane, 256
+ *           c_out per wave (C_out a multiple of 4)
  *   ppw:    output pixels per wave, 1..8
  * Layers with C_out < 32 run one pixel per C_out lanes (gather 1, ppw =
  * 64 / C_out, paths BINS or DENSE); layers outside the merged-list limits

@@ -458,20 +458,25 @@ struct GlobalGather {
     }
 };
 
-// PairGather: for 64 < C_out <= 128 (a c_out row of at most 512 B), one
+// PairGather: a 128-wide c_out block per wave (512 B of each row), one
 // dwordx4 load fetches two events at once -- the lower half-wave loads event
 // 2i's row, the upper half event 2i+1's, 4 c_out per lane -- and two
 // v_permlane32_swap exchange the halves' (2,3) and (0,1) components, so that
-// lane (h, r) ends owning c_out 4r+2h, 4r+2h+1 with both events' weights.
+// lane (h, r) ends owning c_out 128cb+4r+2h, +1 with both events' weights.
 // Every load then carries 1 KB with all 64 lanes busy (a 4-c_out-per-lane
 // load would leave half the wave idle); lanes load for each other, so loads
-// are not skipped per lane.
+// are not skipped per lane.  Against four c_out per lane (one event, 256
+// c_out per load) it moves the same bytes per instruction with half the
+// c_out per wave: twice the waves per pixel, for layers too small to fill
+// the device, and each XCD's share of the weights halves.  Loads past the
+// last c_out (C_out not a multiple of 128) read the next row or, past the
+// buffer, zero; those lanes' results are not stored.
 struct PairGather {
     static constexpr int OWN = 2;
     __amdgpu_buffer_rsrc_t r;
-    int lane_off;  // 16 * (lane % 32)
+    int lane_off;  // 16 * (lane % 32) + 512 * cb
     int h;         // lane / 32: which event of a load this lane fetches
-    __device__ static int c0(int, int lane) { return 4 * (lane & 31) + 2 * (lane >> 5); }
+    __device__ static int c0(int cb, int lane) { return 128 * cb + 4 * (lane & 31) + 2 * (lane >> 5); }
     __device__ __forceinline__ void group(const int2 (&e)[8], Vf<2> (&w)[8], bool) const {
         typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -773,7 +778,7 @@ stream_done:
 }
 
 // One (pixel, c_out block) with the gather type of EPI = events per load:
-// 1 (GlobalGather<VEC>) or 2 (PairGather, VEC = 2, one c_out block).  L and BS
+// 1 (GlobalGather<VEC>) or 2 (PairGather, VEC = 2, 128-wide c_out blocks).  L and BS
 // are the pixel's merged list and bin starts; LR reads the list.
 template <bool COUNT, int VEC, bool CULIF, int EPI, class LR>
 __device__ __forceinline__ void stream_one(const StreamArgs& a, float* __restrict__ out,
@@ -799,7 +804,7 @@ __device__ __forceinline__ void stream_one(const StreamArgs& a, float* __restric
         static_assert(VEC == 2 && EPI == 2, "PairGather owns 2 c_out per lane");
         PairGather g;
         g.r = rsrc;
-        g.lane_off = 16 * (lane & 31);
+        g.lane_off = 16 * (lane & 31) + 512 * cb;
         g.h = lane >> 5;
         stream_pixel<COUNT, CULIF, PairGather, LR>(a, out, L, BS, theta, pix, cb, g, cnt_proc, cnt_bin);
     }
@@ -1665,7 +1670,7 @@ StreamArgs stream_args(vdttfs_ctx* ctx, float* out, const int2* list, int64_t ca
     a.th = culif ? culif->th : 0.0f;
     *vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
     *epi = p.gather == 2 ? 2 : 1;
-    a.n_cblk = *epi > 1 ? 1 : (sh.C_out + 64 * *vec - 1) / (64 * *vec);
+    a.n_cblk = *epi > 1 ? (sh.C_out + 127) / 128 : (sh.C_out + 64 * *vec - 1) / (64 * *vec);
     a.w_bytes = (int)wbytes;
     a.ppw = p.ppw > 0 ? p.ppw : 1;
     return a;
@@ -1977,7 +1982,6 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     if (req.gather) {
         if (req.gather != 1 && req.gather != 2 && req.gather != 4) return plan_error(sh, "gather is 1, 2 or 4");
         if (req.gather != 1 && sh.C_out % 4 != 0) return plan_error(sh, "gather 2 and 4 need C_out % 4 == 0");
-        if (req.gather == 2 && sh.C_out > 128) return plan_error(sh, "gather 2 covers at most 128 c_out");
         p.gather = req.gather;
     } else {
         p.gather = (sh.C_out % 4 == 0 && sh.C_out > 64) ? (sh.C_out <= 128 ? 2 : 4) : 1;
@@ -2012,7 +2016,7 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED && p.path != VDTTFS_PATH_WINDOW) {
             // k_stream's residency (the fused and window kernels' is LDS-bound)
             const int vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
-            const int64_t n_cblk = p.gather == 2 ? 1 : (sh.C_out + 64 * vec - 1) / (64 * vec);
+            const int64_t n_cblk = p.gather == 2 ? (sh.C_out + 127) / 128 : (sh.C_out + 64 * vec - 1) / (64 * vec);
             const int64_t cap = stream_wave_capacity(ctx, p.gather);
             if (cap > 0 && n_pix * n_cblk > cap && (n_pix + 1) / 2 * n_cblk <= cap) p.ppw = 2;
         }

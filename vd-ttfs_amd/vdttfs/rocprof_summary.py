@@ -9,6 +9,7 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
   python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME \
          [--workload KEY] [--first PREFIX] [--copy-name NAME]
   python -m vdttfs.rocprof_summary counters DIR NAME           # occupancy, LDS conflicts
+  python -m vdttfs.rocprof_summary per-wave DIR NAME [PREFIX]  # every counter per wave, per dispatch
 
 ``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
 benchmark, and the same two counters over ``bench.py --copy-calibration``
@@ -205,6 +206,32 @@ def counters(d: str, name: str) -> str:
     return "\n".join(out)
 
 
+def per_wave(d: str, name: str, first: str = "k_encode") -> str:
+    """One row per dispatch of the last non-counting forward: every counter
+    of the run divided by the dispatch's SQ_WAVES (so, per wave), and the
+    derived OccupancyPercent as is."""
+    rows = _csv(d, name, "counter_collection")
+    by = collections.OrderedDict()
+    for r in rows:
+        k = int(r["Dispatch_Id"])
+        e = by.setdefault(k, {"Kernel_Name": r["Kernel_Name"], "Dispatch_Id": k,
+                              "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    fw = [f for f in _forwards(list(by.values()), key_start="Dispatch_Id", first=first) if not _is_counting(f)]
+    if not fw:
+        return "no forward found"
+    f = fw[-1]
+    names = [c for c in f[0] if c not in ("Kernel_Name", "Dispatch_Id", "us", "SQ_WAVES")]
+    out = ["| # | kernel | us | waves | " + " | ".join(n + ("" if n == "OccupancyPercent" else "/wave") for n in names)
+           + " |", "|---:|---|---:|---:|" + "---:|" * len(names)]
+    for i, e in enumerate(f):
+        w = max(e.get("SQ_WAVES", 0.0), 1.0)
+        vals = [("%.1f" % e[n]) if n == "OccupancyPercent" else ("%.1f" % (e[n] / w)) for n in names]
+        out.append("| %d | %s | %.1f | %d | %s |" % (i, short_name(e["Kernel_Name"]), e["us"], e.get("SQ_WAVES", 0),
+                                                     " | ".join(vals)))
+    return "\n".join(out)
+
+
 def main(argv) -> int:
     if len(argv) < 2:
         print(__doc__)
@@ -221,6 +248,8 @@ def main(argv) -> int:
                       copy_name=opts.get("--copy-name", "")))
     elif cmd == "counters":
         print(counters(argv[2], argv[3]))
+    elif cmd == "per-wave":
+        print(per_wave(argv[2], argv[3], *argv[4:5]))
     else:
         print(__doc__)
         return 2
