@@ -211,6 +211,18 @@ constexpr int kDenseMaxBins = 256;
 constexpr int kDenseMaxCin = 64;
 constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 
+// Merged-list entry stores: (row bytes, alpha bits) pairs, or the two as
+// separate arrays (k_stream_quad reads four rows and four alphas at a time).
+struct SoaList {
+    int* row;
+    int* alpha;
+};
+__device__ __forceinline__ void list_put(int2* p, int pos, int row, int alpha) { p[pos] = make_int2(row, alpha); }
+__device__ __forceinline__ void list_put(const SoaList& p, int pos, int row, int alpha) {
+    p.row[pos] = row;
+    p.alpha[pos] = alpha;
+}
+
 // Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
 // tail zeroed) and its T+1 bin starts into `bs`, and returns the list length.
 // `cur` (T ints) and `kinfo` (2 * KMAX ints) are the wave's LDS scratch.  The
@@ -335,7 +347,7 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
                 }
                 if (valid) {
                     const int pos = cur[b] + __popcll(m & lt);
-                    out[pos] = make_int2((pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
+                    list_put(out, pos, (pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
                 }
                 wave_sync();
                 if (valid && (m & lt) == 0) cur[b] += __popcll(m);
@@ -344,7 +356,7 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
         }
     }
     // zeroed tail: the stream kernel reads whole groups of 8 entries
-    for (int i = lane; i < kListPad; i += 64) out[total + i] = make_int2(0, 0);
+    for (int i = lane; i < kListPad; i += 64) list_put(out, total + i, 0, 0);
     return total;
 }
 
@@ -904,6 +916,158 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
         (void)dense_build<9, NB>(m, pix, cur, kinfo, L, bs);
         wave_sync();
         stream_one<COUNT, VEC, CULIF, EPI, LdsList>(a, out, L, bs, theta, pix, 0);
+        wave_sync();  // this pixel's list reads precede the next pixel's build
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_stream_quad: the fused dense path for the LUT-threshold neuron without
+// counters (C_out <= 64, T <= 64), built for the fewest instructions per
+// event and per bin; k_stream_dense serves the counting and CuLIF forms.
+//
+// Gathers: one dwordx4 load fetches four events at once -- lane (q, r)
+// (q = lane / 16, r = lane % 16) loads c_out 4r .. 4r+3 of event q's row --
+// and a 4x4 transpose across lanes r, r+16, r+32, r+48 (v_permlane32_swap
+// on components (0,2), (1,3), then v_permlane16_swap on (0,1), (2,3)) leaves
+// lane (q, r) owning c_out 4r+q with all four events' weights.  A dwordx4
+// load costs the texture unit about 2.3x a dword load and carries 4x the
+// bytes.  The list lives in LDS as two arrays; each lane group reads its
+// event's row (one ds_read_b32 per four events) and every lane the four
+// alphas (one broadcast ds_read_b128), so no v_readlane per event.
+//
+// Bins: the neuron's state is carry, the open bin's delta (acc) and the
+// spike bin; "alive" is a wave mask in SGPRs and a bin where no spike may
+// occur (b < t_min or theta[b] < 1e-5) takes a NaN threshold, so closing a
+// bin is one compare, two mask operations and one v_cndmask.  Positions at
+// or past the list's end close every remaining bin, which ends the stream.
+//
+// LDS words of one wave: list rows and alphas (the list, its zeroed tail and
+// a multiple of 4 so the alpha array stays 16-byte aligned), T + 1 bin
+// starts, T cursors, the tap table.
+__host__ __device__ inline int quad_list_entries(int nel_max) { return (nel_max + kListPad + 3) & ~3; }
+__host__ __device__ inline int quad_wave_words(int nel_max, int T) {
+    return (2 * quad_list_entries(nel_max) + (T + 1) + T + 2 * 9 + 3) & ~3;
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
+                                                     const float* __restrict__ theta, int nel_max) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) int lds_words[];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int E = quad_list_entries(nel_max);
+    int* region = lds_words + wave * quad_wave_words(nel_max, a.T);
+    int* rows = region;
+    int* alph = region + E;
+    int* bs = alph + E;
+    int* cur = bs + a.T + 1;
+    int* kinfo = cur + a.T;
+    const int lane = lane_id();
+    const int q = lane >> 4, r = lane & 15;
+    const int co = 4 * r + q;  // the c_out this lane integrates
+    const bool ok = co < a.C_out;
+    const int voff = 16 * r;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    const int T = a.T;
+    // lane d: theta[d] where a spike may occur in bin d (d >= t_min,
+    // theta[d] >= 1e-5), else NaN, which no carry compares >= to
+    const float th_d = lane < T ? theta[lane] : 0.0f;
+    const float v_th = (lane < T && lane >= a.t_min && th_d >= 1e-5f) ? th_d : __builtin_nanf("");
+    const float bias = ok ? a.bias[co] : 0.0f;
+    const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.ppw;
+    for (int pq = 0; pq < a.ppw; ++pq) {
+        const int64_t pix = pix0 + pq;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        (void)dense_build<9, NB>(m, pix, cur, kinfo, SoaList{rows, alph}, bs);
+        wave_sync();
+        const int v_end = lane < T ? bs[lane + 1] : 0;  // end of bin `lane`
+        float carry = bias, acc = 0.0f;
+        int res = -1;  // spike bin, -1: none yet
+        uint64_t alive = __ballot(ok);
+        int b = 0;
+        int bend = __builtin_amdgcn_readlane(v_end, 0);
+        struct Raw {
+            u4 x[2];
+            f4 al[2];
+        };
+        auto load = [&](int j, Raw& g) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int row = rows[j + 4 * k + q];
+                g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, row + voff, 0, 0);
+                g.al[k] = *reinterpret_cast<const f4*>(alph + j + 4 * k);
+            }
+        };
+        // close bin b and the empty bins after it that end by position p (bin
+        // ends do not decrease, so they are the first `stop` bins); true when
+        // the stream is over
+        auto close_to = [&](int p) -> bool {
+            carry = carry + acc;
+            acc = 0.0f;
+            const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
+            do {
+                const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+                const uint64_t f = __ballot(carry >= th) & alive;
+                res = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res;
+                alive &= ~f;
+            } while (++b < stop);
+            if (b >= T || alive == 0) return true;
+            bend = __builtin_amdgcn_readlane(v_end, b);
+            return false;
+        };
+        // integrates positions j .. j+7; true when the stream is over
+        auto consume = [&](int j, Raw& g) -> bool {
+            float w[8], al[8];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                unsigned c0 = g.x[k].x, c1 = g.x[k].y, c2 = g.x[k].z, c3 = g.x[k].w;
+                auto p = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
+                c0 = p[0];
+                c2 = p[1];
+                p = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
+                c1 = p[0];
+                c3 = p[1];
+                p = __builtin_amdgcn_permlane16_swap(c0, c1, false, false);
+                c0 = p[0];
+                c1 = p[1];
+                p = __builtin_amdgcn_permlane16_swap(c2, c3, false, false);
+                c2 = p[0];
+                c3 = p[1];
+                w[4 * k + 0] = __uint_as_float(c0);
+                w[4 * k + 1] = __uint_as_float(c1);
+                w[4 * k + 2] = __uint_as_float(c2);
+                w[4 * k + 3] = __uint_as_float(c3);
+                al[4 * k + 0] = g.al[k].x;
+                al[4 * k + 1] = g.al[k].y;
+                al[4 * k + 2] = g.al[k].z;
+                al[4 * k + 3] = g.al[k].w;
+            }
+            if (bend >= j + 8) {  // all eight in the open bin
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(w[i], al[i], acc);
+                return false;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (bend <= j + i && close_to(j + i)) return true;
+                acc = __builtin_fmaf(w[i], al[i], acc);
+            }
+            return false;
+        };
+        // the next group's loads are issued before this group's wait
+        Raw g0, g1;
+        load(0, g0);
+        for (int j = 0;; j += 16) {
+            load(j + 8, g1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (consume(j, g0)) break;
+            load(j + 16, g0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (consume(j + 8, g1)) break;
+        }
+        if (ok) out[pix * a.C_out + co] = res >= 0 ? (float)res : kInfTime;
         wave_sync();  // this pixel's list reads precede the next pixel's build
     }
 }
@@ -2151,6 +2315,17 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     if (p.path == VDTTFS_PATH_FUSED) {
         // C_out <= 64: build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
+        if (!counters && !culif) {
+            const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, m.T) * sizeof(int);
+            if (nel_max <= 64)
+                hipLaunchKernelGGL(k_stream_quad<1>, dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds,
+                                   ctx->stream, m, a, out, theta, nel_max);
+            else
+                hipLaunchKernelGGL(k_stream_quad<9>, dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds,
+                                   ctx->stream, m, a, out, theta, nel_max);
+            VD_HIP(hipGetLastError());
+            return VDTTFS_OK;
+        }
         // pixels of at most 64 elements (VGG-16 L0: 27) build from one chunk
         // in the fewest registers
 #define VD_LAUNCH_FUSED_NB(C, L, NB)                                                                      \
