@@ -55,6 +55,7 @@ struct MergeArgs {
     int T;
     int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad_h, pad_w, is_fc;
     int rowbytes;          // C_out * 4
+    FastDiv div_w, div_h;  // by W_out, H_out (n_pix < 2^31)
 };
 
 template <int KMAX>
@@ -72,10 +73,10 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
     if (a.is_fc) {
         img = (int)pix;
     } else {
-        w_out = (int)(pix % a.W_out);
-        const int64_t q = pix / a.W_out;
-        h_out = (int)(q % a.H_out);
-        img = (int)(q / a.H_out);
+        const int q = fdiv((int)pix, a.div_w);
+        w_out = (int)pix - q * a.W_out;
+        img = fdiv(q, a.div_h);
+        h_out = q - img * a.H_out;
     }
     // in-bounds receptive columns, compacted in (kh, kw) order
     int nk;
@@ -205,23 +206,13 @@ struct DenseMergeArgs {
     int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad_h, pad_w;
     int rowbytes;          // C_out * 4
     float inv_cin;         // 1 / C_in
+    FastDiv div_w, div_h;  // by W_out, H_out (n_pix < 2^31)
+    int in_bytes;          // bytes of `in` (k_stream_quad: below 2^31), else 0
 };
 
 constexpr int kDenseMaxBins = 256;
 constexpr int kDenseMaxCin = 64;
 constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
-
-// Merged-list entry stores: (row bytes, alpha bits) pairs, or the two as
-// separate arrays (k_stream_quad reads four rows and four alphas at a time).
-struct SoaList {
-    int* row;
-    int* alpha;
-};
-__device__ __forceinline__ void list_put(int2* p, int pos, int row, int alpha) { p[pos] = make_int2(row, alpha); }
-__device__ __forceinline__ void list_put(const SoaList& p, int pos, int row, int alpha) {
-    p.row[pos] = row;
-    p.alpha[pos] = alpha;
-}
 
 // Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
 // tail zeroed) and its T+1 bin starts into `bs`, and returns the list length.
@@ -231,10 +222,10 @@ template <int KMAX, int NB, class ListPtr, class BinPtr>
 __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo,
                                            ListPtr out, BinPtr bs) {
     const int lane = lane_id();
-    const int w_out = (int)(pix % a.W_out);
-    const int64_t q = pix / a.W_out;
-    const int h_out = (int)(q % a.H_out);
-    const int img = (int)(q / a.H_out);
+    const int q = fdiv((int)pix, a.div_w);
+    const int w_out = (int)pix - q * a.W_out;
+    const int img = fdiv(q, a.div_h);
+    const int h_out = q - img * a.H_out;
     // in-bounds receptive columns, compacted in (kh, kw) order
     int nk;
     {
@@ -347,7 +338,7 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
                 }
                 if (valid) {
                     const int pos = cur[b] + __popcll(m & lt);
-                    list_put(out, pos, (pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
+                    out[pos] = make_int2((pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
                 }
                 wave_sync();
                 if (valid && (m & lt) == 0) cur[b] += __popcll(m);
@@ -356,7 +347,7 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
         }
     }
     // zeroed tail: the stream kernel reads whole groups of 8 entries
-    for (int i = lane; i < kListPad; i += 64) list_put(out, total + i, 0, 0);
+    for (int i = lane; i < kListPad; i += 64) out[total + i] = make_int2(0, 0);
     return total;
 }
 
@@ -941,12 +932,164 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
 // bin is one compare, two mask operations and one v_cndmask.  Positions at
 // or past the list's end close every remaining bin, which ends the stream.
 //
+// List build (quad_build): as dense_build, but the rank of an event among
+// its chunk's lanes of the same bin comes from LDS bit masks instead of a
+// multisplit of bit ballots: each lane ORs its lane bit into its bin's
+// 64-bit mask (OR commutes, so the order the LDS serves same-address lanes
+// in does not matter), reads the mask back and counts the bits below its
+// own; the bin's last lane adds the chunk's count to the bin and clears the
+// mask.  Pass 1 keeps each event's rank in its packed register, so pass 2
+// places it at cursor + rank with no second ranking.
+//
 // LDS words of one wave: list rows and alphas (the list, its zeroed tail and
-// a multiple of 4 so the alpha array stays 16-byte aligned), T + 1 bin
-// starts, T cursors, the tap table.
-__host__ __device__ inline int quad_list_entries(int nel_max) { return (nel_max + kListPad + 3) & ~3; }
+// a multiple of 4 so the alpha array stays 16-byte aligned; the bin masks,
+// 2T words, use the start of this region during pass 1), T + 1 bin starts,
+// T cursors, the tap table.
+__host__ __device__ inline int quad_list_entries(int nel_max, int T) {
+    const int e = nel_max + kListPad > T ? nel_max + kListPad : T;
+    return (e + 3) & ~3;
+}
 __host__ __device__ inline int quad_wave_words(int nel_max, int T) {
-    return (2 * quad_list_entries(nel_max) + (T + 1) + T + 2 * 9 + 3) & ~3;
+    return (2 * quad_list_entries(nel_max, T) + (T + 1) + T + 2 * 9 + 3) & ~3;
+}
+
+// Packed event of quad_build: bin (bits 0..6, 0x7F: no event), decay-LUT
+// index (7..13), rank in its chunk's bin (14..19), last of the chunk's bin
+// (20), weight row (21..31).  T <= 64 and at most 9 x 64 rows.
+template <int NB>
+__device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
+                                          int* alph, int* bs) {
+    constexpr int KMAX = 9;
+    const int lane = lane_id();
+    const int qd = fdiv((int)pix, a.div_w);
+    const int w_out = (int)pix - qd * a.W_out;
+    const int img = fdiv(qd, a.div_h);
+    const int h_out = qd - img * a.H_out;
+    int nk;
+    {
+        bool v = false;
+        int col = 0;
+        if (lane < a.K_h * a.K_w) {
+            const int kh = lane / a.K_w, kw = lane - kh * a.K_w;
+            const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
+            v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
+            col = (img * a.H_in + hi) * a.W_in + wi;
+        }
+        const uint64_t m = __ballot(v);
+        nk = uniform(__popcll(m));
+        if (v) {
+            const int slot = __popcll(m & lanemask_lt());
+            kinfo[slot] = col;
+            kinfo[KMAX + slot] = lane * a.C_in;
+        }
+    }
+    unsigned* msk = reinterpret_cast<unsigned*>(rows);  // 2 words per bin during pass 1
+    if (lane < a.T) {
+        cur[lane] = 0;
+        msk[2 * lane] = 0u;
+        msk[2 * lane + 1] = 0u;
+    }
+    wave_sync();
+    const int nel = nk * a.C_in;       // <= 9 * 64
+    const int n_chunks = (nel + 63) >> 6;  // <= NB
+    int pk[NB];
+    {
+        // element f = c * 64 + lane: tap k = f / C_in (the quotient's
+        // fractional part is >= 0.5 / 64, so the float product rounds it
+        // correctly), cin ci.  Every chunk's load is issued before any is
+        // used (elements past the end load the map's first word).
+        const __amdgpu_buffer_rsrc_t rin =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+        float xs[NB];
+        int rw[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const int f = c * 64 + lane;
+            const bool in = f < nel;
+            const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
+            const int ci = in ? f - k * a.C_in : 0;
+            rw[c] = kinfo[KMAX + k] + ci;
+            const int off = in ? (kinfo[k] * a.C_in + ci) * 4 : 0;
+            xs[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, 0, 0));
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const bool in = c * 64 + lane < nel;
+            const int b = in ? arrival_bin(xs[c], a.tfs, a.T) : -1;
+            const int ai = b >= 0 ? alpha_index(xs[c], b, a.alpha_by_time, a.T) : 0;
+            pk[c] = (rw[c] << 21) | (ai << 7) | (b & 0x7F);
+        }
+    }
+    // pass 1: ranks within each chunk's bins, counts per bin
+    const uint64_t lt = lanemask_lt();
+    const unsigned bit = 1u << (lane & 31);
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+        if (c < n_chunks) {  // uniform
+            const int b = pk[c] & 0x7F;
+            const bool valid = b != 0x7F;
+            if (valid) atomicOr(&msk[2 * b + (lane >> 5)], bit);
+            wave_sync();
+            uint64_t mm = 0;
+            if (valid) mm = *reinterpret_cast<const uint64_t*>(&msk[2 * b]);
+            wave_sync();
+            const int rank = __popcll(mm & lt);
+            const bool last = valid && (mm >> lane) == 1ull;
+            if (last) {
+                cur[b] += rank + 1;
+                *reinterpret_cast<uint64_t*>(&msk[2 * b]) = 0ull;
+            }
+            wave_sync();
+            pk[c] |= (rank << 14) | ((last ? 1 : 0) << 20);
+        }
+    }
+    // bin starts: lane l scans bins 4l .. 4l+3 (T <= 64: lane l < 16)
+    int v4[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * lane + i;
+        v4[i] = t < a.T ? cur[t] : 0;
+        sum += v4[i];
+    }
+    const int incl = wave_incl_scan(sum);
+    int run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * lane + i;
+        if (t < a.T) {
+            cur[t] = run;
+            bs[t] = run;
+        }
+        run += v4[i];
+    }
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (lane == 0) bs[a.T] = total;
+    wave_sync();
+    // pass 2: event (chunk c, rank) of bin b goes to cur[b] + rank
+    float al[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) al[c] = a.alpha[(pk[c] >> 7) & 0x7F];  // index 0 where no event
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+        if (c < n_chunks) {  // uniform
+            const int b = pk[c] & 0x7F;
+            const int rank = (pk[c] >> 14) & 0x3F;
+            if (b != 0x7F) {
+                const int pos = cur[b] + rank;
+                rows[pos] = ((unsigned)pk[c] >> 21) * a.rowbytes;
+                alph[pos] = __float_as_int(al[c]);
+            }
+            wave_sync();
+            if ((pk[c] >> 20) & 1) cur[b] += rank + 1;
+            wave_sync();
+        }
+    }
+    // zeroed tail: the stream reads up to 16 entries past the end
+    if (lane < kListPad) {
+        rows[total + lane] = 0;
+        alph[total + lane] = 0;
+    }
+    return total;
 }
 
 template <int NB>
@@ -956,7 +1099,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
     typedef float f4 __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) int lds_words[];
     const int wave = uniform(threadIdx.x >> 6);
-    const int E = quad_list_entries(nel_max);
+    const int E = quad_list_entries(nel_max, a.T);
     int* region = lds_words + wave * quad_wave_words(nel_max, a.T);
     int* rows = region;
     int* alph = region + E;
@@ -980,7 +1123,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)dense_build<9, NB>(m, pix, cur, kinfo, SoaList{rows, alph}, bs);
+        (void)quad_build<NB>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : 0;  // end of bin `lane`
         float carry = bias, acc = 0.0f;
@@ -1114,10 +1257,10 @@ __device__ __forceinline__ void win_setup(const MergeArgs& m, int64_t pix, WinCt
     if (m.is_fc) {
         img = (int)pix;
     } else {
-        w_out = (int)(pix % m.W_out);
-        const int64_t q = pix / m.W_out;
-        h_out = (int)(q % m.H_out);
-        img = (int)(q / m.H_out);
+        const int q = fdiv((int)pix, m.div_w);
+        w_out = (int)pix - q * m.W_out;
+        img = fdiv(q, m.div_h);
+        h_out = q - img * m.H_out;
     }
     int nk;
     if (m.is_fc) {
@@ -2229,6 +2372,9 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     m.pad_w = sh.pad_w;
     m.is_fc = sh.is_fc;
     m.rowbytes = sh.C_out * 4;
+    if (n_pix >= (INT64_C(1) << 31)) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: 2^31 output pixels or more");
+    m.div_w = make_fastdiv(sh.W_out);
+    m.div_h = make_fastdiv(sh.H_out);
     if (p.path == VDTTFS_PATH_WINDOW)
         return launch_stream_window(ctx, m, out, ev, W, wbytes, bias, theta, t_min, sh, counters, culif, p);
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
@@ -2294,6 +2440,11 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.pad_w = sh.pad_w;
     m.rowbytes = sh.C_out * 4;
     m.inv_cin = 1.0f / (float)sh.C_in;
+    if (n_pix >= (INT64_C(1) << 31)) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: 2^31 output pixels or more");
+    m.div_w = make_fastdiv(sh.W_out);
+    m.div_h = make_fastdiv(sh.H_out);
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
+    m.in_bytes = in_bytes < (INT64_C(1) << 31) ? (int)in_bytes : 0;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
     if (narrow) {
@@ -2315,7 +2466,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     if (p.path == VDTTFS_PATH_FUSED) {
         // C_out <= 64: build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
-        if (!counters && !culif) {
+        if (!counters && !culif && m.in_bytes > 0) {
             const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, m.T) * sizeof(int);
             if (nel_max <= 64)
                 hipLaunchKernelGGL(k_stream_quad<1>, dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds,

@@ -36,6 +36,26 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Division of 0 <= n < 2^31 by a fixed divisor d >= 1 with a precomputed
+// multiplier (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994, the round-up method): l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (umulhi(n, m) + n) >> l (the
+// sum stays below 2^32 because n < 2^31).  Wave-uniform n keeps it in
+// scalar instructions.
+struct FastDiv {
+    unsigned m;
+    int l, d;
+};
+inline FastDiv make_fastdiv(int d) {
+    FastDiv f{0u, 0, d};
+    while ((1ll << f.l) < (long long)d) ++f.l;
+    f.m = (unsigned)((((unsigned long long)1 << 32) * ((1ull << f.l) - (unsigned long long)d)) / (unsigned)d + 1);
+    return f;
+}
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+    return (int)((__umulhi((unsigned)n, f.m) + (unsigned)n) >> f.l);
+}
+
 // Arrival bin of a spike (T1V:58-59 / T2V:59-60): -1 if no spike or outside
 // the window.
 __device__ __forceinline__ int arrival_bin(float t, float tfs, int T) {
