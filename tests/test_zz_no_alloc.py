@@ -2,8 +2,9 @@
 library's static per-GPU scratch must give exactly what vdttfs_layer_forward
 (context scratch grown with hipMalloc) gives, on two calls in a row -- the
 second with a smaller input, so stale scratch from the first call cannot
-leak into it -- on every list path (fused, dense, bins, narrow, register,
-FC), and reject a layer whose scratch exceeds the buffer."""
+leak into it -- on every list path (fused with one or two events per load,
+dense, bins, narrow, register, FC), and reject a layer whose scratch exceeds
+the buffer."""
 import sys
 import zlib
 
@@ -19,7 +20,8 @@ INF = np.float32(9999.0)
 # name, task2, is_fc, (B, B2), H, W, C_in, C_out, K
 CASES = [
     ("fused 32->64 3x3", True, False, (5, 2), 12, 12, 32, 64, 3),
-    ("dense 16->128 3x3", True, False, (4, 3), 16, 16, 16, 128, 3),
+    ("fused pair 16->128 3x3", True, False, (4, 3), 16, 16, 16, 128, 3),
+    ("dense 24->256 3x3", True, False, (3, 2), 8, 8, 24, 256, 3),
     ("bins 130->256 3x3", True, False, (3, 1), 8, 8, 130, 256, 3),
     ("narrow 6->16 5x5 valid", False, False, (40, 7), 12, 12, 6, 16, 5),
     ("register 1->6 5x5 valid", False, False, (50, 9), 28, 28, 1, 6, 5),
@@ -80,12 +82,13 @@ def test_noalloc_matches_layer_forward(gpu_ctx_factory, case):
 
 
 def test_noalloc_rejects_oversized_layer(gpu_ctx_factory):
-    """A 64->128 conv at 64x32x32 needs ~320 MB of merged lists: refused with
-    VDTTFS_E_UNSUPPORTED before any launch, the output left untouched."""
+    """A 128->128 conv at 64x32x32 (bins path) needs ~0.7 GB of bucketize
+    output and merged lists: refused with VDTTFS_E_UNSUPPORTED before any
+    launch, the output left untouched."""
     say("noalloc oversized layer")
     tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
     ctx = gpu_ctx_factory(tc)
-    B, H, W, C_in, C_out = 64, 32, 32, 64, 128
+    B, H, W, C_in, C_out = 64, 32, 32, 128, 128
     d_in = ctx.empty(B * H * W * C_in).fill(0)
     d_out = ctx.empty(B * H * W * C_out).fill(0x7F)
     d_W, d_b = ctx.empty(9 * C_in * C_out).fill(0), ctx.empty(C_out).fill(0)

@@ -114,6 +114,10 @@ struct LaunchPlan {
 constexpr int kMaxPixPerWave = 8;
 // The plan's lists come from the bin-layout bucketize (the bins and window paths).
 inline bool plan_bins(const LaunchPlan& p) { return p.path == VDTTFS_PATH_BINS || p.path == VDTTFS_PATH_WINDOW; }
+// Whether a layer integrated under resolved plan p builds its merged lists in
+// LDS (so it needs no merged-list scratch), with or without counters and the
+// CuLIF neuron.
+bool plan_lds_list(const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif);
 // Fills every field of *out: a requested field is checked against the
 // layer's shape (VDTTFS_E_UNSUPPORTED when the kernels cannot run it), a zero
 // field takes the built-in choice.

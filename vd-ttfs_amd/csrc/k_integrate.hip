@@ -1092,9 +1092,12 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     return total;
 }
 
-template <int NB>
+template <int GEO, int NB>
 __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
                                                      const float* __restrict__ theta, int nel_max) {
+    static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
+    constexpr int OWN = 4 / GEO;  // c_out per lane
+    constexpr int LPG = 8 / GEO;  // loads per group of 8 events
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
     typedef float f4 __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) int lds_words[];
@@ -1107,9 +1110,12 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
     int* cur = bs + a.T + 1;
     int* kinfo = cur + a.T;
     const int lane = lane_id();
-    const int q = lane >> 4, r = lane & 15;
-    const int co = 4 * r + q;  // the c_out this lane integrates
-    const bool ok = co < a.C_out;
+    // GEO 4: lane (q, r) = (lane / 16, lane % 16) loads c_out 4r..4r+3 of
+    // event q and owns c_out 4r+q; GEO 2: lane (q, r) = (lane / 32, lane % 32)
+    // loads c_out 4r..4r+3 of event q and owns c_out 4r+2q, 4r+2q+1
+    const int q = GEO == 4 ? lane >> 4 : lane >> 5;
+    const int r = GEO == 4 ? (lane & 15) : (lane & 31);
+    const int co = GEO == 4 ? 4 * r + q : 4 * r + 2 * q;  // first c_out of the lane
     const int voff = 16 * r;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
@@ -1118,7 +1124,13 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
     // theta[d] >= 1e-5), else NaN, which no carry compares >= to
     const float th_d = lane < T ? theta[lane] : 0.0f;
     const float v_th = (lane < T && lane >= a.t_min && th_d >= 1e-5f) ? th_d : __builtin_nanf("");
-    const float bias = ok ? a.bias[co] : 0.0f;
+    bool ok[OWN];
+    float bias[OWN];
+#pragma unroll
+    for (int v = 0; v < OWN; ++v) {
+        ok[v] = co + v < a.C_out;
+        bias[v] = ok[v] ? a.bias[co + v] : 0.0f;
+    }
     const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.ppw;
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
@@ -1126,76 +1138,106 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         (void)quad_build<NB>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : 0;  // end of bin `lane`
-        float carry = bias, acc = 0.0f;
-        int res = -1;  // spike bin, -1: none yet
-        uint64_t alive = __ballot(ok);
+        float carry[OWN], acc[OWN];
+        int res[OWN];  // spike bin, -1: none yet
+        uint64_t alive[OWN];
+#pragma unroll
+        for (int v = 0; v < OWN; ++v) {
+            carry[v] = bias[v];
+            acc[v] = 0.0f;
+            res[v] = -1;
+            alive[v] = __ballot(ok[v]);
+        }
         int b = 0;
         int bend = __builtin_amdgcn_readlane(v_end, 0);
         struct Raw {
-            u4 x[2];
+            u4 x[LPG];
             f4 al[2];
         };
         auto load = [&](int j, Raw& g) {
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int row = rows[j + 4 * k + q];
+            for (int k = 0; k < LPG; ++k) {
+                const int row = rows[j + GEO * k + q];
                 g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, row + voff, 0, 0);
-                g.al[k] = *reinterpret_cast<const f4*>(alph + j + 4 * k);
             }
+            g.al[0] = *reinterpret_cast<const f4*>(alph + j);
+            g.al[1] = *reinterpret_cast<const f4*>(alph + j + 4);
         };
         // close bin b and the empty bins after it that end by position p (bin
         // ends do not decrease, so they are the first `stop` bins); true when
         // the stream is over
         auto close_to = [&](int p) -> bool {
-            carry = carry + acc;
-            acc = 0.0f;
+#pragma unroll
+            for (int v = 0; v < OWN; ++v) {
+                carry[v] = carry[v] + acc[v];
+                acc[v] = 0.0f;
+            }
             const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
             do {
                 const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
-                const uint64_t f = __ballot(carry >= th) & alive;
-                res = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res;
-                alive &= ~f;
+#pragma unroll
+                for (int v = 0; v < OWN; ++v) {
+                    const uint64_t f = __ballot(carry[v] >= th) & alive[v];
+                    res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                    alive[v] &= ~f;
+                }
             } while (++b < stop);
-            if (b >= T || alive == 0) return true;
+            uint64_t any = alive[0];
+#pragma unroll
+            for (int v = 1; v < OWN; ++v) any |= alive[v];
+            if (b >= T || any == 0) return true;
             bend = __builtin_amdgcn_readlane(v_end, b);
             return false;
         };
         // integrates positions j .. j+7; true when the stream is over
         auto consume = [&](int j, Raw& g) -> bool {
-            float w[8], al[8];
+            float w[8][OWN], al[8];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            for (int k = 0; k < LPG; ++k) {
                 unsigned c0 = g.x[k].x, c1 = g.x[k].y, c2 = g.x[k].z, c3 = g.x[k].w;
+                // permlane32_swap(x, y): x's lanes 32..63 <-> y's lanes 0..31
                 auto p = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
                 c0 = p[0];
                 c2 = p[1];
                 p = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
                 c1 = p[0];
                 c3 = p[1];
-                p = __builtin_amdgcn_permlane16_swap(c0, c1, false, false);
-                c0 = p[0];
-                c1 = p[1];
-                p = __builtin_amdgcn_permlane16_swap(c2, c3, false, false);
-                c2 = p[0];
-                c3 = p[1];
-                w[4 * k + 0] = __uint_as_float(c0);
-                w[4 * k + 1] = __uint_as_float(c1);
-                w[4 * k + 2] = __uint_as_float(c2);
-                w[4 * k + 3] = __uint_as_float(c3);
-                al[4 * k + 0] = g.al[k].x;
-                al[4 * k + 1] = g.al[k].y;
-                al[4 * k + 2] = g.al[k].z;
-                al[4 * k + 3] = g.al[k].w;
+                if constexpr (GEO == 4) {
+                    // permlane16_swap(x, y): x's lanes 16..31, 48..63 <-> y's 0..15, 32..47
+                    p = __builtin_amdgcn_permlane16_swap(c0, c1, false, false);
+                    c0 = p[0];
+                    c1 = p[1];
+                    p = __builtin_amdgcn_permlane16_swap(c2, c3, false, false);
+                    c2 = p[0];
+                    c3 = p[1];
+                    w[4 * k + 0][0] = __uint_as_float(c0);
+                    w[4 * k + 1][0] = __uint_as_float(c1);
+                    w[4 * k + 2][0] = __uint_as_float(c2);
+                    w[4 * k + 3][0] = __uint_as_float(c3);
+                } else {
+                    w[2 * k + 0][0] = __uint_as_float(c0);
+                    w[2 * k + 0][OWN - 1] = __uint_as_float(c1);
+                    w[2 * k + 1][0] = __uint_as_float(c2);
+                    w[2 * k + 1][OWN - 1] = __uint_as_float(c3);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                al[i] = g.al[0][i];
+                al[4 + i] = g.al[1][i];
             }
             if (bend >= j + 8) {  // all eight in the open bin
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(w[i], al[i], acc);
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int v = 0; v < OWN; ++v) acc[v] = __builtin_fmaf(w[i][v], al[i], acc[v]);
                 return false;
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (bend <= j + i && close_to(j + i)) return true;
-                acc = __builtin_fmaf(w[i], al[i], acc);
+#pragma unroll
+                for (int v = 0; v < OWN; ++v) acc[v] = __builtin_fmaf(w[i][v], al[i], acc[v]);
             }
             return false;
         };
@@ -1210,7 +1252,9 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
             __builtin_amdgcn_sched_barrier(0);
             if (consume(j + 8, g1)) break;
         }
-        if (ok) out[pix * a.C_out + co] = res >= 0 ? (float)res : kInfTime;
+#pragma unroll
+        for (int v = 0; v < OWN; ++v)
+            if (ok[v]) out[pix * a.C_out + co + v] = res[v] >= 0 ? (float)res[v] : kInfTime;
         wave_sync();  // this pixel's list reads precede the next pixel's build
     }
 }
@@ -2121,12 +2165,29 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
     return !sh.is_fc && shape_ok && ctx->c.T <= kDenseMaxBins && sh.C_in <= kDenseMaxCin;
 }
 
+bool plan_lds_list(const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif) {
+    if (p.path == VDTTFS_PATH_WINDOW) return true;
+    if (p.path == VDTTFS_PATH_REG) return !counters && !culif;
+    if (p.path != VDTTFS_PATH_FUSED) return false;
+    // two events per load: k_stream_quad only (no counters, the LUT neuron,
+    // 32-bit input offsets); otherwise k_merge_dense + k_stream
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
+    return p.gather != 2 || (!counters && !culif && in_bytes < (INT64_C(1) << 31));
+}
+
 namespace {
 
+// The fused path: one c_out per lane up to 64 c_out (k_stream_quad, or
+// k_stream_dense for counting and CuLIF forwards), or two events per load
+// up to 128 (k_stream_quad; counting and CuLIF forwards of such a layer
+// take k_merge_dense + k_stream, as the dense path).
 bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     const int nel_max = sh.K_h * sh.K_w * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, ctx->c.T) * sizeof(int);
-    return gather == 1 && sh.C_out <= 64 && ctx->c.T <= kBlockBins && lds <= kFusedMaxLds;
+    const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, ctx->c.T) * sizeof(int);
+    if (ctx->c.T > kBlockBins) return false;
+    if (gather == 1) return sh.C_out <= 64 && lds <= kFusedMaxLds;
+    return gather == 2 && sh.C_out <= 128 && sh.C_out % 4 == 0 && qlds <= kFusedMaxLds;
 }
 
 // k_stream_window's limits: one bin block, the per-pixel tables of <= 9 columns
@@ -2413,8 +2474,9 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int nk_max = sh.K_h * sh.K_w;
     const int64_t n_pix = n_pixels(sh);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
-    // the fused kernel keeps its lists in LDS; the others need the scratch
-    if (p.path != VDTTFS_PATH_FUSED && (!list || !bstart || list_cap < cap))
+    // the fused kernels keep their lists in LDS; the others need the scratch
+    const bool lds_list = plan_lds_list(sh, p, counters != nullptr, culif != nullptr);
+    if (!lds_list && (!list || !bstart || list_cap < cap))
         return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
     DenseMergeArgs m{};
     m.list = list;
@@ -2463,17 +2525,26 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
                                      counters, culif, p, &vec, &epi);
     const int nel_max = nk_max * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
-    if (p.path == VDTTFS_PATH_FUSED) {
-        // C_out <= 64: build the list in LDS and stream it there
+    if (p.path == VDTTFS_PATH_FUSED && lds_list) {
+        // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
         if (!counters && !culif && m.in_bytes > 0) {
             const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, m.T) * sizeof(int);
-            if (nel_max <= 64)
-                hipLaunchKernelGGL(k_stream_quad<1>, dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds,
-                                   ctx->stream, m, a, out, theta, nel_max);
-            else
-                hipLaunchKernelGGL(k_stream_quad<9>, dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds,
-                                   ctx->stream, m, a, out, theta, nel_max);
+#define VD_LAUNCH_QUAD(G, NB)                                                                           \
+    hipLaunchKernelGGL((k_stream_quad<G, NB>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds, \
+                       ctx->stream, m, a, out, theta, nel_max)
+            if (epi == 2) {
+                if (nel_max <= 64)
+                    VD_LAUNCH_QUAD(2, 1);
+                else
+                    VD_LAUNCH_QUAD(2, 9);
+            } else {
+                if (nel_max <= 64)
+                    VD_LAUNCH_QUAD(4, 1);
+                else
+                    VD_LAUNCH_QUAD(4, 9);
+            }
+#undef VD_LAUNCH_QUAD
             VD_HIP(hipGetLastError());
             return VDTTFS_OK;
         }
