@@ -836,6 +836,148 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     }
 }
 
+// k_stream_lean: k_stream for the LUT-threshold neuron without counters and
+// T <= 64, with k_stream_quad's bin closing: the wave's live neurons are SGPR
+// lane masks (one per c_out a lane owns), a bin where no spike may occur has
+// a NaN threshold, so a bin closes with one compare, one v_cndmask and two
+// mask operations per owned c_out, and a run of empty bins up to the next
+// event costs one ballot to find.  GEO 4: four c_out per lane (256 per wave),
+// one event per dwordx4 load with the row in soffset; GEO 2: the pair gather
+// (128 c_out per wave, two events per load, permlane32 exchange).  The list
+// is read through the scalar cache a group of 8 events ahead.
+template <int GEO>
+__global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __restrict__ out,
+                                                     const int2* __restrict__ list,
+                                                     const int32_t* __restrict__ bstart,
+                                                     const float* __restrict__ theta) {
+    static_assert(GEO == 4 || GEO == 2, "four c_out per lane or the pair gather");
+    constexpr int OWN = GEO == 4 ? 4 : 2;  // c_out per lane
+    constexpr int LPG = GEO == 4 ? 8 : 4;  // loads per group of 8 events
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const int wave = uniform(threadIdx.x >> 6);
+    int cb;
+    int64_t pg;
+    map_block(a.n_cblk, cb, pg);
+    const int lane = lane_id();
+    const int h = lane >> 5;  // GEO 2: which event of a load this lane fetches
+    const int hmask = -h;
+    const int co = GEO == 4 ? 256 * cb + 4 * lane : 128 * cb + 4 * (lane & 31) + 2 * h;
+    const int voff = GEO == 4 ? co * 4 : 16 * (lane & 31) + 512 * cb;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    const int T = a.T;
+    const float th_d = lane < T ? theta[lane] : 0.0f;
+    const float v_th = (lane < T && lane >= a.t_min && th_d >= 1e-5f) ? th_d : __builtin_nanf("");
+    bool ok[OWN];
+    float bias[OWN];
+#pragma unroll
+    for (int v = 0; v < OWN; ++v) {
+        ok[v] = co + v < a.C_out;
+        bias[v] = ok[v] ? a.bias[co + v] : 0.0f;
+    }
+    const int vsafe = GEO == 4 && !ok[0] ? 0 : voff;  // C_out is a multiple of 4
+    const int64_t pix0 = (pg * 4 + wave) * a.ppw;
+    for (int pq = 0; pq < a.ppw; ++pq) {
+        const int64_t pix = pix0 + pq;
+        if (pix >= a.n_pix) return;  // uniform per wave
+        const int2* L = list + pix * a.cap;
+        const int32_t* BS = bstart + pix * (int64_t)(T + 1);
+        const int v_end = lane < T ? BS[lane + 1] : 0;  // end of bin `lane`
+        float carry[OWN], acc[OWN];
+        int res[OWN];
+        uint64_t alive[OWN];
+#pragma unroll
+        for (int v = 0; v < OWN; ++v) {
+            carry[v] = bias[v];
+            acc[v] = 0.0f;
+            res[v] = -1;
+            alive[v] = __ballot(ok[v]);
+        }
+        int b = 0;
+        int bend = __builtin_amdgcn_readlane(v_end, 0);
+        auto close_to = [&](int p) -> bool {
+#pragma unroll
+            for (int v = 0; v < OWN; ++v) {
+                carry[v] = carry[v] + acc[v];
+                acc[v] = 0.0f;
+            }
+            const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
+            do {
+                const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+#pragma unroll
+                for (int v = 0; v < OWN; ++v) {
+                    const uint64_t f = __ballot(carry[v] >= th) & alive[v];
+                    res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                    alive[v] &= ~f;
+                }
+            } while (++b < stop);
+            uint64_t any = alive[0];
+#pragma unroll
+            for (int v = 1; v < OWN; ++v) any |= alive[v];
+            if (b >= T || any == 0) return true;
+            bend = __builtin_amdgcn_readlane(v_end, b);
+            return false;
+        };
+        ScalarList lr;
+        lr.start(L, 0, a);
+        for (int j = 0;; j += 8) {
+            const Group8 e = lr.take(j);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) asm volatile("" ::"s"(e.v[g].x), "s"(e.v[g].y));
+            float w[8][OWN];
+#pragma unroll
+            for (int k = 0; k < LPG; ++k) {
+                if constexpr (GEO == 4) {
+                    const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, vsafe, e.v[k].x, 0);
+                    w[k][0] = __uint_as_float(x.x);
+                    w[k][1 % OWN] = __uint_as_float(x.y);
+                    w[k][2 % OWN] = __uint_as_float(x.z);
+                    w[k][3 % OWN] = __uint_as_float(x.w);
+                } else {
+                    // lower half: event 2k's row, upper half: 2k+1's (a mask,
+                    // not a select, keeps the entries in SGPRs)
+                    const int d = e.v[2 * k + 1].x - e.v[2 * k].x;
+                    const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, e.v[2 * k].x + (d & hmask) + voff, 0, 0);
+                    unsigned c0 = x.x, c1 = x.y, c2 = x.z, c3 = x.w;
+                    auto p = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
+                    c0 = p[0];
+                    c2 = p[1];
+                    p = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
+                    c1 = p[0];
+                    c3 = p[1];
+                    w[2 * k][0] = __uint_as_float(c0);
+                    w[2 * k][1 % OWN] = __uint_as_float(c1);
+                    w[2 * k + 1][0] = __uint_as_float(c2);
+                    w[2 * k + 1][1 % OWN] = __uint_as_float(c3);
+                }
+            }
+            // integrates positions j .. j+7; true when the stream is over
+            auto consume = [&]() -> bool {
+                if (bend >= j + 8) {  // all eight in the open bin
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+#pragma unroll
+                        for (int v = 0; v < OWN; ++v)
+                            acc[v] = __builtin_fmaf(w[i][v], __int_as_float(e.v[i].y), acc[v]);
+                    return false;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (bend <= j + i && close_to(j + i)) return true;
+#pragma unroll
+                    for (int v = 0; v < OWN; ++v)
+                        acc[v] = __builtin_fmaf(w[i][v], __int_as_float(e.v[i].y), acc[v]);
+                }
+                return false;
+            };
+            if (consume()) break;
+        }
+#pragma unroll
+        for (int v = 0; v < OWN; ++v)
+            if (ok[v]) out[pix * a.C_out + co + v] = res[v] >= 0 ? (float)res[v] : kInfTime;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // k_stream_dense: k_merge_dense and k_stream fused for layers whose pixel is
 // one wave of dword gathers (C_out <= 64) and T <= 64.  Each wave builds its
@@ -2052,7 +2194,14 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
         else                                  \
             VD_LAUNCH_STREAM(C, 1, L, 1);     \
     } while (0)
-    if (culif) {
+    if (!culif && !counters && a.T <= kBlockBins && (epi == 2 || vec == 4)) {
+        if (epi == 2)
+            hipLaunchKernelGGL(k_stream_lean<2>, dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, a, out,
+                               list, bstart, theta);
+        else
+            hipLaunchKernelGGL(k_stream_lean<4>, dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, a, out,
+                               list, bstart, theta);
+    } else if (culif) {
         if (counters)
             VD_LAUNCH_STREAM_V(true, true);
         else
