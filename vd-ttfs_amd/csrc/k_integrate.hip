@@ -2521,7 +2521,7 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     const bool fused = dense && fused_ok(ctx, sh, p.gather);
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
-        return plan_error(sh, "fused path needs the dense limits, C_out <= 64, T <= 64 and gather 1");
+        return plan_error(sh, "fused path needs the dense limits, T <= 64 and gather 1 (C_out <= 64) or 2 (C_out <= 128)");
     if (req.path == VDTTFS_PATH_WINDOW && !window_ok(ctx, sh))
         return plan_error(sh, "window path needs T <= 64 and at most 9 taps (or an FC layer)");
     p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
@@ -2531,7 +2531,12 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         const int64_t n_pix = n_pixels(sh);
         p.ppw = n_pix >= (INT64_C(1) << 20) ? 2 : 1;
         if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED && p.path != VDTTFS_PATH_WINDOW) {
-            // k_stream's residency (the fused and window kernels' is LDS-bound)
+            // k_stream's residency (the fused and window kernels' is LDS-bound).
+            // The rule keeps k_stream's figures (six waves per SIMD at four
+            // c_out per lane) where the timed forward runs k_stream_lean
+            // (eight): with k_stream_lean's own, VGG-16's 8x8 layers would
+            // take two pixels per wave and its 4x4 layers one, and both lose
+            // (0.447 -> 0.478 and 0.349 -> 0.415 ms).
             const int vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
             const int64_t n_cblk = p.gather == 2 ? (sh.C_out + 127) / 128 : (sh.C_out + 64 * vec - 1) / (64 * vec);
             const int64_t cap = stream_wave_capacity(ctx, p.gather);
