@@ -314,7 +314,10 @@ def work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr):
                 l.C_out, 1 if fc else l.K_h, 1 if fc else l.K_w, ph, pw, fc, tfs, T)
             ms = float(layer_ms[i])
             path, gather, ppw = net.get_plan(i)
-            roof = roofs[1] if gather == 1 else roofs[4]
+            # dword gathers: one c_out per lane outside the fused path (k_stream,
+            # k_stream_narrow, k_conv_small); the fused path (k_stream_quad)
+            # and gathers 2 and 4 load dwordx4
+            roof = roofs[1] if gather == 1 and path != 3 else roofs[4]
             gb = 4.0 * float(ebin[i])
             row = {"layer": i, "kind": "fc" if fc else "conv",
                    "shape": f"{l.C_in}->{l.C_out} @ {l.H_in}x{l.W_in}" + ("" if fc else f", {l.K_h}x{l.K_w}"),
@@ -521,13 +524,15 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": hbm / HBM_PEAK_GBS if tr else None,
             "traffic": tr["per_step"] / tr["launches"] if tr else None,
-            "kernel": "integrator = one layer's list build + stream: k_stream_dense (conv, C_in <= 64, "
-                      "32 <= C_out <= 64: list built in LDS), k_merge_dense + k_stream (other conv, "
-                      "C_in <= 64) or k_bucketize + k_merge + k_stream (wider conv, FC); layers with C_out < 32 "
-                      "stream with k_stream_narrow, or with k_conv_small when the receptive field has <= 32 "
-                      "elements.  A launch is one layer's integrate; achieved = rocprofv3 FETCH_SIZE + "
-                      "WRITE_SIZE bytes of the integrator dispatches of one forward / the live HIP-event "
-                      "integrator time of a forward",
+            "kernel": "integrator = one layer's list build + stream: k_stream_quad (conv, C_in <= 64, "
+                      "32 <= C_out <= 128: merged list built in LDS, four events per dwordx4 load up to 64 "
+                      "c_out, two up to 128), k_merge_dense + k_stream_lean (other conv, C_in <= 64) or "
+                      "k_bucketize + k_merge + k_stream_lean (wider conv; FC) with pair or four-c_out-per-lane "
+                      "dwordx4 gathers (k_stream for one c_out per lane); layers with C_out < 32 stream with "
+                      "k_stream_narrow, or with k_conv_small when the receptive field has <= 32 elements.  A "
+                      "launch is one layer's integrate; achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE bytes of "
+                      "the integrator dispatches of one forward / the live HIP-event integrator time of a "
+                      "forward",
             "traffic_per_step": tr["per_step"] if tr else None,
             "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
                                f"no counter summary for {key} in profiles/"),
@@ -546,8 +551,8 @@ def bench_ttfs(args) -> int:
                 "frac": t_roof / integ_s,
                 "model": "4 B per integrated synapse under the per-bin exit the kernels run (E_bin); roof = "
                          "vdttfs_probe_gather with weights in one XCD's L2, dword rows for layers gathering one "
-                         "c_out per lane, dwordx4 rows for the others; frac = (time at each layer's roof) / "
-                         "(integrator time)",
+                         "c_out per lane outside the fused path, dwordx4 rows for the others; frac = (time at "
+                         "each layer's roof) / (integrator time)",
                 "probe": roofs,
             },
         },
