@@ -836,8 +836,9 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
     }
 }
 
-// k_stream_lean: k_stream for the LUT-threshold neuron without counters and
-// T <= 64, with k_stream_quad's bin closing: the wave's live neurons are SGPR
+// k_stream_lean: k_stream without counters and T <= 64 (the LUT-threshold
+// neuron, or the CuLIF neuron, which steps every bin, empty ones with an
+// input of 0), with k_stream_quad's bin closing: the wave's live neurons are SGPR
 // lane masks (one per c_out a lane owns), a bin where no spike may occur has
 // a NaN threshold, so a bin closes with one compare, one v_cndmask and two
 // mask operations per owned c_out, and a run of empty bins up to the next
@@ -845,7 +846,7 @@ __global__ __launch_bounds__(256) void k_stream(StreamArgs a, float* __restrict_
 // one event per dwordx4 load with the row in soffset; GEO 2: the pair gather
 // (128 c_out per wave, two events per load, permlane32 exchange).  The list
 // is read through the scalar cache a group of 8 events ahead.
-template <int GEO>
+template <int GEO, bool CULIF>
 __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __restrict__ out,
                                                      const int2* __restrict__ list,
                                                      const int32_t* __restrict__ bstart,
@@ -873,7 +874,7 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
 #pragma unroll
     for (int v = 0; v < OWN; ++v) {
         ok[v] = co + v < a.C_out;
-        bias[v] = ok[v] ? a.bias[co + v] : 0.0f;
+        bias[v] = (ok[v] && !CULIF) ? a.bias[co + v] : 0.0f;  // the CuLIF neuron starts at V = 0
     }
     const int vsafe = GEO == 4 && !ok[0] ? 0 : voff;  // C_out is a multiple of 4
     const int64_t pix0 = (pg * 4 + wave) * a.ppw;
@@ -883,32 +884,49 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
         const int2* L = list + pix * a.cap;
         const int32_t* BS = bstart + pix * (int64_t)(T + 1);
         const int v_end = lane < T ? BS[lane + 1] : 0;  // end of bin `lane`
-        float carry[OWN], acc[OWN];
+        float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
         int res[OWN];
         uint64_t alive[OWN];
 #pragma unroll
         for (int v = 0; v < OWN; ++v) {
             carry[v] = bias[v];
             acc[v] = 0.0f;
+            cur[v] = 0.0f;
             res[v] = -1;
             alive[v] = __ballot(ok[v]);
         }
         int b = 0;
         int bend = __builtin_amdgcn_readlane(v_end, 0);
         auto close_to = [&](int p) -> bool {
+            if constexpr (!CULIF) {
 #pragma unroll
-            for (int v = 0; v < OWN; ++v) {
-                carry[v] = carry[v] + acc[v];
-                acc[v] = 0.0f;
+                for (int v = 0; v < OWN; ++v) {
+                    carry[v] = carry[v] + acc[v];
+                    acc[v] = 0.0f;
+                }
             }
             const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
             do {
-                const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+                if constexpr (CULIF) {
+                    // I = fma(I, decay, in_b); V += I; fire at V >= th (T3V:50-62);
+                    // every bin steps the neuron, empty ones with in_b = 0
 #pragma unroll
-                for (int v = 0; v < OWN; ++v) {
-                    const uint64_t f = __ballot(carry[v] >= th) & alive[v];
-                    res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                    alive[v] &= ~f;
+                    for (int v = 0; v < OWN; ++v) {
+                        cur[v] = __builtin_fmaf(cur[v], a.decay, acc[v]);
+                        acc[v] = 0.0f;
+                        carry[v] = carry[v] + cur[v];
+                        const uint64_t f = __ballot(carry[v] >= a.th) & alive[v];
+                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                        alive[v] &= ~f;
+                    }
+                } else {
+                    const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+#pragma unroll
+                    for (int v = 0; v < OWN; ++v) {
+                        const uint64_t f = __ballot(carry[v] >= th) & alive[v];
+                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                        alive[v] &= ~f;
+                    }
                 }
             } while (++b < stop);
             uint64_t any = alive[0];
@@ -1054,9 +1072,10 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
 }
 
 // ---------------------------------------------------------------------------
-// k_stream_quad: the fused dense path for the LUT-threshold neuron without
-// counters (C_out <= 64, T <= 64), built for the fewest instructions per
-// event and per bin; k_stream_dense serves the counting and CuLIF forms.
+// k_stream_quad: the fused dense path without counters (C_out <= 128,
+// T <= 64), built for the fewest instructions per event and per bin, for
+// the LUT-threshold neuron or (CULIF) the CuLIF neuron; counting forwards
+// take k_stream_dense (C_out <= 64) or k_merge_dense + k_stream.
 //
 // Gathers: one dwordx4 load fetches four events at once -- lane (q, r)
 // (q = lane / 16, r = lane % 16) loads c_out 4r .. 4r+3 of event q's row --
@@ -1234,7 +1253,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     return total;
 }
 
-template <int GEO, int NB>
+template <int GEO, int NB, bool CULIF>
 __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
                                                      const float* __restrict__ theta, int nel_max) {
     static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
@@ -1271,7 +1290,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
 #pragma unroll
     for (int v = 0; v < OWN; ++v) {
         ok[v] = co + v < a.C_out;
-        bias[v] = ok[v] ? a.bias[co + v] : 0.0f;
+        bias[v] = (ok[v] && !CULIF) ? a.bias[co + v] : 0.0f;  // the CuLIF neuron starts at V = 0
     }
     const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.ppw;
     for (int pq = 0; pq < a.ppw; ++pq) {
@@ -1280,13 +1299,14 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         (void)quad_build<NB>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : 0;  // end of bin `lane`
-        float carry[OWN], acc[OWN];
+        float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
         int res[OWN];  // spike bin, -1: none yet
         uint64_t alive[OWN];
 #pragma unroll
         for (int v = 0; v < OWN; ++v) {
             carry[v] = bias[v];
             acc[v] = 0.0f;
+            cur[v] = 0.0f;
             res[v] = -1;
             alive[v] = __ballot(ok[v]);
         }
@@ -1309,19 +1329,35 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         // ends do not decrease, so they are the first `stop` bins); true when
         // the stream is over
         auto close_to = [&](int p) -> bool {
+            if constexpr (!CULIF) {
 #pragma unroll
-            for (int v = 0; v < OWN; ++v) {
-                carry[v] = carry[v] + acc[v];
-                acc[v] = 0.0f;
+                for (int v = 0; v < OWN; ++v) {
+                    carry[v] = carry[v] + acc[v];
+                    acc[v] = 0.0f;
+                }
             }
             const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
             do {
-                const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+                if constexpr (CULIF) {
+                    // I = fma(I, decay, in_b); V += I; fire at V >= th (T3V:50-62);
+                    // every bin steps the neuron, empty ones with in_b = 0
 #pragma unroll
-                for (int v = 0; v < OWN; ++v) {
-                    const uint64_t f = __ballot(carry[v] >= th) & alive[v];
-                    res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                    alive[v] &= ~f;
+                    for (int v = 0; v < OWN; ++v) {
+                        cur[v] = __builtin_fmaf(cur[v], a.decay, acc[v]);
+                        acc[v] = 0.0f;
+                        carry[v] = carry[v] + cur[v];
+                        const uint64_t f = __ballot(carry[v] >= a.th) & alive[v];
+                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                        alive[v] &= ~f;
+                    }
+                } else {
+                    const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+#pragma unroll
+                    for (int v = 0; v < OWN; ++v) {
+                        const uint64_t f = __ballot(carry[v] >= th) & alive[v];
+                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
+                        alive[v] &= ~f;
+                    }
                 }
             } while (++b < stop);
             uint64_t any = alive[0];
@@ -2194,13 +2230,21 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
         else                                  \
             VD_LAUNCH_STREAM(C, 1, L, 1);     \
     } while (0)
-    if (!culif && !counters && a.T <= kBlockBins && (epi == 2 || vec == 4)) {
-        if (epi == 2)
-            hipLaunchKernelGGL(k_stream_lean<2>, dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, a, out,
-                               list, bstart, theta);
-        else
-            hipLaunchKernelGGL(k_stream_lean<4>, dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, a, out,
-                               list, bstart, theta);
+#define VD_LAUNCH_LEAN(G, L)                                                                                \
+    hipLaunchKernelGGL((k_stream_lean<G, L>), dim3((unsigned)blocks), dim3(64 * waves), 0, ctx->stream, a, out, \
+                       list, bstart, theta)
+    if (!counters && a.T <= kBlockBins && (epi == 2 || vec == 4)) {
+        if (epi == 2) {
+            if (culif)
+                VD_LAUNCH_LEAN(2, true);
+            else
+                VD_LAUNCH_LEAN(2, false);
+        } else {
+            if (culif)
+                VD_LAUNCH_LEAN(4, true);
+            else
+                VD_LAUNCH_LEAN(4, false);
+        }
     } else if (culif) {
         if (counters)
             VD_LAUNCH_STREAM_V(true, true);
@@ -2212,6 +2256,7 @@ int launch_stream(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, co
         else
             VD_LAUNCH_STREAM_V(false, false);
     }
+#undef VD_LAUNCH_LEAN
 #undef VD_LAUNCH_STREAM_V
 #undef VD_LAUNCH_STREAM
     VD_HIP(hipGetLastError());
@@ -2318,10 +2363,11 @@ bool plan_lds_list(const IntegShape& sh, const LaunchPlan& p, bool counters, boo
     if (p.path == VDTTFS_PATH_WINDOW) return true;
     if (p.path == VDTTFS_PATH_REG) return !counters && !culif;
     if (p.path != VDTTFS_PATH_FUSED) return false;
-    // two events per load: k_stream_quad only (no counters, the LUT neuron,
-    // 32-bit input offsets); otherwise k_merge_dense + k_stream
+    // two events per load: k_stream_quad only (no counters, 32-bit input
+    // offsets); otherwise k_merge_dense + k_stream
+    (void)culif;
     const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
-    return p.gather != 2 || (!counters && !culif && in_bytes < (INT64_C(1) << 31));
+    return p.gather != 2 || (!counters && in_bytes < (INT64_C(1) << 31));
 }
 
 namespace {
@@ -2682,22 +2728,30 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     if (p.path == VDTTFS_PATH_FUSED && lds_list) {
         // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
-        if (!counters && !culif && m.in_bytes > 0) {
+        if (!counters && m.in_bytes > 0) {
             const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, m.T) * sizeof(int);
-#define VD_LAUNCH_QUAD(G, NB)                                                                           \
-    hipLaunchKernelGGL((k_stream_quad<G, NB>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds, \
+#define VD_LAUNCH_QUAD(G, NB, L)                                                                           \
+    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds, \
                        ctx->stream, m, a, out, theta, nel_max)
+#define VD_LAUNCH_QUAD_NB(G, L)          \
+    do {                                 \
+        if (nel_max <= 64)               \
+            VD_LAUNCH_QUAD(G, 1, L);     \
+        else                             \
+            VD_LAUNCH_QUAD(G, 9, L);     \
+    } while (0)
             if (epi == 2) {
-                if (nel_max <= 64)
-                    VD_LAUNCH_QUAD(2, 1);
+                if (culif)
+                    VD_LAUNCH_QUAD_NB(2, true);
                 else
-                    VD_LAUNCH_QUAD(2, 9);
+                    VD_LAUNCH_QUAD_NB(2, false);
             } else {
-                if (nel_max <= 64)
-                    VD_LAUNCH_QUAD(4, 1);
+                if (culif)
+                    VD_LAUNCH_QUAD_NB(4, true);
                 else
-                    VD_LAUNCH_QUAD(4, 9);
+                    VD_LAUNCH_QUAD_NB(4, false);
             }
+#undef VD_LAUNCH_QUAD_NB
 #undef VD_LAUNCH_QUAD
             VD_HIP(hipGetLastError());
             return VDTTFS_OK;
