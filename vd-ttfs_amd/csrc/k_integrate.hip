@@ -133,41 +133,36 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
         for (int k = 0; k < KMAX; ++k) S += o[k];
         const int C0 = uniform(S);
         int A = 0, P = 0;
-        int st[KMAX], kc[KMAX];  // per column: first event of the block, run start in f order
-        int run = 0;
+        int st[KMAX], cnt[KMAX];  // per column: first event of the block, events in the block
+        int total = 0;            // events of the block
 #pragma unroll
         for (int k = 0; k < KMAX; ++k) {
             st[k] = 0;
-            kc[k] = run;
+            cnt[k] = 0;
             if (k < nk) {
                 P += o[k];
                 if (lane < nb) dtab[k * kBlockBins + lane] = A + (S - P) - C0;
                 A += on[k];
                 st[k] = __builtin_amdgcn_readlane(o[k], 0);
-                run += __builtin_amdgcn_readlane(on[k], nb - 1) - st[k];
+                cnt[k] = __builtin_amdgcn_readlane(on[k], nb - 1) - st[k];
+                total += cnt[k];
             }
         }
         if (lane < nb) bs[t0 + lane] = base + S - C0;
-        const int total = run;  // events of the block
         wave_sync();
-        for (int f0 = 0; f0 < total; f0 += 64) {
-            const int f = f0 + lane;
-            if (f < total) {
-                int k = 0, kb = 0, s0 = st[0], col = colk[0], kr = krow[0];
+        // column by column, lanes over the column's events (the column and
+        // its weight-row base stay wave-uniform)
 #pragma unroll
-                for (int kk = 1; kk < KMAX; ++kk)
-                    if (kk < nk && f >= kc[kk]) {
-                        k = kk;
-                        kb = kc[kk];
-                        s0 = st[kk];
-                        col = colk[kk];
-                        kr = krow[kk];
-                    }
-                const int i = s0 + (f - kb);
-                const vd_event e = a.ev[(int64_t)col * a.C_in + i];
-                const int pos = dtab[k * kBlockBins + (int)(e.key >> 24) - t0] + i;
-                out[base + pos] = make_int2(kr + (int)(e.key & 0xFFFFFFu) * a.rowbytes,
-                                            __float_as_int(e.alpha));
+        for (int k = 0; k < KMAX; ++k) {
+            if (k < nk) {  // uniform
+                const vd_event* evk = a.ev + (int64_t)colk[k] * a.C_in + st[k];
+                const int* dk = dtab + k * kBlockBins - t0;
+                for (int f = lane; f < cnt[k]; f += 64) {
+                    const vd_event e = evk[f];
+                    const int pos = dk[(int)(e.key >> 24)] + st[k] + f;
+                    out[base + pos] = make_int2(krow[k] + (int)(e.key & 0xFFFFFFu) * a.rowbytes,
+                                                __float_as_int(e.alpha));
+                }
             }
         }
         base += total;
