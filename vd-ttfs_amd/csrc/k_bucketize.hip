@@ -136,6 +136,123 @@ __global__ __launch_bounds__(256) void k_bucketize(
     }
 }
 
+// Long columns on a narrow grid (an FC layer's inputs: a few hundred columns
+// of thousands of inputs each) would leave most of the chip idle with one
+// wave per column walking its chunks one load at a time.  k_bucketize_wide
+// gives each column a workgroup of W waves: wave w takes a contiguous range of
+// 64-input chunks, counts it into its own LDS histogram, then wave 0 turns the
+// W histograms into the column's bucket offsets and each wave's starting
+// cursor per bucket (buckets in order, waves in order within a bucket), and
+// every wave places its chunks as k_bucketize does.  Waves hold consecutive
+// cin ranges, so the placement is the same stable (bucket, cin) order.
+// Loads are issued 8 chunks at a time.
+constexpr int kWideWaves = 8;
+constexpr int kWideBatch = 8;
+
+template <bool BINS>
+__global__ __launch_bounds__(64 * kWideWaves) void k_bucketize_wide(
+    const float* __restrict__ in, int c_in, BktParams p, int nb, int32_t* __restrict__ out_cin,
+    float* __restrict__ out_tin, vd_event* __restrict__ out_ev, const float* __restrict__ alpha,
+    int32_t* __restrict__ out_off, unsigned long long* __restrict__ n_ev_counter) {
+    extern __shared__ int lds[];
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int64_t col = blockIdx.x;
+    const int OS = nb + 1;
+    int* cur = lds + wave * OS;  // this wave's counts, then its cursors
+    const float* src = in + col * (int64_t)c_in;
+    const int n_chunks = (c_in + 63) >> 6;
+    const int per = (n_chunks + kWideWaves - 1) / kWideWaves;
+    const int c_begin = wave * per;
+    const int c_end = c_begin + per < n_chunks ? c_begin + per : n_chunks;
+    for (int i = lane; i < OS; i += 64) cur[i] = 0;
+    wave_sync();
+    // element `lane` of chunks c0 .. c0+kWideBatch-1 (past the range: no event)
+    auto load_batch = [&](int c0, float (&x)[kWideBatch]) {
+#pragma unroll
+        for (int k = 0; k < kWideBatch; ++k) {
+            const int i = (c0 + k) * 64 + lane;
+            const bool ok = c0 + k < c_end && i < c_in;
+            const float v = src[ok ? i : 0];
+            x[k] = ok ? v : kInfTime;
+        }
+    };
+    // pass 1: this wave's histogram
+    for (int c0 = c_begin; c0 < c_end; c0 += kWideBatch) {
+        float x[kWideBatch];
+        load_batch(c0, x);
+#pragma unroll
+        for (int k = 0; k < kWideBatch; ++k) {
+            const int tb = arrival_bin(x[k], p.tfs, p.T);
+            if (tb >= 0) atomicAdd(&cur[BINS ? tb : tb / p.delta], 1);
+        }
+    }
+    __syncthreads();
+    // wave 0: the column's bucket offsets; every wave's cursor per bucket
+    if (wave == 0) {
+        int run = 0;
+        for (int b0 = 0; b0 < nb; b0 += 64) {
+            const int b = b0 + lane;
+            int tot = 0;
+            if (b < nb)
+                for (int w = 0; w < kWideWaves; ++w) tot += lds[w * OS + b];
+            const int incl = wave_incl_scan(tot);
+            if (b < nb) {
+                int s = run + incl - tot;
+                out_off[col * OS + b] = s;
+                for (int w = 0; w < kWideWaves; ++w) {
+                    const int c = lds[w * OS + b];
+                    lds[w * OS + b] = s;
+                    s += c;
+                }
+            }
+            run += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) {
+            out_off[col * OS + nb] = run;
+            if (n_ev_counter != nullptr) atomicAdd(counter_stripe(n_ev_counter), (unsigned long long)run);
+        }
+    }
+    __syncthreads();
+    // pass 2: stable scatter of this wave's chunks (multisplit ranks, as k_bucketize)
+    const uint64_t lt = lanemask_lt();
+    const int nbits = nb > 1 ? 32 - __clz(nb - 1) : 0;
+    for (int c0 = c_begin; c0 < c_end; c0 += kWideBatch) {
+        float x[kWideBatch];
+        load_batch(c0, x);
+#pragma unroll
+        for (int k = 0; k < kWideBatch; ++k) {
+            if (c0 + k >= c_end) break;  // uniform
+            const int i = (c0 + k) * 64 + lane;
+            const float t = x[k];
+            const int tb = arrival_bin(t, p.tfs, p.T);
+            const int b = (tb < 0) ? -1 : (BINS ? tb : tb / p.delta);
+            const bool active = b >= 0;
+            uint64_t same = __ballot(active);
+            for (int bit = 0; bit < nbits; ++bit) {
+                const uint64_t ones = __ballot(active && ((b >> bit) & 1));
+                same &= ((b >> bit) & 1) ? ones : ~ones;
+            }
+            if (active) {
+                const int pos = cur[b] + __popcll(same & lt);
+                const int64_t dst = col * (int64_t)c_in + pos;
+                if (BINS) {
+                    vd_event e;
+                    e.key = (uint32_t)i | ((uint32_t)tb << 24);
+                    e.alpha = alpha[alpha_index(t, tb, p.alpha_by_time, p.T)];
+                    out_ev[dst] = e;
+                } else {
+                    out_cin[dst] = i;
+                    out_tin[dst] = t;
+                }
+            }
+            wave_sync();
+            if (active && (same & lt) == 0) cur[b] += __popcll(same);
+            wave_sync();
+        }
+    }
+}
+
 int seg_log2_for(int c_in) {
     int s = 0;
     while ((1 << s) < c_in && s < 6) ++s;
@@ -147,6 +264,16 @@ int launch_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
                      int32_t* out_cin, float* out_tin, vd_event* out_ev, const float* alpha,
                      int32_t* out_off, unsigned long long* n_ev_counter) {
     if (n_cols <= 0 || c_in <= 0) return VDTTFS_OK;
+    BktParams p{ctx->c.T, ctx->c.tfs, ctx->c.delta, ctx->c.alpha_by_time};
+    // few long columns: a workgroup per column (fewer columns than 2 waves per
+    // SIMD of a 256-CU device, at least 8 chunks each)
+    if (c_in >= 64 * kWideWaves && n_cols < 2048 && (size_t)kWideWaves * (nb + 1) * sizeof(int) <= 64 * 1024) {
+        hipLaunchKernelGGL(k_bucketize_wide<BINS>, dim3((unsigned)n_cols), dim3(64 * kWideWaves),
+                           (size_t)kWideWaves * (nb + 1) * sizeof(int), ctx->stream, in, c_in, p, nb, out_cin,
+                           out_tin, out_ev, alpha, out_off, n_ev_counter);
+        VD_HIP(hipGetLastError());
+        return VDTTFS_OK;
+    }
     // one segment per column; widen segments (fewer columns per wave) until
     // the wave's bucket counters fit 16 KB, so 4 waves stay within 64 KB
     int sl = seg_log2_for(c_in);
@@ -159,7 +286,6 @@ int launch_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_cols, int c_in,
     const int64_t n_waves = (n_cols + cpw - 1) / cpw;
     const int64_t blocks = (n_waves + waves - 1) / waves;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "bucketize: grid too large");
-    BktParams p{ctx->c.T, ctx->c.tfs, ctx->c.delta, ctx->c.alpha_by_time};
     hipLaunchKernelGGL(k_bucketize<BINS>, dim3((unsigned)blocks), dim3(64 * waves),
                        wave_lds * waves, ctx->stream, in, n_cols, c_in, sl, p, nb, out_cin,
                        out_tin, out_ev, alpha, out_off, n_ev_counter);
