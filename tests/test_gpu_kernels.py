@@ -58,6 +58,9 @@ BKT_CASES = [
     (16, 0.0, 5, 4096, 40),
     (255, 0.0, 1, 6, 777),
     (64, 0.0, 1, 130, 200),
+    # few long columns (a workgroup per column): ragged chunks, waves with no chunk, 255 bins
+    (64, 32.0, 8, 700, 50),
+    (255, 0.0, 1, 1000, 30),
 ]
 
 
