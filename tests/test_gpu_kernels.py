@@ -190,7 +190,9 @@ def test_integrate_paths_bitexact(gpu_ctx_factory, case):
 def test_integrate_theta_not_monotone(gpu_ctx_factory, shape):
     """Threshold tables the engine may not skip empty bins on: a shuffled
     theta (rises and falls), entries below 1e-5 and t_min > 0, next to the
-    monotone decaying table the skip relies on."""
+    monotone decaying table the skip relies on, a decaying table whose tail
+    falls below 1e-5 (spikes possible in bins t_min .. 49 only), a flat one
+    and a decaying one with a hole below 1e-5 (allowed bins not one range)."""
     say(f"integrate non-monotone theta ({shape})")
     rng = np.random.default_rng(77)
     tc = consts(64, 0.0, 8, True)
@@ -203,7 +205,13 @@ def test_integrate_theta_not_monotone(gpu_ctx_factory, shape):
     theta_mix = rng.permutation(theta_mono).astype(np.float32)
     theta_mix[5:9] = np.float32(1e-6)
     d_in, d_W, d_b, d_a = ctx.to_device(sp), ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha)
-    for theta, t_min in ((theta_mix, 3), (theta_mono, 0), (theta_mono * np.float32(0.3), 7)):
+    theta_tail = theta_mono.copy()
+    theta_tail[50:] = np.float32(1e-6)
+    theta_flat = np.full_like(theta_mono, theta_mono[20])
+    theta_hole = theta_mono.copy()
+    theta_hole[9:12] = np.float32(1e-6)
+    for theta, t_min in ((theta_mix, 3), (theta_mono, 0), (theta_mono * np.float32(0.3), 7), (theta_tail, 2),
+                         (theta_flat, 0), (theta_hole, 1)):
         exp, ep, eb = oracle_layer(tc, sp, Wt, bias, alpha, theta, n_cols, shp, t_min, is_fc)
         d_t = ctx.to_device(theta)
         d_out = ctx.empty(exp.size, np.float32)

@@ -878,16 +878,16 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
         if (pix >= a.n_pix) return;  // uniform per wave
         const int2* L = list + pix * a.cap;
         const int32_t* BS = bstart + pix * (int64_t)(T + 1);
-        const int v_end = lane < T ? BS[lane + 1] : 0;  // end of bin `lane`
+        const int v_end = lane < T ? BS[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
-        int res[OWN];
+        int res[OWN];  // bins closed with the neuron still alive: its spike bin once it fired
         uint64_t alive[OWN];
 #pragma unroll
         for (int v = 0; v < OWN; ++v) {
             carry[v] = bias[v];
             acc[v] = 0.0f;
             cur[v] = 0.0f;
-            res[v] = -1;
+            res[v] = 0;
             alive[v] = __ballot(ok[v]);
         }
         int b = 0;
@@ -900,9 +900,9 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
                     acc[v] = 0.0f;
                 }
             }
-            const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
-            do {
-                if constexpr (CULIF) {
+            const int stop = __popcll(__builtin_amdgcn_ballot_w64(v_end <= p));  // > b (lanes >= T: INT_MAX)
+            if constexpr (CULIF) {
+                do {
                     // I = fma(I, decay, in_b); V += I; fire at V >= th (T3V:50-62);
                     // every bin steps the neuron, empty ones with in_b = 0
 #pragma unroll
@@ -910,20 +910,22 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
                         cur[v] = __builtin_fmaf(cur[v], a.decay, acc[v]);
                         acc[v] = 0.0f;
                         carry[v] = carry[v] + cur[v];
-                        const uint64_t f = __ballot(carry[v] >= a.th) & alive[v];
-                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                        alive[v] &= ~f;
+                        alive[v] &= ~__ballot(carry[v] >= a.th);
+                        res[v] = add_lane_bit(res[v], alive[v]);
                     }
-                } else {
+                } while (++b < stop);
+            } else {
+                auto close_bin = [&]() {
                     const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
 #pragma unroll
                     for (int v = 0; v < OWN; ++v) {
-                        const uint64_t f = __ballot(carry[v] >= th) & alive[v];
-                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                        alive[v] &= ~f;
+                        alive[v] &= ~__ballot(carry[v] >= th);
+                        res[v] = add_lane_bit(res[v], alive[v]);
                     }
-                }
-            } while (++b < stop);
+                };
+                do close_bin();
+                while (++b < stop);
+            }
             uint64_t any = alive[0];
 #pragma unroll
             for (int v = 1; v < OWN; ++v) any |= alive[v];
@@ -987,7 +989,7 @@ __global__ __launch_bounds__(256) void k_stream_lean(StreamArgs a, float* __rest
         }
 #pragma unroll
         for (int v = 0; v < OWN; ++v)
-            if (ok[v]) out[pix * a.C_out + co + v] = res[v] >= 0 ? (float)res[v] : kInfTime;
+            if (ok[v]) out[pix * a.C_out + co + v] = __builtin_amdgcn_inverse_ballot_w64(alive[v]) ? kInfTime : (float)res[v];
     }
 }
 
@@ -1135,15 +1137,16 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
         nk = uniform(__popcll(m));
         if (v) {
             const int slot = __popcll(m & lanemask_lt());
-            kinfo[slot] = col;
+            kinfo[slot] = col * a.C_in;
             kinfo[KMAX + slot] = lane * a.C_in;
         }
     }
     unsigned* msk = reinterpret_cast<unsigned*>(rows);  // 2 words per bin during pass 1
     if (lane < a.T) {
-        cur[lane] = 0;
-        msk[2 * lane] = 0u;
-        msk[2 * lane + 1] = 0u;
+        const int z = vzero();
+        cur[lane] = z;
+        msk[2 * lane] = z;
+        msk[2 * lane + 1] = z;
     }
     wave_sync();
     const int nel = nk * a.C_in;       // <= 9 * 64
@@ -1153,7 +1156,8 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
         // element f = c * 64 + lane: tap k = f / C_in (the quotient's
         // fractional part is >= 0.5 / 64, so the float product rounds it
         // correctly), cin ci.  Every chunk's load is issued before any is
-        // used (elements past the end load the map's first word).
+        // used, with no branch (elements past the end load the map's first
+        // word; their row and tap fields are never read).
         const __amdgpu_buffer_rsrc_t rin =
             __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
         float xs[NB];
@@ -1163,17 +1167,24 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int f = c * 64 + lane;
             const bool in = f < nel;
             const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
-            const int ci = in ? f - k * a.C_in : 0;
+            const int ci = f - (int)__umul24((unsigned)k, (unsigned)a.C_in);  // k <= 8, C_in <= 64
             rw[c] = kinfo[KMAX + k] + ci;
-            const int off = in ? (kinfo[k] * a.C_in + ci) * 4 : 0;
-            xs[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, 0, 0));
+            const int off = (kinfo[k] + ci) * 4;
+            xs[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? off : 0, 0, 0));
         }
+        // arrival_bin and alpha_index without branches: bin floor(t - tfs)
+        // clamped below at 0 (floor commutes with the clamp), -1 for no
+        // spike (t >= kInfTime or NaN) or a bin past the window; the LUT
+        // index is the bin, or clamp((int)t, 0, T) by spike time
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
-            const bool in = c * 64 + lane < nel;
-            const int b = in ? arrival_bin(xs[c], a.tfs, a.T) : -1;
-            const int ai = b >= 0 ? alpha_index(xs[c], b, a.alpha_by_time, a.T) : 0;
-            pk[c] = (rw[c] << 21) | (ai << 7) | (b & 0x7F);
+            const float t = xs[c];
+            const int tb = (int)floorf(fmaxf(t - a.tfs, 0.0f));  // t < kInfTime keeps it in range
+            const bool ev = c * 64 + lane < nel && t < kInfTime && tb < a.T;
+            int ai = tb;
+            if (a.alpha_by_time) ai = (int)fminf(fmaxf(t, 0.0f), (float)a.T);
+            pk[c] = ev ? (rw[c] << 21) | (ai << 7) | tb : 0x7F;
+            __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: fewer live registers
         }
     }
     // pass 1: ranks within each chunk's bins, counts per bin
@@ -1193,7 +1204,8 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const bool last = valid && (mm >> lane) == 1ull;
             if (last) {
                 cur[b] += rank + 1;
-                *reinterpret_cast<uint64_t*>(&msk[2 * b]) = 0ull;
+                const int z = vzero();
+                *reinterpret_cast<int2*>(&msk[2 * b]) = make_int2(z, z);
             }
             wave_sync();
             pk[c] |= (rank << 14) | ((last ? 1 : 0) << 20);
@@ -1232,7 +1244,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int rank = (pk[c] >> 14) & 0x3F;
             if (b != 0x7F) {
                 const int pos = cur[b] + rank;
-                rows[pos] = ((unsigned)pk[c] >> 21) * a.rowbytes;
+                rows[pos] = (int)__umul24((unsigned)pk[c] >> 21, (unsigned)a.rowbytes);  // row < 2^11, <= 512 B
                 alph[pos] = __float_as_int(al[c]);
             }
             wave_sync();
@@ -1242,8 +1254,9 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     }
     // zeroed tail: the stream reads up to 16 entries past the end
     if (lane < kListPad) {
-        rows[total + lane] = 0;
-        alph[total + lane] = 0;
+        const int z = vzero();
+        rows[total + lane] = z;
+        alph[total + lane] = z;
     }
     return total;
 }
@@ -1293,23 +1306,26 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         if (pix >= a.n_pix) return;  // uniform per wave
         (void)quad_build<NB>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
-        const int v_end = lane < T ? bs[lane + 1] : 0;  // end of bin `lane`
+        const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
-        int res[OWN];  // spike bin, -1: none yet
+        int res[OWN];  // bins closed with the neuron still alive: its spike bin once it fired
         uint64_t alive[OWN];
 #pragma unroll
         for (int v = 0; v < OWN; ++v) {
             carry[v] = bias[v];
             acc[v] = 0.0f;
             cur[v] = 0.0f;
-            res[v] = -1;
+            res[v] = 0;
             alive[v] = __ballot(ok[v]);
         }
         int b = 0;
         int bend = __builtin_amdgcn_readlane(v_end, 0);
+        // GEO 2 reads a group's alphas when it consumes the group rather than
+        // with its loads: 8 fewer registers in flight (5 waves per SIMD, not 4)
+        constexpr bool AL_AHEAD = GEO == 4;
         struct Raw {
             u4 x[LPG];
-            f4 al[2];
+            f4 al[AL_AHEAD ? 2 : 1];
         };
         auto load = [&](int j, Raw& g) {
 #pragma unroll
@@ -1317,8 +1333,10 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
                 const int row = rows[j + GEO * k + q];
                 g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, row + voff, 0, 0);
             }
-            g.al[0] = *reinterpret_cast<const f4*>(alph + j);
-            g.al[1] = *reinterpret_cast<const f4*>(alph + j + 4);
+            if constexpr (AL_AHEAD) {
+                g.al[0] = *reinterpret_cast<const f4*>(alph + j);
+                g.al[1] = *reinterpret_cast<const f4*>(alph + j + 4);
+            }
         };
         // close bin b and the empty bins after it that end by position p (bin
         // ends do not decrease, so they are the first `stop` bins); true when
@@ -1331,9 +1349,9 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
                     acc[v] = 0.0f;
                 }
             }
-            const int stop = __popcll(__ballot(lane < T && v_end <= p));  // > b
-            do {
-                if constexpr (CULIF) {
+            const int stop = __popcll(__builtin_amdgcn_ballot_w64(v_end <= p));  // > b (lanes >= T: INT_MAX)
+            if constexpr (CULIF) {
+                do {
                     // I = fma(I, decay, in_b); V += I; fire at V >= th (T3V:50-62);
                     // every bin steps the neuron, empty ones with in_b = 0
 #pragma unroll
@@ -1341,20 +1359,22 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
                         cur[v] = __builtin_fmaf(cur[v], a.decay, acc[v]);
                         acc[v] = 0.0f;
                         carry[v] = carry[v] + cur[v];
-                        const uint64_t f = __ballot(carry[v] >= a.th) & alive[v];
-                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                        alive[v] &= ~f;
+                        alive[v] &= ~__ballot(carry[v] >= a.th);
+                        res[v] = add_lane_bit(res[v], alive[v]);
                     }
-                } else {
+                } while (++b < stop);
+            } else {
+                auto close_bin = [&]() {
                     const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
 #pragma unroll
                     for (int v = 0; v < OWN; ++v) {
-                        const uint64_t f = __ballot(carry[v] >= th) & alive[v];
-                        res[v] = __builtin_amdgcn_inverse_ballot_w64(f) ? b : res[v];
-                        alive[v] &= ~f;
+                        alive[v] &= ~__ballot(carry[v] >= th);
+                        res[v] = add_lane_bit(res[v], alive[v]);
                     }
-                }
-            } while (++b < stop);
+                };
+                do close_bin();
+                while (++b < stop);
+            }
             uint64_t any = alive[0];
 #pragma unroll
             for (int v = 1; v < OWN; ++v) any |= alive[v];
@@ -1394,10 +1414,18 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
                     w[2 * k + 1][OWN - 1] = __uint_as_float(c3);
                 }
             }
+            f4 a0, a1;
+            if constexpr (AL_AHEAD) {
+                a0 = g.al[0];
+                a1 = g.al[AL_AHEAD ? 1 : 0];
+            } else {
+                a0 = *reinterpret_cast<const f4*>(alph + j);
+                a1 = *reinterpret_cast<const f4*>(alph + j + 4);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                al[i] = g.al[0][i];
-                al[4 + i] = g.al[1][i];
+                al[i] = a0[i];
+                al[4 + i] = a1[i];
             }
             if (bend >= j + 8) {  // all eight in the open bin
 #pragma unroll
@@ -1427,7 +1455,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         }
 #pragma unroll
         for (int v = 0; v < OWN; ++v)
-            if (ok[v]) out[pix * a.C_out + co + v] = res[v] >= 0 ? (float)res[v] : kInfTime;
+            if (ok[v]) out[pix * a.C_out + co + v] = __builtin_amdgcn_inverse_ballot_w64(alive[v]) ? kInfTime : (float)res[v];
         wave_sync();  // this pixel's list reads precede the next pixel's build
     }
 }

@@ -36,6 +36,25 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// A zero made in a VGPR where it is used: a plain 0 stored to LDS is often
+// hoisted by the compiler into a register that stays live for the whole
+// kernel.
+__device__ __forceinline__ int vzero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+// x + 1 in the lanes whose bit of `mask` is set, x elsewhere: one
+// v_addc_co_u32 with the mask as its carry-in (the compiler would spend a
+// v_cndmask and a v_add).
+__device__ __forceinline__ int add_lane_bit(int x, uint64_t mask) {
+    int r;
+    uint64_t carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(x), "s"(mask));
+    return r;
+}
+
 // Division of 0 <= n < 2^31 by a fixed divisor d >= 1 with a precomputed
 // multiplier (Granlund and Montgomery, "Division by invariant integers using
 // multiplication", 1994, the round-up method): l = ceil(log2 d),
