@@ -216,9 +216,10 @@ def test_culif_engine_narrow_convs(gpu_ctx_factory):
 def test_culif_engine_conv1_inputs_and_weights(gpu_ctx_factory):
     """The engine's conv1 integrates from masks of nonzero steps when every
     weight is finite: inputs other than 1.0 (read back under the site's
-    flag), -0.0 (skipped like 0) and T > 64 (two step blocks) match the
-    oracle; an infinite weight keeps the dense kernel (inf * 0 = NaN)."""
-    for T, delta in ((64, 32), (96, 32)):
+    flag), -0.0 (skipped like 0), T > 64 (two step blocks) and T not a
+    multiple of 8 (a last partial group of steps) match the oracle; an
+    infinite weight keeps the dense kernel (inf * 0 = NaN)."""
+    for T, delta in ((64, 32), (96, 32), (60, 20), (100, 20)):
         w = models.culif7(H=24, W=24, T=T, delta=delta)
         B = 2
         ev = models.dvs_events(w, B)

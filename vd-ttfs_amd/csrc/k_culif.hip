@@ -22,6 +22,8 @@
 //  k_fc_currents       the engine's per-step feed-forward input of that layer,
 //                      computed per (sample, step group) from the dense input.
 //  k_nhwc_to_nchw      flattening order for an FC layer after a spatial map.
+#include <type_traits>
+
 #include "common.h"
 #include "wave.h"
 
@@ -269,26 +271,27 @@ __global__ __launch_bounds__(256) void k_culif_event_masks(MaskArgs a) {
 
 // One wave per kMaskPixPerWave consecutive output pixels and a 64-wide c_out
 // block (lanes = c_out), four waves of one c_out block per workgroup; NK =
-// C_in * 9 taps, the block's
-// weights in LDS (w_lds[k][lane]).  Per 64-step block the tap masks are
-// transposed so that lane t holds the taps with input at step t (NK <= 32
-// bits); a step with input then visits only its set taps, in ascending k,
-// one LDS read and one add each (fma(w, 1, in) is exactly in + w).  All T
-// steps run the neuron update (a step without input still decays I and adds
-// it to V).
+// C_in * 9 taps, the lane's NK weights in registers.  Per 64-step block the
+// tap masks are transposed so that lane t holds the taps with input at step t
+// (NK <= 32 bits); a step with input then visits only its set taps, in
+// ascending k, one add each (fma(w, 1, in) is exactly in + w).  All T steps
+// run the neuron update (a step without input still decays I and adds it to
+// V).  The wave's live neurons are an SGPR lane mask and each lane counts the
+// steps it has lived through, which is its spike step once it fires; steps
+// are tested eight at a time against one byte of the block's input mask.
 template <int NK>
 __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint64_t* __restrict__ mask,
                                                           const uint32_t* __restrict__ nonbin, int nblk) {
     static_assert(NK <= 32, "tap masks are 32-bit");
-    __shared__ float w_lds[NK][64];
     const int wave = uniform(threadIdx.x >> 6);
     const int64_t b = blockIdx.x;
     const int cb = (int)(b % a.n_cblk);
-    for (int i = threadIdx.x; i < NK * 64; i += 256) {
-        const int k = i >> 6, cc = cb * 64 + (i & 63);
-        w_lds[k][i & 63] = cc < a.C_out ? a.W[(int64_t)cc * NK + k] : 0.0f;
-    }
-    __syncthreads();
+    const int lane = lane_id();
+    const int c = cb * 64 + lane;
+    const bool ok = c < a.C_out;
+    float w[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) w[k] = ok ? a.W[(int64_t)c * NK + k] : 0.0f;
     const int pix0 = uniform((int)((b / a.n_cblk) * 4 + wave)) * kMaskPixPerWave;  // < 2^31 (host check)
     for (int pq = 0; pq < kMaskPixPerWave; ++pq) {
         const int pix = pix0 + pq;
@@ -296,17 +299,15 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
         const int x = pix % a.Wd;
         const int y = (pix / a.Wd) % a.H;
         const int n = pix / (a.Wd * a.H);
-        const int lane = lane_id();
-        const int c = cb * 64 + lane;
-        const bool ok = c < a.C_out;
         // site of tap k, or -1 out of bounds (skipped, as the reference does)
         auto tap_site = [&](int k) {
             const int ci = k / 9, iy = y + (k % 9) / 3 - 1, ix = x + k % 3 - 1;
             return (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? ((n * a.C_in + ci) * a.H + iy) * a.Wd + ix : -1;
         };
-        float I = 0.0f, V = 0.0f, res = kInfTime;
-        bool alive = ok;
-        for (int tb = 0; tb < nblk; ++tb) {
+        float I = 0.0f, V = 0.0f;
+        int lived = 0;  // steps survived: the spike step once the lane fired
+        uint64_t alive = __ballot(ok);
+        for (int tb = 0; tb < nblk && alive; ++tb) {
             uint32_t tapm = 0;  // lane t: taps with input at step t0 + t
             uint32_t nbm = 0;   // taps whose nonzero inputs are not all 1.0 (uniform)
 #pragma unroll
@@ -314,54 +315,68 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
                 const int st = tap_site(k);
                 if (st >= 0) {  // uniform
                     const uint64_t mk = mask[(int64_t)st * nblk + tb];
-                    tapm |= (uint32_t)((mk >> lane) & 1ull) << k;
+                    tapm |= (__builtin_amdgcn_inverse_ballot_w64(mk) ? 1u : 0u) << k;
                     nbm |= (nonbin[(int64_t)st * nblk + tb] != 0 ? 1u : 0u) << k;
                 }
             }
             const uint64_t any = __ballot(tapm != 0);  // steps with input (none at t >= T)
             const int t0 = tb * 64;
             const int tn = (a.T - t0) < 64 ? (a.T - t0) : 64;
-            for (int t8 = 0; t8 < tn; t8 += 8) {
-                // eight steps without input while every lane's current is zero
-                // change nothing: I stays 0, V stays V (the threshold is fixed),
-                // and a lane with V >= th would have fired at the step before
-                if (((any >> t8) & 0xffull) == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) continue;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int t = t8 + u;
-                    float in = 0.0f;
-                    if ((any >> t) & 1) {
-                        uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)tapm, t);
-                        if (tm & nbm) {
-                            // an input value other than 1.0 at this step (rare)
-                            while (tm) {
-                                const int k = __builtin_ctz(tm);
-                                tm &= tm - 1;
-                                const float v =
-                                    ((nbm >> k) & 1) ? a.data[(int64_t)tap_site(k) * a.T + t0 + t] : 1.0f;
-                                in = __builtin_fmaf(w_lds[k][lane], v, in);
-                            }
-                        } else {
-                            while (tm) {
-                                const int k = __builtin_ctz(tm);
-                                tm &= tm - 1;
-                                in = __builtin_fmaf(w_lds[k][lane], 1.0f, in);
-                            }
-                        }
-                    }
-                    if (t < tn) {  // uniform; only a last partial block stops early
-                        I = __builtin_fmaf(I, a.decay, in);
-                        V = V + I;
-                        const bool f = alive && V >= a.th;
-                        res = f ? (float)(t0 + t) : res;
-                        alive = alive && !f;
-                    }
+            // the input current of step t0 + t, which has input in some tap
+            // (so tm != 0); NB: some tap's values are not all 1.0
+            auto input = [&](int t, auto nb) -> float {
+                uint32_t tm = (uint32_t)__builtin_amdgcn_readlane((int)tapm, t);
+                float in = 0.0f;
+                if (decltype(nb)::value && (tm & nbm)) {
+                    // an input value other than 1.0 at this step (rare)
+                    do {
+                        const int k = __builtin_ctz(tm);
+                        tm &= tm - 1;
+                        const float v = ((nbm >> k) & 1) ? a.data[(int64_t)tap_site(k) * a.T + t0 + t] : 1.0f;
+                        in = __builtin_fmaf(w[k], v, in);
+                    } while (tm);
+                } else {
+                    do {
+                        const int k = __builtin_ctz(tm);
+                        tm &= tm - 1;
+                        in = in + w[k];
+                    } while (tm);
                 }
-                if (__ballot(alive) == 0) goto done;
-            }
+                return in;
+            };
+            auto neuron = [&](float in) {
+                I = __builtin_fmaf(I, a.decay, in);
+                V = V + I;
+                alive &= ~__builtin_amdgcn_ballot_w64(V >= a.th);
+                lived = add_lane_bit(lived, alive);
+            };
+            auto run = [&](auto nb) {
+                for (int t8 = 0; t8 < tn; t8 += 8) {
+                    const uint32_t a8 = (uint32_t)(any >> t8) & 0xffu;
+                    const int n8 = (tn - t8) < 8 ? (tn - t8) : 8;
+                    // steps without input while every lane's current is zero
+                    // change nothing: I stays 0, V stays V (the threshold is
+                    // fixed), and a lane with V >= th would have fired at the
+                    // step before; its live lanes live through them
+                    if (a8 == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) {
+                        lived += __builtin_amdgcn_inverse_ballot_w64(alive) ? n8 : 0;
+                        continue;
+                    }
+                    if (n8 == 8) {
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
+                    } else {  // the last, partial chunk of T
+                        for (int u = 0; u < n8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
+                    }
+                    if (alive == 0) break;
+                }
+            };
+            if (nbm) run(std::true_type{});
+            else run(std::false_type{});
         }
-done:
-        if (ok) a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] = res;
+        if (ok)
+            a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] =
+                __builtin_amdgcn_inverse_ballot_w64(alive) ? kInfTime : (float)lived;
     }
 }
 
