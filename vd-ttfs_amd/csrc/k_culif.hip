@@ -292,6 +292,11 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
     float w[NK];
 #pragma unroll
     for (int k = 0; k < NK; ++k) w[k] = ok ? a.W[(int64_t)c * NK + k] : 0.0f;
+    // lane k < NK: tap k = (ci, ky, kx) in the reference's order, as a site
+    // offset from (n, ci = 0, y, x)
+    const int tk = lane < NK ? lane : 0;
+    const int tdy = (tk % 9) / 3 - 1, tdx = tk % 3 - 1;
+    const int64_t toff = ((int64_t)(tk / 9) * a.H + tdy) * a.Wd + tdx;
     const int pix0 = uniform((int)((b / a.n_cblk) * 4 + wave)) * kMaskPixPerWave;  // < 2^31 (host check)
     for (int pq = 0; pq < kMaskPixPerWave; ++pq) {
         const int pix = pix0 + pq;
@@ -299,24 +304,37 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
         const int x = pix % a.Wd;
         const int y = (pix / a.Wd) % a.H;
         const int n = pix / (a.Wd * a.H);
-        // site of tap k, or -1 out of bounds (skipped, as the reference does)
-        auto tap_site = [&](int k) {
-            const int ci = k / 9, iy = y + (k % 9) / 3 - 1, ix = x + k % 3 - 1;
-            return (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? ((n * a.C_in + ci) * a.H + iy) * a.Wd + ix : -1;
+        // this lane's tap site, or none out of bounds (skipped, as the
+        // reference does)
+        const int iy = y + tdy, ix = x + tdx;
+        const bool tap_in = lane < NK && iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd;
+        const int64_t site = ((int64_t)n * a.C_in * a.H + y) * a.Wd + x + toff;
+        auto tap_site = [&](int k) -> int64_t {  // wave-uniform, for a tap with input
+            const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)site, k);
+            const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)site >> 32), k);
+            return (int64_t)(lo | (hi << 32));
         };
         float I = 0.0f, V = 0.0f;
         int lived = 0;  // steps survived: the spike step once the lane fired
         uint64_t alive = __ballot(ok);
         for (int tb = 0; tb < nblk && alive; ++tb) {
+            // lane k's tap: its mask of steps with input, and whether a
+            // nonzero input is not 1.0
+            uint64_t mk = 0;
+            bool nbk = false;
+            if (tap_in) {
+                mk = mask[site * nblk + tb];
+                nbk = nonbin[site * nblk + tb] != 0;
+            }
+            const uint32_t nbm = (uint32_t)__ballot(nbk);  // bit k: tap k (NK <= 32)
             uint32_t tapm = 0;  // lane t: taps with input at step t0 + t
-            uint32_t nbm = 0;   // taps whose nonzero inputs are not all 1.0 (uniform)
+            if (__ballot(mk != 0)) {  // the transpose, for a block with any input
+                const int mlo = (int)(uint32_t)mk, mhi = (int)(uint32_t)(mk >> 32);
 #pragma unroll
-            for (int k = 0; k < NK; ++k) {
-                const int st = tap_site(k);
-                if (st >= 0) {  // uniform
-                    const uint64_t mk = mask[(int64_t)st * nblk + tb];
-                    tapm |= (__builtin_amdgcn_inverse_ballot_w64(mk) ? 1u : 0u) << k;
-                    nbm |= (nonbin[(int64_t)st * nblk + tb] != 0 ? 1u : 0u) << k;
+                for (int k = 0; k < NK; ++k) {
+                    const uint64_t m = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(mlo, k) |
+                                       ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mhi, k) << 32);
+                    tapm |= (__builtin_amdgcn_inverse_ballot_w64(m) ? 1u : 0u) << k;
                 }
             }
             const uint64_t any = __ballot(tapm != 0);  // steps with input (none at t >= T)
