@@ -127,6 +127,12 @@ def test_conv_pool_fc_fcrec_dropin(gpu_ctx_factory, delta):
     ctx.culif_pool(ctx.to_device(xp), d_p, 3, 7, 8, 6, 0.5, 1.0)
     assert np.any(exp < INF) and np.any(exp == INF)
     np.testing.assert_array_equal(d_p.download(), exp)
+    # thresholds at or below 0: every neuron fires at step 0, input or not;
+    # and a decay above 1 and below 0
+    for decay, th in ((0.5, 0.0), (0.5, -1.0), (1.5, 2.5), (-0.5, 0.75)):
+        exp = oracle.culif_pool(xp, 3, 7, 8, 6, T, delta, decay, th)
+        ctx.culif_pool(ctx.to_device(xp), d_p, 3, 7, 8, 6, decay, th)
+        np.testing.assert_array_equal(d_p.download(), exp)
     # fc2_bucketed_early and fc1_bucketed_recurrent
     for (N, F, O) in [(3, 300, 11), (2, 513, 128), (2, 70, 70)]:
         xf = spike_map(rng, N * F, T, p=0.5)

@@ -538,17 +538,37 @@ struct CPoolArgs {
     int64_t iN, iC, iY, iX;         // input strides
     int64_t oN, oC, oY, oX;         // output strides
     float decay, th;
+    FastDiv div_c, div_w, div_h;    // C, W_out, H_out (flat indices below 2^31)
 };
 
 // T3V:146-168.  in_t = 1.0 when one of the 4 inputs has floor(tf) == t
 // (the reference sets in_val[(int)tf - chunk] for chunk <= tf < chunk+D).
+// I32: flat indices below 2^31, split with precomputed multipliers instead
+// of 64-bit divisions.  Before a neuron's first input step I and V are +0,
+// so it fires there only if th <= 0, at step 0.
+template <bool I32>
 __global__ __launch_bounds__(256) void k_culif_pool(CPoolArgs a) {
     const int H_out = a.H_in / 2, W_out = a.W_in / 2;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
          idx += (int64_t)gridDim.x * blockDim.x) {
         int64_t n;
         int c, yo, xo;
-        if (a.nhwc) {
+        if constexpr (I32) {
+            const int i = (int)idx;
+            if (a.nhwc) {
+                const int p = fdiv(i, a.div_c), q = fdiv(p, a.div_w), r = fdiv(q, a.div_h);
+                c = i - p * a.C;
+                xo = p - q * W_out;
+                yo = q - r * H_out;
+                n = r;
+            } else {
+                const int p = fdiv(i, a.div_w), q = fdiv(p, a.div_h), r = fdiv(q, a.div_c);
+                xo = i - p * W_out;
+                yo = p - q * H_out;
+                c = q - r * a.C;
+                n = r;
+            }
+        } else if (a.nhwc) {
             c = (int)(idx % a.C);
             xo = (int)((idx / a.C) % W_out);
             yo = (int)((idx / a.C / W_out) % H_out);
@@ -560,22 +580,21 @@ __global__ __launch_bounds__(256) void k_culif_pool(CPoolArgs a) {
             n = idx / ((int64_t)a.C * W_out * H_out);
         }
         int tf[4];
-        bool any = false;
+        int t_first = a.T;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float v = a.in[n * a.iN + c * a.iC + (int64_t)(yo * 2 + (k >> 1)) * a.iY +
                                  (int64_t)(xo * 2 + (k & 1)) * a.iX];
             // arrival step, or -1: only 0 <= tf < T can ever set in_t
             tf[k] = (v >= 0.0f && v < (float)a.T) ? (int)v : -1;
-            any = any || tf[k] >= 0;
+            t_first = (tf[k] >= 0 && tf[k] < t_first) ? tf[k] : t_first;
         }
         float res = kInfTime;
-        if (!any) {
-            // no input: I and V stay +0
-            res = (0.0f >= a.th) ? 0.0f : kInfTime;
+        if (0.0f >= a.th) {
+            res = 0.0f;  // V = +0 reaches th at step 0, input or not
         } else {
             float I = 0.0f, V = 0.0f;
-            for (int t = 0; t < a.T; ++t) {
+            for (int t = t_first; t < a.T; ++t) {
                 const float in = (tf[0] == t || tf[1] == t || tf[2] == t || tf[3] == t) ? 1.0f : 0.0f;
                 I = __builtin_fmaf(I, a.decay, in);
                 V = V + I;
@@ -1033,7 +1052,13 @@ int launch_culif_pool(vdttfs_ctx* ctx, const float* in, float* out, int N, int C
     }
     a.decay = decay;
     a.th = th;
-    hipLaunchKernelGGL(k_culif_pool, dim3(flat_grid(a.total)), dim3(256), 0, ctx->stream, a);
+    a.div_c = make_fastdiv(C);
+    a.div_w = make_fastdiv(W_out > 0 ? W_out : 1);
+    a.div_h = make_fastdiv(H_out > 0 ? H_out : 1);
+    if (a.total < (INT64_C(1) << 31))
+        hipLaunchKernelGGL(k_culif_pool<true>, dim3(flat_grid(a.total)), dim3(256), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(k_culif_pool<false>, dim3(flat_grid(a.total)), dim3(256), 0, ctx->stream, a);
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }
