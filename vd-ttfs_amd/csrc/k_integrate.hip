@@ -1114,11 +1114,18 @@ __host__ __device__ inline int quad_wave_words(int nel_max, int T) {
 // Packed event of quad_build: bin (bits 0..6, 0x7F: no event), decay-LUT
 // index (7..13), rank in its chunk's bin (14..19), last of the chunk's bin
 // (20), weight row (21..31).  T <= 64 and at most 9 x 64 rows.
-template <int NB>
+// OPAQUE: the lane index is made opaque per pixel, so that nothing derived
+// from it (per-chunk element indices and offsets) is hoisted out of the
+// pixel loop into registers held through the stream.  The CuLIF kernel
+// takes it (k_stream_quad<2, 9, true>: 91 -> 67 VGPRs, 5 -> 7 waves per
+// SIMD, CuLIF-7 conv2 4.46 -> 4.08 ms); the VALU-bound LUT kernels keep the
+// hoisted values (VGG-16 conv 1 +0.7% with it).
+template <int NB, bool OPAQUE>
 __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
                                           int* alph, int* bs) {
     constexpr int KMAX = 9;
-    const int lane = lane_id();
+    int lane = lane_id();
+    if constexpr (OPAQUE) asm volatile("" : "+v"(lane));
     const int qd = fdiv((int)pix, a.div_w);
     const int w_out = (int)pix - qd * a.W_out;
     const int img = fdiv(qd, a.div_h);
@@ -1304,7 +1311,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)quad_build<NB>(m, pix, cur, kinfo, rows, alph, bs);
+        (void)quad_build<NB, CULIF>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
