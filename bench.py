@@ -66,7 +66,7 @@ HBM_PEAK_GBS = 8000.0
 COPY_FLOATS = 1 << 28  # 1 GiB read + 1 GiB written per calibration dispatch
 CSRC = os.path.join(ROOT, "vd-ttfs_amd", "csrc")
 # the sources that decide the integrator's dispatches and their memory traffic
-INTEG_SOURCES = ("k_integrate.hip", "k_bucketize.hip", "net.cpp", "capi.cpp", "k_culif.hip", "culif.cpp")
+INTEG_SOURCES = ("k_integrate.hip", "k_bucketize.hip", "net.cpp", "capi.cpp", "k_culif.hip", "culif.cpp", "wave.h")
 # gather-roof probe: rows uniformly random over a footprint that fits one XCD's 4 MB L2
 PROBE_L2_BYTES = 2 << 20
 PROBE_WAVES, PROBE_EVENTS, PROBE_REPS = 32768, 512, 5
@@ -682,8 +682,8 @@ def bench_culif(args) -> int:
             "unit": "GB/s",
             "frac": hbm / HBM_PEAK_GBS if tr else None,
             "traffic": tr["per_step"] / tr["launches"] if tr else None,
-            "kernel": "conv layers after conv1 (C_in <= 64: k_merge_dense + k_stream<CuLIF>; wider: "
-                      "k_bucketize + k_merge + k_stream<CuLIF>); achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE "
+            "kernel": "conv layers after conv1 (C_in <= 64: k_stream_quad<CuLIF>, list built in LDS; wider: "
+                      "k_bucketize + k_merge + k_stream_lean<CuLIF>); achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE "
                       "bytes of their dispatches / their live HIP-event time",
             "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
                                f"no counter summary for {key} in profiles/"),

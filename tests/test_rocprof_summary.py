@@ -91,3 +91,54 @@ def test_fc_layer_calls_split_at_bucketize(runs, tmp_path):
     kv = dict(t.split("=") for t in line.split())
     assert int(kv["LAUNCHES_PER_STEP"]) == 1
     assert float(kv["TRAFFIC_PER_STEP_BYTES"]) == pytest.approx((1 + 2 + 3) * KIB * 2 + (1 + 2 + 3) * KIB, rel=1e-6)
+
+
+def write_multi(d, name, rows):
+    """rows: (dispatch id, kernel, {counter: value}, duration)"""
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, f"{name}_counter_collection.csv"), "w", newline="") as f:
+        wr = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value",
+                                           "Start_Timestamp", "End_Timestamp"])
+        wr.writeheader()
+        t = 0
+        for i, kern, cnt, dur in rows:
+            for c, v in cnt.items():
+                wr.writerow({"Dispatch_Id": i, "Kernel_Name": f"void vdttfs::(anonymous namespace)::{kern}(args)",
+                             "Counter_Name": c, "Counter_Value": v, "Start_Timestamp": t,
+                             "End_Timestamp": t + dur})
+            t += dur + 10
+
+
+def test_counters_merges_runs(tmp_path):
+    """Per-wave counts from two runs over the same program, each divided by
+    its own run's SQ_WAVES; derived percentages weighted by duration; the
+    counting kernels left out."""
+    k = "k_stream_quad<4, 9, false>"
+    write_multi(tmp_path / "occ", "x", [
+        (1, k, {"SQ_WAVES": 100, "SQ_INSTS_LDS": 400, "SQ_LDS_BANK_CONFLICT": 100, "SQ_INSTS_VMEM_RD": 900,
+                "OccupancyPercent": 50.0}, 1000),
+        (2, k, {"SQ_WAVES": 100, "SQ_INSTS_LDS": 400, "SQ_LDS_BANK_CONFLICT": 100, "SQ_INSTS_VMEM_RD": 900,
+                "OccupancyPercent": 80.0}, 3000),
+        (3, "k_stream<true, 1, false, 1>", {"SQ_WAVES": 7, "SQ_INSTS_LDS": 1, "OccupancyPercent": 1.0}, 9000)])
+    write_multi(tmp_path / "mix", "x", [
+        (1, k, {"SQ_WAVES": 50, "SQ_INSTS_VALU": 1000, "SQ_INSTS_SALU": 500, "VALUBusy": 90.0, "SALUBusy": 30.0}, 2000),
+        (2, k, {"SQ_WAVES": 50, "SQ_INSTS_VALU": 1000, "SQ_INSTS_SALU": 500, "VALUBusy": 100.0, "SALUBusy": 50.0},
+         2000)])
+    out = rs.counters([(str(tmp_path / "occ"), "x"), (str(tmp_path / "mix"), "x")])
+    lines = out.splitlines()
+    head = [h.strip() for h in lines[0].strip("|").split("|")]
+    assert head == ["kernel", "dispatches", "us", "waves", "VALU/wave", "SALU/wave", "LDS/wave", "gathers/wave",
+                    "bank conflicts/LDS instr", "VALU busy %", "SALU busy %", "occupancy % of 32 waves/CU"]
+    assert len(lines) == 3  # header, rule, one kernel (the counting kernel is left out)
+    row = [c.strip() for c in lines[2].strip("|").split("|")]
+    assert row[0] == k and row[1] == "2"
+    assert float(row[2]) == pytest.approx(4.0)  # us, from the first run's timestamps (ns)
+    assert row[3] == "200"
+    assert float(row[4]) == pytest.approx(20.0)   # 2000 VALU / 100 waves of the mix run
+    assert float(row[5]) == pytest.approx(10.0)
+    assert float(row[6]) == pytest.approx(4.0)    # 800 LDS / 200 waves of the occupancy run
+    assert float(row[7]) == pytest.approx(9.0)
+    assert float(row[8]) == pytest.approx(0.25)
+    assert float(row[9]) == pytest.approx(95.0)   # equal durations
+    assert float(row[10]) == pytest.approx(40.0)
+    assert float(row[11]) == pytest.approx(72.5)  # (50 * 1 + 80 * 3) / 4

@@ -8,7 +8,7 @@ Reads the files that ``rocprofv3 --output-format csv -d DIR -o NAME`` writes
   python -m vdttfs.rocprof_summary layers  DIR NAME            # one forward, per layer
   python -m vdttfs.rocprof_summary traffic FETCH_DIR WRITE_DIR CFETCH_DIR CWRITE_DIR NAME \
          [--workload KEY] [--first PREFIX] [--copy-name NAME]
-  python -m vdttfs.rocprof_summary counters DIR NAME           # occupancy, LDS conflicts
+  python -m vdttfs.rocprof_summary counters DIR NAME [DIR NAME ...]  # instruction mix, occupancy, LDS conflicts
   python -m vdttfs.rocprof_summary per-wave DIR NAME [PREFIX]  # every counter per wave, per dispatch
 
 ``traffic`` takes four counter runs: FETCH_SIZE and WRITE_SIZE over the
@@ -169,40 +169,70 @@ def traffic(fdir: str, wdir: str, cfdir: str, cwdir: str, name: str, workload: s
     return "\n".join(lines)
 
 
-def counters(d: str, name: str) -> str:
-    """Per kernel (non-counting dispatches, summed): waves, gathers and LDS
-    instructions per wave, LDS bank conflicts per LDS instruction, and
-    rocprofv3's OccupancyPercent (400 * SQ_WAVE_CYCLES / GRBM_GUI_ACTIVE /
-    CU_NUM / 32: resident waves as a share of 32 per CU over the dispatch),
-    weighted by dispatch duration."""
-    rows = _csv(d, name, "counter_collection")
-    by = collections.OrderedDict()
-    for r in rows:
-        k = int(r["Dispatch_Id"])
-        e = by.setdefault(k, {"name": short_name(r["Kernel_Name"]),
-                              "dur": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
-        e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+# derived percentages rocprofv3 computes per dispatch (averaged over a
+# kernel's dispatches, weighted by duration)
+_PERCENT = (("VALUBusy", "VALU busy %"), ("SALUBusy", "SALU busy %"),
+            ("OccupancyPercent", "occupancy % of 32 waves/CU"))
+
+
+def counters(runs) -> str:
+    """Per kernel (non-counting dispatches, summed over each run): waves,
+    instructions per wave (VALU, SALU, LDS, vector-memory reads; whichever
+    the runs collected), LDS bank conflicts per LDS instruction, and
+    rocprofv3's derived percentages where collected, weighted by dispatch
+    duration: VALUBusy and SALUBusy (100 * SQ_ACTIVE_INST_VALU or
+    SQ_INST_CYCLES_SALU / CU_NUM / GRBM_GUI_ACTIVE: the share of the
+    dispatch's cycles in which a CU's vector or scalar ALUs were busy) and
+    OccupancyPercent (400 *
+    SQ_WAVE_CYCLES / GRBM_GUI_ACTIVE / CU_NUM / 32: resident waves as a
+    share of 32 per CU).  `runs` is a list of (DIR, NAME) pairs of counter
+    runs over the same program; each counter is divided by SQ_WAVES of its
+    own run, and the durations shown are those of the first run."""
     agg = collections.OrderedDict()
-    for e in by.values():
-        n = e["name"]
-        if _COUNTING.match(n):
-            continue
-        a = agg.setdefault(n, collections.defaultdict(float))
-        a["dispatches"] += 1
-        a["dur"] += e["dur"]
-        for c in ("SQ_WAVES", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT"):
-            a[c] += e.get(c, 0.0)
-        a["OccupancyPercent"] += e.get("OccupancyPercent", 0.0) * e["dur"]
-    out = ["| kernel | dispatches | us | waves | gathers/wave | LDS instr/wave | bank conflicts/LDS instr "
-           "| occupancy % of 32 waves/CU |",
-           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for ri, (d, name) in enumerate(runs):
+        by = collections.OrderedDict()
+        for r in _csv(d, name, "counter_collection"):
+            k = int(r["Dispatch_Id"])
+            e = by.setdefault(k, {"name": short_name(r["Kernel_Name"]),
+                                  "dur": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for e in by.values():
+            n = e["name"]
+            if _COUNTING.match(n):
+                continue
+            a = agg.setdefault(n, collections.defaultdict(float))
+            if ri == 0:
+                a["dispatches"] += 1
+                a["dur"] += e["dur"]
+            a["waves%d" % ri] += e.get("SQ_WAVES", 0.0)
+            for c, v in e.items():
+                if c.startswith("SQ_") and c != "SQ_WAVES":
+                    a[c] += v
+                    a["run_of_" + c] = ri
+            for c, _ in _PERCENT:
+                if c in e:
+                    a[c] += e[c] * e["dur"]
+                    a[c + "_dur"] += e["dur"]
+    have = set(c for a in agg.values() for c in a)
+    per_wave_cols = [(c, h) for c, h in (("SQ_INSTS_VALU", "VALU"), ("SQ_INSTS_SALU", "SALU"),
+                                         ("SQ_INSTS_LDS", "LDS"), ("SQ_INSTS_VMEM_RD", "gathers"))
+                     if c in have]
+    pct_cols = [(c, h) for c, h in _PERCENT if c in have]
+    head = ["kernel", "dispatches", "us", "waves"] + ["%s/wave" % h for _, h in per_wave_cols]
+    if "SQ_LDS_BANK_CONFLICT" in have:
+        head.append("bank conflicts/LDS instr")
+    head += [h for _, h in pct_cols]
+    out = ["| " + " | ".join(head) + " |", "|---|" + "---:|" * (len(head) - 1)]
     for n, a in sorted(agg.items(), key=lambda kv: -kv[1]["dur"]):
-        w = max(a["SQ_WAVES"], 1.0)
-        lds = a["SQ_INSTS_LDS"]
-        out.append("| %s | %d | %.1f | %d | %.1f | %.1f | %s | %.1f |" % (
-            n, a["dispatches"], a["dur"], a["SQ_WAVES"], a["SQ_INSTS_VMEM_RD"] / w, lds / w,
-            ("%.3f" % (a["SQ_LDS_BANK_CONFLICT"] / lds)) if lds else "-",
-            a["OccupancyPercent"] / a["dur"]))
+        row = [n, "%d" % a["dispatches"], "%.1f" % a["dur"], "%d" % a["waves0"]]
+        for c, _ in per_wave_cols:
+            w = a["waves%d" % int(a.get("run_of_" + c, 0))]
+            row.append("%.1f" % (a[c] / w) if w else "-")
+        if "SQ_LDS_BANK_CONFLICT" in have:
+            row.append(("%.3f" % (a["SQ_LDS_BANK_CONFLICT"] / a["SQ_INSTS_LDS"])) if a["SQ_INSTS_LDS"] else "-")
+        for c, _ in pct_cols:
+            row.append(("%.1f" % (a[c] / a[c + "_dur"])) if a[c + "_dur"] else "-")
+        out.append("| " + " | ".join(row) + " |")
     return "\n".join(out)
 
 
@@ -247,7 +277,8 @@ def main(argv) -> int:
         print(traffic(*argv[2:7], workload=opts.get("--workload", ""), first=opts.get("--first", "k_encode"),
                       copy_name=opts.get("--copy-name", "")))
     elif cmd == "counters":
-        print(counters(argv[2], argv[3]))
+        rest = argv[2:]
+        print(counters(list(zip(rest[::2], rest[1::2]))))
     elif cmd == "per-wave":
         print(per_wave(argv[2], argv[3], *argv[4:5]))
     else:
