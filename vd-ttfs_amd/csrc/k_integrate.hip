@@ -36,6 +36,10 @@ namespace {
 constexpr int kBlockBins = 64;  // arrival bins handled per table / per VGPR of bin starts
 constexpr int kListPad = 32;    // zeroed entries after each pixel's merged list (four groups)
 constexpr int kMergeWaves = 4;
+// most waves per workgroup of k_stream_quad.  Each wave has its own LDS
+// region and pixels, so a workgroup is only the unit its LDS is freed in;
+// the launcher picks 1 or 4 (see launch_integrate_dense).
+constexpr int kQuadWaves = 4;
 
 // ---------------------------------------------------------------------------
 // k_merge: one wave per output pixel.  The in-bounds receptive columns' bin
@@ -1269,7 +1273,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
 }
 
 template <int GEO, int NB, bool CULIF>
-__global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
+__global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
                                                      const float* __restrict__ theta, int nel_max) {
     static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
     constexpr int OWN = 4 / GEO;  // c_out per lane
@@ -1307,7 +1311,7 @@ __global__ __launch_bounds__(256) void k_stream_quad(DenseMergeArgs m, StreamArg
         ok[v] = co + v < a.C_out;
         bias[v] = (ok[v] && !CULIF) ? a.bias[co + v] : 0.0f;  // the CuLIF neuron starts at V = 0
     }
-    const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.ppw;
+    const int64_t pix0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave) * a.ppw;
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
@@ -2409,7 +2413,7 @@ namespace {
 bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     const int nel_max = sh.K_h * sh.K_w * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, ctx->c.T) * sizeof(int);
-    const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, ctx->c.T) * sizeof(int);
+    const size_t qlds = (size_t)kQuadWaves * quad_wave_words(nel_max, ctx->c.T) * sizeof(int);
     if (ctx->c.T > kBlockBins) return false;
     if (gather == 1) return sh.C_out <= 64 && lds <= kFusedMaxLds;
     return gather == 2 && sh.C_out <= 128 && sh.C_out % 4 == 0 && qlds <= kFusedMaxLds;
@@ -2759,9 +2763,15 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
         // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
         if (!counters && m.in_bytes > 0) {
-            const size_t qlds = (size_t)kMergeWaves * quad_wave_words(nel_max, m.T) * sizeof(int);
+            // waves per workgroup: one, except the one-chunk four-event
+            // kernel (VGG conv 0), measured A/B on one box: CuLIF conv2
+            // 4.08 -> 3.31 ms with 1 (4.23 with 2), VGG conv 1 -0.8% and
+            // conv 2 -1.4% with 1, conv 0 +1.4% with 1
+            const int qw = (epi != 2 && nel_max <= 64) ? kQuadWaves : 1;
+            const size_t qlds = (size_t)qw * quad_wave_words(nel_max, m.T) * sizeof(int);
+            const int64_t qblocks = (n_pix + qw * a.ppw - 1) / (qw * a.ppw);
 #define VD_LAUNCH_QUAD(G, NB, L)                                                                           \
-    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)fblocks), dim3(64 * kMergeWaves), qlds, \
+    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)qblocks), dim3(64 * qw), qlds, \
                        ctx->stream, m, a, out, theta, nel_max)
 #define VD_LAUNCH_QUAD_NB(G, L)          \
     do {                                 \
