@@ -10,7 +10,8 @@
 Each case must equal the oracle bit for bit through the drop-in pair
 (reference-layout bucketize + integrate) and through the engine path with
 and without work counters (counts equal too).  The shapes put one layer on
-each path: fused list in LDS (one and two events per load), bucketize + merge
+each path: fused list in LDS (one and two events per load, and past the
+dense path's C_in limit), bucketize + merge
 + dwordx4 gather, the narrow stream, the register path and the generic
 integrator (> 25 taps).
 """
@@ -31,6 +32,7 @@ INF = 9999.0
 SHAPES = [
     ("fused-c64", 64, 32.0, True, False, 2, 6, 6, 16, 64, 3),
     ("fused-pair-c128", 64, 32.0, True, False, 2, 5, 5, 32, 128, 3),
+    ("fused-wide-c128", 64, 32.0, True, False, 2, 5, 5, 128, 128, 3),
     ("bins-x4-c256", 64, 0.0, False, False, 2, 6, 6, 96, 256, 3),
     ("narrow-c10", 64, 0.0, False, False, 3, 8, 8, 6, 10, 5),
     ("reg-c3-o16", 64, 32.0, True, False, 2, 7, 7, 3, 16, 3),

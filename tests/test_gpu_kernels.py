@@ -109,6 +109,12 @@ LAYER_CASES = [
     # the integrating kernel (Task 1 alpha-by-bin, valid conv; Task 2 same conv)
     ("t1-conv3x3-lds-list", 64, 0.0, 16, False, False, 3, 11, 9, 48, 40, 3),
     ("t2-conv3x3-lds-list-c3", 64, 32.0, 8, True, False, 4, 12, 10, 3, 64, 3),
+    # 64 < C_in <= 128: the list still built in LDS from the dense map (18
+    # chunks of 64) without counters; the counting forward takes bucketize +
+    # merge + stream
+    ("t2-conv3x3-wide-c96-o128", 64, 32.0, 8, True, False, 2, 7, 6, 96, 128, 3),
+    ("t1-conv3x3-wide-c128-o64", 64, 0.0, 16, False, False, 2, 6, 7, 128, 64, 3),
+    ("t2-conv3x3-wide-c72-o100", 64, 32.0, 8, True, False, 3, 5, 5, 72, 100, 3),
     # K_h * K_w * C_in <= 32, C_out <= 64, T <= 64: receptive field in
     # registers, 64 / C_out pixels per wave (the two cases above take it too)
     ("t1-conv2x2-reg-c8-o40", 64, 0.0, 16, False, False, 3, 9, 9, 8, 40, 2),

@@ -32,7 +32,7 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
     net = make_net(ctx, w, 16)
     try:
         got = [net.get_plan(i) for i in range(len(w.layers))]
-        exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (FUSED, 2, 1), 4: (BINS, 2, 1), 6: (BINS, 4, 1),
+        exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (FUSED, 2, 1), 4: (FUSED, 2, 1), 6: (BINS, 4, 1),
                10: (BINS, 4, 1), 16: (BINS, 4, 1), 18: (BINS, 1, 1)}
         for i, p in exp.items():
             assert got[i] == p, f"layer {i}: {got[i]}"
@@ -43,6 +43,8 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
                (4, DENSE, 0, 0),    # dense merge needs C_in <= 64
                (1, FUSED, 4, 0),    # the fused kernels gather one c_out per lane or two events per load
                (3, FUSED, 4, 0),    # ... and C_out <= 128
+               (4, FUSED, 4, 0),    # ... also past the dense path's C_in limit (128 -> 128)
+               (6, FUSED, 0, 0),    # 128 -> 256: no fused kernel gathers 256 c_out
                (0, 0, 3, 0),        # gather is 1, 2 or 4
                (2, BINS, 0, 0),     # pools have no integrator
                (1, REG, 0, 0),      # 9 * 64 receptive elements do not fit in registers

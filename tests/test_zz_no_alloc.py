@@ -23,6 +23,7 @@ CASES = [
     ("fused pair 16->128 3x3", True, False, (4, 3), 16, 16, 16, 128, 3),
     ("dense 24->256 3x3", True, False, (3, 2), 8, 8, 24, 256, 3),
     ("bins 130->256 3x3", True, False, (3, 1), 8, 8, 130, 256, 3),
+    ("fused wide 96->128 3x3", True, False, (3, 2), 10, 10, 96, 128, 3),
     ("narrow 6->16 5x5 valid", False, False, (40, 7), 12, 12, 6, 16, 5),
     ("register 1->6 5x5 valid", False, False, (50, 9), 28, 28, 1, 6, 5),
     ("fc 600->300", True, True, (40, 13), 1, 1, 600, 300, 1),
@@ -82,13 +83,13 @@ def test_noalloc_matches_layer_forward(gpu_ctx_factory, case):
 
 
 def test_noalloc_rejects_oversized_layer(gpu_ctx_factory):
-    """A 128->128 conv at 64x32x32 (bins path) needs ~0.7 GB of bucketize
+    """A 128->256 conv at 64x32x32 (bins path) needs ~0.7 GB of bucketize
     output and merged lists: refused with VDTTFS_E_UNSUPPORTED before any
     launch, the output left untouched."""
     say("noalloc oversized layer")
     tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
     ctx = gpu_ctx_factory(tc)
-    B, H, W, C_in, C_out = 64, 32, 32, 128, 128
+    B, H, W, C_in, C_out = 64, 32, 32, 128, 256
     d_in = ctx.empty(B * H * W * C_in).fill(0)
     d_out = ctx.empty(B * H * W * C_out).fill(0x7F)
     d_W, d_b = ctx.empty(9 * C_in * C_out).fill(0), ctx.empty(C_out).fill(0)

@@ -351,8 +351,8 @@ static int engine_layer(vdttfs_ctx* ctx, float* d_out, const float* d_in, const 
     const int64_t cols = s.is_fc ? s.B : (int64_t)s.B * s.H_in * s.W_in;
     const int64_t n_pix = s.is_fc ? s.B : (int64_t)s.B * s.H_out * s.W_out;
     const int64_t cap = merged_list_cap(s);
-    const bool dense = integrate_dense_ok(ctx, s) && !plan_bins(p);
-    const bool lds_list = plan_lds_list(s, p, counters != nullptr, false);
+    const bool dense = plan_from_dense(ctx, s, p, counters != nullptr);
+    const bool lds_list = plan_lds_list(ctx, s, p, counters != nullptr, false);
     if (!lds_list)
         VD_TRY(ensure_merge_scratch(ctx, (size_t)(n_pix * cap), (size_t)n_pix * (ctx->c.T + 1)));
     if (dense)  // conv: merged lists straight from the dense map

@@ -117,7 +117,7 @@ inline bool plan_bins(const LaunchPlan& p) { return p.path == VDTTFS_PATH_BINS |
 // Whether a layer integrated under resolved plan p builds its merged lists in
 // LDS (so it needs no merged-list scratch), with or without counters and the
 // CuLIF neuron.
-bool plan_lds_list(const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif);
+bool plan_lds_list(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif);
 // Fills every field of *out: a requested field is checked against the
 // layer's shape (VDTTFS_E_UNSUPPORTED when the kernels cannot run it), a zero
 // field takes the built-in choice.
@@ -136,6 +136,13 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
 // from the dense spike map d_in (no bucketize pass); alpha is the layer's
 // decay LUT.  Same results as bucketize + launch_integrate_bins.
 bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& s);
+// Conv layers past those limits (C_in <= 128) that the fused plan still
+// builds from the dense map when no counters are asked for.
+bool quad_wide_ok(const vdttfs_ctx* ctx, const IntegShape& s);
+// Whether a layer under resolved plan p takes launch_integrate_dense (its
+// lists built from the dense map) rather than bucketize +
+// launch_integrate_bins, with or without counters.
+bool plan_from_dense(const vdttfs_ctx* ctx, const IntegShape& s, const LaunchPlan& p, bool counters);
 int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
                            int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
                            const float* theta, int t_min, const IntegShape& s,

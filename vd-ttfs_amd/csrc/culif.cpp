@@ -304,9 +304,12 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
                 const int64_t cols = (int64_t)B * d.H_in * d.W_in;
                 IntegShape sh{B, d.H_in, d.W_in, d.C_in, d.H_in, d.W_in, d.C_out, 3, 3,
                               /*pad_h=*/1, /*pad_w=*/1, /*is_fc=*/0};
-                // narrow inputs build the merged lists from the dense map (the
-                // bin-layout bucketize then only counts retained events)
-                const bool dense = integrate_dense_ok(ctx, sh);
+                // inputs up to C_in 64, and outside counting forwards up to 128
+                // (the fused list build), build the merged lists from the dense
+                // map (the bin-layout bucketize then only counts retained events)
+                LaunchPlan plan;
+                VD_TRY(resolve_plan(ctx, sh, LaunchPlan{}, &plan));
+                const bool dense = plan_from_dense(ctx, sh, plan, count_here);
                 if (!dense || count_here)
                     VD_TRY(launch_bucketize_bins(ctx, cur, cols, d.C_in, net->ones, net->ev, net->off,
                                                  count_here ? ctx->d_counters + 2 : nullptr));

@@ -211,6 +211,7 @@ struct DenseMergeArgs {
 
 constexpr int kDenseMaxBins = 256;
 constexpr int kDenseMaxCin = 64;
+constexpr int kQuadMaxCin = 128;  // k_stream_quad's list build: 18 chunks of 64 per 3x3 pixel
 constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 
 // Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
@@ -1117,13 +1118,14 @@ __host__ __device__ inline int quad_wave_words(int nel_max, int T) {
 
 // Packed event of quad_build: bin (bits 0..6, 0x7F: no event), decay-LUT
 // index (7..13), rank in its chunk's bin (14..19), last of the chunk's bin
-// (20), weight row (21..31).  T <= 64 and at most 9 x 64 rows.
+// (20), weight row (21..31).  T <= 64 and at most 9 x 128 rows.
 // OPAQUE: the lane index is made opaque per pixel, so that nothing derived
 // from it (per-chunk element indices and offsets) is hoisted out of the
 // pixel loop into registers held through the stream.  The CuLIF kernel
 // takes it (k_stream_quad<2, 9, true>: 91 -> 67 VGPRs, 5 -> 7 waves per
-// SIMD, CuLIF-7 conv2 4.46 -> 4.08 ms); the VALU-bound LUT kernels keep the
-// hoisted values (VGG-16 conv 1 +0.7% with it).
+// SIMD, CuLIF-7 conv2 4.46 -> 4.08 ms), and so do the 18-chunk builds (120
+// -> 79 VGPRs); the VALU-bound 9-chunk LUT kernels keep the hoisted values
+// (VGG-16 conv 1 +0.7% with it).
 template <int NB, bool OPAQUE>
 __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
                                           int* alph, int* bs) {
@@ -1160,13 +1162,13 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
         msk[2 * lane + 1] = z;
     }
     wave_sync();
-    const int nel = nk * a.C_in;       // <= 9 * 64
+    const int nel = nk * a.C_in;       // <= 9 * 128
     const int n_chunks = (nel + 63) >> 6;  // <= NB
     int pk[NB];
     {
         // element f = c * 64 + lane: tap k = f / C_in (the quotient's
-        // fractional part is >= 0.5 / 64, so the float product rounds it
-        // correctly), cin ci.  Every chunk's load is issued before any is
+        // fractional part is >= 0.5 / C_in >= 0.5 / 128, far above the
+        // product's rounding error, so it rounds down correctly), cin ci.  Every chunk's load is issued before any is
         // used, with no branch (elements past the end load the map's first
         // word; their row and tap fields are never read).
         const __amdgpu_buffer_rsrc_t rin =
@@ -1315,7 +1317,7 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)quad_build<NB, CULIF>(m, pix, cur, kinfo, rows, alph, bs);
+        (void)quad_build<NB, (CULIF || NB > 9)>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
@@ -2393,10 +2395,30 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
     return !sh.is_fc && shape_ok && ctx->c.T <= kDenseMaxBins && sh.C_in <= kDenseMaxCin;
 }
 
-bool plan_lds_list(const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif) {
+// Conv layers past the dense path's C_in limit whose lists k_stream_quad
+// still builds in LDS straight from the dense map (no counters; a counting
+// forward of such a layer takes bucketize + merge + stream): up to 9 taps
+// and C_in <= 128 (18 chunks of 64), T <= 64, the four- or two-event gather
+// (C_out <= 64, or <= 128 and a multiple of 4), 32-bit input offsets.
+bool quad_wide_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    int64_t wbytes;
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
+    return !sh.is_fc && sh.K_h * sh.K_w <= 9 && ctx->c.T <= kBlockBins && sh.C_in > kDenseMaxCin &&
+           sh.C_in <= kQuadMaxCin && !narrow_path_ok(sh, &wbytes) && wave_path_ok(sh, &wbytes) &&
+           in_bytes < (INT64_C(1) << 31) && (sh.C_out <= 64 || (sh.C_out <= 128 && sh.C_out % 4 == 0));
+}
+
+bool plan_from_dense(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters) {
+    if (plan_bins(p)) return false;
+    return integrate_dense_ok(ctx, sh) || (!counters && p.path == VDTTFS_PATH_FUSED && quad_wide_ok(ctx, sh));
+}
+
+bool plan_lds_list(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif) {
     if (p.path == VDTTFS_PATH_WINDOW) return true;
     if (p.path == VDTTFS_PATH_REG) return !counters && !culif;
     if (p.path != VDTTFS_PATH_FUSED) return false;
+    // past the dense limits a counting forward takes bucketize + merge + stream
+    if (counters && !integrate_dense_ok(ctx, sh)) return false;
     // two events per load: k_stream_quad only (no counters, 32-bit input
     // offsets); otherwise k_merge_dense + k_stream
     (void)culif;
@@ -2415,7 +2437,9 @@ bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, ctx->c.T) * sizeof(int);
     const size_t qlds = (size_t)kQuadWaves * quad_wave_words(nel_max, ctx->c.T) * sizeof(int);
     if (ctx->c.T > kBlockBins) return false;
-    if (gather == 1) return sh.C_out <= 64 && lds <= kFusedMaxLds;
+    // past the dense limits only k_stream_quad runs (no counters)
+    const bool wide = quad_wide_ok(ctx, sh);
+    if (gather == 1) return sh.C_out <= 64 && (wide ? qlds : lds) <= kFusedMaxLds;
     return gather == 2 && sh.C_out <= 128 && sh.C_out % 4 == 0 && qlds <= kFusedMaxLds;
 }
 
@@ -2598,7 +2622,7 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     // 8,192 waves against 5,120 resident, 0.42 -> 0.39 ms each): the second
     // round would run mostly empty.
     if (req.ppw > kMaxPixPerWave) return plan_error(sh, "at most 8 pixels per wave");
-    const bool fused = dense && fused_ok(ctx, sh, p.gather);
+    const bool fused = (dense || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, p.gather);
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
         return plan_error(sh, "fused path needs the dense limits, T <= 64 and gather 1 (C_out <= 64) or 2 (C_out <= 128)");
@@ -2633,7 +2657,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
                           unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
-    if (plan && plan->path && !plan_bins(*plan))
+    // a fused plan past the dense limits falls back here for counting forwards
+    if (plan && plan->path && !plan_bins(*plan) && !(plan->path == VDTTFS_PATH_FUSED && quad_wide_ok(ctx, sh)))
         return set_error(VDTTFS_E_INVALID, "integrate_bins: the plan asks for a dense path");
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
@@ -2692,10 +2717,14 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
                            unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
-    if (!integrate_dense_ok(ctx, sh) || (!narrow && !wave_path_ok(sh, &wbytes)))
+    const bool wide = !integrate_dense_ok(ctx, sh) && quad_wide_ok(ctx, sh);
+    if ((!integrate_dense_ok(ctx, sh) && !(wide && !counters)) || (!narrow && !wave_path_ok(sh, &wbytes)))
         return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
+    if (wide && p.path != VDTTFS_PATH_FUSED)
+        return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: past C_in %d only the fused path builds from the map",
+                         kDenseMaxCin);
     if (plan_bins(p))
         return set_error(VDTTFS_E_INVALID, "integrate_dense: the plan asks for the bins path");
     if (p.path == VDTTFS_PATH_REG) {
@@ -2709,7 +2738,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int64_t n_pix = n_pixels(sh);
     const int64_t cap = (int64_t)nk_max * sh.C_in + kListPad;
     // the fused kernels keep their lists in LDS; the others need the scratch
-    const bool lds_list = plan_lds_list(sh, p, counters != nullptr, culif != nullptr);
+    const bool lds_list = plan_lds_list(ctx, sh, p, counters != nullptr, culif != nullptr);
     if (!lds_list && (!list || !bstart || list_cap < cap))
         return set_error(VDTTFS_E_INVALID, "integrate: merged-list scratch too small");
     DenseMergeArgs m{};
@@ -2777,8 +2806,10 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     do {                                 \
         if (nel_max <= 64)               \
             VD_LAUNCH_QUAD(G, 1, L);     \
-        else                             \
+        else if (nel_max <= 9 * 64)      \
             VD_LAUNCH_QUAD(G, 9, L);     \
+        else                             \
+            VD_LAUNCH_QUAD(G, 18, L);    \
     } while (0)
             if (epi == 2) {
                 if (culif)

@@ -202,7 +202,7 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             // and in a counting forward for its retained-event count
             LaunchPlan plan;
             VD_TRY(resolve_plan(ctx, s, l.plan, &plan));
-            const bool dense = !plan_bins(plan);
+            const bool dense = plan_from_dense(ctx, s, plan, count);
             TimedPair tb{}, ti{};
             tb.layer = ti.layer = (int)i;
             if (!dense || count) {

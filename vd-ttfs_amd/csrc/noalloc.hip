@@ -87,8 +87,8 @@ extern "C" int vdttfs_layer_forward_noalloc(vdttfs_ctx* ctx, float* d_out, const
     const int64_t cols = s.is_fc ? s.B : (int64_t)s.B * s.H_in * s.W_in;
     const int64_t n_pix = s.is_fc ? s.B : (int64_t)s.B * s.H_out * s.W_out;
     const int64_t cap = merged_list_cap(s);
-    const bool dense = integrate_dense_ok(ctx, s) && !plan_bins(p);
-    const bool lds_list = plan_lds_list(s, p, false, false);
+    const bool dense = plan_from_dense(ctx, s, p, false);
+    const bool lds_list = plan_lds_list(ctx, s, p, false, false);
     // scratch layout: [merged list | bin starts | bin-layout events | bin offsets]
     const size_t list_b = lds_list ? 0 : align256((size_t)n_pix * cap * sizeof(int2));
     const size_t bs_b = lds_list ? 0 : align256((size_t)n_pix * (ctx->c.T + 1) * 4);
