@@ -524,9 +524,9 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": hbm / HBM_PEAK_GBS if tr else None,
             "traffic": tr["per_step"] / tr["launches"] if tr else None,
-            "kernel": "integrator = one layer's list build + stream: k_stream_quad (conv, C_in <= 64, "
-                      "32 <= C_out <= 128: merged list built in LDS, four events per dwordx4 load up to 64 "
-                      "c_out, two up to 128), k_merge_dense + k_stream_lean (other conv, C_in <= 64) or "
+            "kernel": "integrator = one layer's list build + stream: k_stream_quad (conv, <= 9 taps, "
+                      "C_in <= 128, 32 <= C_out <= 128: merged list built in LDS, four events per dwordx4 load "
+                      "up to 64 c_out, two up to 128), k_merge_dense + k_stream_lean (other conv, C_in <= 64) or "
                       "k_bucketize + k_merge + k_stream_lean (wider conv; FC) with pair or four-c_out-per-lane "
                       "dwordx4 gathers (k_stream for one c_out per lane); layers with C_out < 32 stream with "
                       "k_stream_narrow, or with k_conv_small when the receptive field has <= 32 elements.  A "
@@ -682,7 +682,7 @@ def bench_culif(args) -> int:
             "unit": "GB/s",
             "frac": hbm / HBM_PEAK_GBS if tr else None,
             "traffic": tr["per_step"] / tr["launches"] if tr else None,
-            "kernel": "conv layers after conv1 (C_in <= 64: k_stream_quad<CuLIF>, list built in LDS; wider: "
+            "kernel": "conv layers after conv1 (C_in <= 128: k_stream_quad<CuLIF>, list built in LDS; wider: "
                       "k_bucketize + k_merge + k_stream_lean<CuLIF>); achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE "
                       "bytes of their dispatches / their live HIP-event time",
             "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
