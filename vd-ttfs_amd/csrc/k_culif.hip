@@ -369,24 +369,31 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
                 lived = add_lane_bit(lived, alive);
             };
             auto run = [&](auto nb) {
-                for (int t8 = 0; t8 < tn; t8 += 8) {
+                // whole groups of 8 steps, then the last, partial group of T
+                int t8 = 0;
+                int first = t0 == 0 ? 1 : 0;  // the group holding step 0 never skips
+                for (; t8 + 8 <= tn; t8 += 8) {
                     const uint32_t a8 = (uint32_t)(any >> t8) & 0xffu;
-                    const int n8 = (tn - t8) < 8 ? (tn - t8) : 8;
                     // steps without input while every lane's current is zero
                     // change nothing: I stays 0, V stays V (the threshold is
                     // fixed), and a lane with V >= th would have fired at the
-                    // step before; its live lanes live through them
-                    if (a8 == 0 && t0 + t8 > 0 && __ballot(I != 0.0f) == 0) {
-                        lived += __builtin_amdgcn_inverse_ballot_w64(alive) ? n8 : 0;
-                        continue;
+                    // step before (none precedes step 0); its live lanes live
+                    // through them
+                    const int key = (int)a8 | first;
+                    first = 0;
+                    if (key == 0) {
+                        if (__builtin_amdgcn_ballot_w64(I != 0.0f) == 0) {
+                            lived += __builtin_amdgcn_inverse_ballot_w64(alive) ? 8 : 0;
+                            continue;
+                        }
                     }
-                    if (n8 == 8) {
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
-                    } else {  // the last, partial chunk of T
-                        for (int u = 0; u < n8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
-                    }
-                    if (alive == 0) break;
+                    for (int u = 0; u < 8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
+                    if (alive == 0) return;
+                }
+                if (t8 < tn) {
+                    const uint32_t a8 = (uint32_t)(any >> t8) & 0xffu;
+                    for (int u = 0; u < tn - t8; ++u) neuron((a8 & (1u << u)) ? input(t8 + u, nb) : 0.0f);
                 }
             };
             if (nbm) run(std::true_type{});
