@@ -33,7 +33,7 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
     try:
         got = [net.get_plan(i) for i in range(len(w.layers))]
         exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (FUSED, 2, 1), 4: (FUSED, 2, 1), 6: (BINS, 4, 1),
-               10: (BINS, 4, 1), 16: (BINS, 4, 1), 18: (BINS, 1, 1)}
+               10: (BINS, 4, 1), 16: (BINS, 4, 1), 18: (BINS, 2, 1)}
         for i, p in exp.items():
             assert got[i] == p, f"layer {i}: {got[i]}"
         assert got[2] == (0, 0, 0) and got[19] == (0, 0, 0)  # pool, vmem

@@ -2607,11 +2607,12 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     } else {
         p.gather = (sh.C_out % 4 == 0 && sh.C_out > 64) ? (sh.C_out <= 128 ? 2 : 4) : 1;
         // an FC layer's pixels are its batch: where four c_out per lane would
-        // leave fewer waves than the device has SIMDs, one c_out per lane
-        // (4x the c_out blocks) is faster (VGG-16's 512 -> 512 FC at B=256:
-        // 512 waves, 0.072 -> 0.060 ms; the 2x2 conv L14's 2,048 keep four)
+        // leave fewer waves than the device has SIMDs, the pair gather (2x
+        // the c_out blocks, two events per load) is faster (VGG-16's 512 ->
+        // 512 FC at B=256: 512 waves, 0.072 ms; one c_out per lane, 0.055;
+        // the pair, 0.047; the 2x2 conv L14's 2,048 keep four)
         const int64_t simds = 4 * cu_count(ctx);
-        if (p.gather == 4 && sh.is_fc && simds > 0 && n_pixels(sh) * ((sh.C_out + 255) / 256) < simds) p.gather = 1;
+        if (p.gather == 4 && sh.is_fc && simds > 0 && n_pixels(sh) * ((sh.C_out + 255) / 256) < simds) p.gather = 2;
     }
     // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
     // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
