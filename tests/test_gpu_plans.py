@@ -244,13 +244,15 @@ def test_register_path_forced_matches_oracle(gpu_ctx_factory, case):
 def test_builtin_pixels_per_wave_follow_residency(gpu_ctx_factory):
     """VGG-16 at B=256: two pixels per wave exactly where one pixel per wave
     needs between one and two rounds of resident waves (the 4x4 layers,
-    8,192 waves) and two fit in one; one elsewhere."""
+    8,192 waves) and two fit in one; four on the one-chunk fused conv 0; one
+    elsewhere."""
     say("plans: VGG-16 B=256 pixels per wave from residency")
     w = models.vgg16()
     ctx = gpu_ctx_factory(w.consts)
     net = make_net(ctx, w, 256)
     try:
-        ppw = {i: net.get_plan(i)[2] for i in (3, 4, 6, 7, 8, 10, 11, 12, 14, 15, 16, 18)}
-        assert ppw == {3: 1, 4: 1, 6: 1, 7: 1, 8: 1, 10: 2, 11: 2, 12: 2, 14: 1, 15: 1, 16: 1, 18: 1}, ppw
+        ppw = {i: net.get_plan(i)[2] for i in (0, 1, 3, 4, 6, 7, 8, 10, 11, 12, 14, 15, 16, 18)}
+        # conv 0: the one-chunk fused kernel takes four pixels per wave at 2^18 pixels
+        assert ppw == {0: 4, 1: 1, 3: 1, 4: 1, 6: 1, 7: 1, 8: 1, 10: 2, 11: 2, 12: 2, 14: 1, 15: 1, 16: 1, 18: 1}, ppw
     finally:
         net.close()

@@ -2635,6 +2635,12 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     } else {
         const int64_t n_pix = n_pixels(sh);
         p.ppw = n_pix >= (INT64_C(1) << 20) ? 2 : 1;
+        // the one-chunk fused kernel (receptive field <= 64 elements) spends
+        // a large share of a pixel on the wave's set-up: four pixels per wave
+        // where that still leaves 16K waves (VGG-16's conv 0 at B=256:
+        // 0.295 -> 0.283 ms; the nine-chunk conv 1 gains nothing at 2 or 4)
+        if (p.path == VDTTFS_PATH_FUSED && !sh.is_fc && sh.K_h * sh.K_w * sh.C_in <= 64 && n_pix >= (INT64_C(1) << 16))
+            p.ppw = 4;
         if (p.ppw == 1 && p.path != VDTTFS_PATH_FUSED && p.path != VDTTFS_PATH_WINDOW) {
             // k_stream's residency (the fused and window kernels' is LDS-bound).
             // The rule keeps k_stream's figures (six waves per SIMD at four
