@@ -707,12 +707,13 @@ __global__ __launch_bounds__(1024) void k_culif_fc_rec(CRecArgs a) {
 //   k_fcsort_scatter  each input's j to its step's list, ranked within a
 //                     64-input chunk by a bit-ballot multisplit.
 // k_fc_currents then gives each (sample, step, 64 outputs) wave its list:
-// 32 rows gathered at a time (entries read one group ahead), added in list (= ascending j) order.  Scanning
+// 32 rows gathered at a time with the next 32 in flight (entries read 64 at a time, a window ahead), added in list
+// (= ascending j) order; the waves run step-major, so the long lists of the dense early steps start first.  Scanning
 // every input per step group instead left each wave about one gather per
 // 64-input chunk, a memory latency each.
 constexpr int kFcSeg = 2048;    // inputs per sort segment
 constexpr int kFcGroup = 32;    // rows gathered together
-constexpr int kFcListPad = 2 * kFcGroup;  // list entries readable past the end
+constexpr int kFcListPad = 6 * kFcGroup;  // list entries readable past the end (k_fc_currents' windows)
 
 __global__ __launch_bounds__(256) void k_fcsort_count(const float* __restrict__ x, int32_t* __restrict__ counts,
                                                       int N, int F, int T, int S) {
@@ -821,11 +822,13 @@ __global__ __launch_bounds__(256) void k_fc_currents(const int32_t* __restrict__
                                                      const float* __restrict__ W, float* __restrict__ cur,
                                                      int N, int T, int F, int out_f, int n_oblk, int w_bytes) {
     const int wave = uniform(threadIdx.x >> 6);
-    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (n, t, oblk)
+    // step-major: the dense early steps, whose lists are the longest (and
+    // bound the kernel's time), start first
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // (t, n, oblk)
     if (u >= (int64_t)N * T * n_oblk) return;          // uniform per wave
     const int ob = (int)(u % n_oblk);
-    const int t = (int)((u / n_oblk) % T);
-    const int64_t n = u / ((int64_t)n_oblk * T);
+    const int64_t n = (u / n_oblk) % N;
+    const int t = (int)(u / ((int64_t)n_oblk * N));
     const int lane = lane_id();
     const int o = ob * 64 + lane;
     const bool ok = o < out_f;
@@ -835,25 +838,43 @@ __global__ __launch_bounds__(256) void k_fc_currents(const int32_t* __restrict__
     const int voff = (ok ? o : 0) * 4;
     const int rowb = out_f * 4;
     float acc = 0.0f;
-    // list entries one group ahead of the gathers; the list is padded, so
-    // entries past `end` are read but never used
-    int jn[kFcGroup];
-#pragma unroll
-    for (int g = 0; g < kFcGroup; ++g) jn[g] = L[beg + g];
-    for (int i = beg; i < end; i += kFcGroup) {
-        int j[kFcGroup];
+    // two groups of gathers in flight: the next group's are issued before
+    // this group's are added.  List entries come 64 at a time, one per lane
+    // (a window, read one window ahead), and v_readlane hands each gather its
+    // row; the list is padded, so entries past `end` are read but never used
+    // (the last window read starts below end + 96)
+    static_assert(kFcGroup == 32, "two groups per 64-entry window");
+    int wcur = L[beg + lane];       // entries beg + 64k .. beg + 64k + 63
+    int wnxt = L[beg + 64 + lane];  // the window after it
+    auto issue = [&](int i, int win, int half, float (&w)[kFcGroup]) {
 #pragma unroll
         for (int g = 0; g < kFcGroup; ++g) {
-            j[g] = jn[g];
-            jn[g] = L[i + kFcGroup + g];
+            const int j = __builtin_amdgcn_readlane(win, 32 * half + g);
+            w[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, (i + g < end ? j : 0) * rowb, 0));
         }
-        float w[kFcGroup];
+    };
+    auto add = [&](int i, const float (&w)[kFcGroup]) {
+        if (i + kFcGroup <= end) {
 #pragma unroll
-        for (int g = 0; g < kFcGroup; ++g)
-            w[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, (i + g < end ? j[g] : 0) * rowb, 0));
+            for (int g = 0; g < kFcGroup; ++g) acc = acc + w[g];
+        } else {
 #pragma unroll
-        for (int g = 0; g < kFcGroup; ++g)
-            if (i + g < end) acc = acc + w[g];
+            for (int g = 0; g < kFcGroup; ++g)
+                if (i + g < end) acc = acc + w[g];
+        }
+    };
+    float w0[kFcGroup], w1[kFcGroup];
+    if (beg < end) issue(beg, wcur, 0, w0);
+    for (int i = beg; i < end; i += 2 * kFcGroup) {
+        issue(i + kFcGroup, wcur, 1, w1);
+        __builtin_amdgcn_sched_barrier(0);
+        add(i, w0);
+        if (i + kFcGroup >= end) break;
+        issue(i + 2 * kFcGroup, wnxt, 0, w0);
+        __builtin_amdgcn_sched_barrier(0);
+        add(i + kFcGroup, w1);
+        wcur = wnxt;
+        wnxt = L[i + 128 + lane];
     }
     if (ok) cur[(n * T + t) * out_f + o] = acc;
 }
