@@ -76,7 +76,8 @@ def test_bucketize_conv_and_fc(gpu_ctx_factory):
     T, delta = 64, 16
     ctx = gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=delta))
     rng = np.random.default_rng(32)
-    for (N, Cc, H, W) in [(2, 64, 5, 6), (1, 3, 7, 1), (3, 130, 2, 2)]:
+    # up to 4,096 sites run one wave per site, more one thread per site
+    for (N, Cc, H, W) in [(2, 64, 5, 6), (1, 3, 7, 1), (3, 130, 2, 2), (2, 5, 64, 40)]:
         x = spike_map(rng, N * Cc * H * W, T)
         cin, tin, off = oracle.culif_bucketize_nchw(x, N, Cc, H, W, T, delta)
         d_c, d_t, d_o = ctx.empty(cin.size, np.int32), ctx.empty(tin.size), ctx.empty(off.size, np.int32)
@@ -89,18 +90,21 @@ def test_bucketize_conv_and_fc(gpu_ctx_factory):
             n = off[s * OS + OS - 1]
             np.testing.assert_array_equal(gc[s * Cc:s * Cc + n], cin[s * Cc:s * Cc + n])
             np.testing.assert_array_equal(gt[s * Cc:s * Cc + n], tin[s * Cc:s * Cc + n])
-    N, F = 5, 1000
-    x = spike_map(rng, N * F, T)
-    cin, tin, off = oracle.culif_bucketize_fc(x, N, F, T, delta)
-    d_c, d_t, d_o = ctx.empty(cin.size, np.int32), ctx.empty(tin.size), ctx.empty(off.size, np.int32)
-    ctx.culif_bucketize_fc(ctx.to_device(x), N, F, d_c, d_t, d_o)
-    np.testing.assert_array_equal(d_o.download(), off)
-    OS = T // delta + 1
-    gc, gt = d_c.download(), d_t.download()
-    for n in range(N):
-        k = off[n * OS + OS - 1]
-        np.testing.assert_array_equal(gc[n * F:n * F + k], cin[n * F:n * F + k])
-        np.testing.assert_array_equal(gt[n * F:n * F + k], tin[n * F:n * F + k])
+    # FC inputs (one site per sample), with 4, 64 and 1 chunks
+    for d in (delta, 1, T):
+        c = ctx if d == delta else gpu_ctx_factory(vdttfs.task3_consts(T=T, delta=d))
+        N, F = 5, 1000
+        x = spike_map(rng, N * F, T)
+        cin, tin, off = oracle.culif_bucketize_fc(x, N, F, T, d)
+        d_c, d_t, d_o = c.empty(cin.size, np.int32), c.empty(tin.size), c.empty(off.size, np.int32)
+        c.culif_bucketize_fc(c.to_device(x), N, F, d_c, d_t, d_o)
+        np.testing.assert_array_equal(d_o.download(), off)
+        OS = T // d + 1
+        gc, gt = d_c.download(), d_t.download()
+        for n in range(N):
+            k = off[n * OS + OS - 1]
+            np.testing.assert_array_equal(gc[n * F:n * F + k], cin[n * F:n * F + k])
+            np.testing.assert_array_equal(gt[n * F:n * F + k], tin[n * F:n * F + k])
 
 
 @pytest.mark.parametrize("delta", [8, 32])

@@ -12,7 +12,8 @@
 //                      output layout by strides (NCHW for the drop-in, NHWC
 //                      for the engine).
 //  k_culif_bucketize   k_bucketize_conv / k_bucketize_fc (T3V:70-106) in the
-//                      reference layout: one thread per site, counters in LDS.
+//                      reference layout: one thread per site, counters in LDS
+//                      (k_culif_bucketize_wave: a wave per site, for few sites).
 //  k_culif_generic     conv_bucketed_early / fc2_bucketed_early (T3V:109-143,
 //                      203-225) over the reference layout, one thread per
 //                      neuron (the drop-in path and the engine's small FC).
@@ -457,6 +458,63 @@ __global__ __launch_bounds__(kCBktThreads) void k_culif_bucketize(CBktArgs a) {
             const int p = my[(tb / a.D) * kCBktThreads]++;
             dc[p] = c;
             dt[p] = tf;
+        }
+    }
+}
+
+// Few sites (an FC layer's sites are its samples, one thread each above):
+// one wave per site, 64 elements a step.  Ranks within a chunk come from one
+// ballot per chunk the step holds, lane k keeps chunk k's count (NC <= 64);
+// the elements are read twice (count, then place).  Same output as
+// k_culif_bucketize.
+constexpr int64_t kCBktWaveMaxSites = 4096;
+
+__global__ __launch_bounds__(256) void k_culif_bucketize_wave(CBktArgs a) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int64_t s = (int64_t)blockIdx.x * 4 + wave;
+    if (s >= a.n_sites) return;  // uniform per wave; no barriers below
+    const int lane = lane_id();
+    const int64_t base = (s / a.HW) * (int64_t)a.C * a.HW + s % a.HW;
+    const uint64_t lt = lanemask_lt();
+    auto chunk_of = [&](int c, float& tf) {
+        tf = c < a.C ? a.in[base + (int64_t)c * a.HW] : kInfTime;
+        const int tb = culif_bin(tf, a.T);
+        return tb >= 0 ? tb / a.D : -1;
+    };
+    int cnt = 0;  // lane k: events of chunk k
+    for (int c0 = 0; c0 < a.C; c0 += 64) {
+        float tf;
+        const int k = chunk_of(c0 + lane, tf);
+        uint64_t pending = __ballot(k >= 0);
+        while (pending) {
+            const int kk = __builtin_amdgcn_readlane(k, __builtin_ctzll(pending));
+            const uint64_t m = __ballot(k == kk);
+            if (lane == kk) cnt += __popcll(m);
+            pending &= ~m;
+        }
+    }
+    const int OS = a.NC + 1;
+    const int incl = wave_incl_scan(cnt);  // lanes >= NC hold 0
+    int pos = incl - cnt;                  // lane k < NC: chunk k's first position
+    if (lane < a.NC) a.off[s * OS + lane] = pos;
+    if (lane == a.NC - 1) a.off[s * OS + a.NC] = incl;
+    int32_t* dc = a.cin + s * a.C;
+    float* dt = a.tin + s * a.C;
+    for (int c0 = 0; c0 < a.C; c0 += 64) {
+        float tf;
+        const int k = chunk_of(c0 + lane, tf);
+        uint64_t pending = __ballot(k >= 0);
+        while (pending) {
+            const int kk = __builtin_amdgcn_readlane(k, __builtin_ctzll(pending));
+            const uint64_t m = __ballot(k == kk);
+            const int start = __builtin_amdgcn_readlane(pos, kk);
+            if (k == kk) {
+                const int p = start + __popcll(m & lt);
+                dc[p] = c0 + lane;
+                dt[p] = tf;
+            }
+            if (lane == kk) pos += __popcll(m);
+            pending &= ~m;
         }
     }
 }
@@ -1011,6 +1069,11 @@ int launch_culif_bucketize(vdttfs_ctx* ctx, const float* in, int64_t n_sites, in
                          kCBktMaxChunks);
     if (n_sites <= 0 || C <= 0 || HW <= 0) return set_error(VDTTFS_E_INVALID, "culif bucketize: bad shape");
     CBktArgs a{in, cin, tin, off, n_sites, C, HW, ctx->c.T, ctx->c.delta, NC};
+    if (n_sites <= kCBktWaveMaxSites) {  // a thread per site would leave the device idle
+        hipLaunchKernelGGL(k_culif_bucketize_wave, dim3((unsigned)((n_sites + 3) / 4)), dim3(256), 0, ctx->stream, a);
+        VD_HIP(hipGetLastError());
+        return VDTTFS_OK;
+    }
     const int64_t blocks = (n_sites + kCBktThreads - 1) / kCBktThreads;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "culif bucketize: grid too large");
     hipLaunchKernelGGL(k_culif_bucketize, dim3((unsigned)blocks), dim3(kCBktThreads), 0, ctx->stream, a);
