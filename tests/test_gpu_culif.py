@@ -258,6 +258,47 @@ def test_culif_engine_conv1_inputs_and_weights(gpu_ctx_factory):
             np.testing.assert_array_equal(pred, rpred)
 
 
+@pytest.mark.parametrize("decay,th", [(0.9, 1.0), (0.85, 0.6), (-0.8, 0.3), (0.95, 1.0)])
+def test_culif_engine_tail_steps(gpu_ctx_factory, decay, th):
+    """Slow decays keep V rising long after a pixel's last input, so neurons
+    fire in the input-free steps the fused conv streams close after the list
+    ends (C_in 64 and 128, C_out 64 and 128, decay < 0 too): every layer
+    equals the oracle, and for decay > 0 some spikes come after the pixel's
+    last input."""
+    say(f"culif engine tail steps decay={decay} th={th}")
+    H = W = 16
+    k = models.kaiming
+    L = [vdttfs.CulifLayerSpec(vdttfs.CULIF_RAW_CONV, 2, H, W, 64, k(9, 0, (64, 2, 3, 3), 18), None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 64, H, W, 128, k(9, 1, (128, 64, 3, 3), 576), None, decay, th),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 128, H, W, 64, k(9, 2, (64, 128, 3, 3), 1152), None, decay, th),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_CONV, 64, H, W, 128, k(9, 3, (128, 64, 3, 3), 576), None, decay, th),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_POOL, 128, H, W, 128, None, None, 0.5, 1.0),
+         vdttfs.CulifLayerSpec(vdttfs.CULIF_FC, 128 * 8 * 8, 1, 1, 11, k(9, 4, (11, 128 * 64), 128 * 64), None,
+                               0.5, 1.0)]
+    w = models.CulifWorkload("tail", vdttfs.task3_consts(T=64, delta=32), L, (2, H, W), 11, 9,
+                             meta={"decay": 0.5, "th": 1.0, "density": 0.05, "sigma_px": 4.0,
+                                   "vmax_px_per_step": 0.5})
+    B = 2
+    ev = models.dvs_events(w, B)
+    outs, pred = run_engine(gpu_ctx_factory(w.consts), w, B, ev)
+    ref, rpred = oracle.culif_net_forward(w.layers, ev, B, 64, 32)
+    tail_fires = 0
+    for i, (g, o) in enumerate(zip(outs, ref)):
+        o = o.reshape(g.shape)
+        assert np.array_equal(g, o), f"layer {i} differs at {np.flatnonzero(g != o)[:8]}"
+        if i in (1, 2, 3):  # spikes after the last input step of the pixel's 3x3 field
+            x = ref[i - 1].reshape(B, -1, H, W)
+            step = np.where((x >= 0) & (x < 64), np.floor(x), -1).max(axis=1)
+            last = np.full((B, H + 2, W + 2), -1.0)
+            last[:, 1:-1, 1:-1] = step
+            last = np.max([last[:, dy:dy + H, dx:dx + W] for dy in range(3) for dx in range(3)], axis=0)
+            y = o.reshape(B, -1, H, W)
+            tail_fires += int(np.sum((y < INF) & (y > last[:, None])))
+    np.testing.assert_array_equal(pred, rpred)
+    if decay > 0:  # an alternating I (decay < 0) rarely lifts V after its last input
+        assert tail_fires > 0
+
+
 def test_culif_config4_full(gpu_ctx_factory):
     """Config 4 at full size (2x128x128, T=64, B=64): the first 16 samples
     equal the oracle at every layer; Delta in {16, 64} gives bit-identical

@@ -94,6 +94,9 @@ int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const 
                          int is_fc);
 
 // CuLIF neuron constants (T3V:24-27 per layer; one decay and threshold).
+// Integration with a CuLIF neuron adds weights unscaled (the reference's
+// acc + w): its callers pass an all-ones alpha LUT, and the fused kernel
+// (k_stream_quad) does not read it.
 struct CulifNeuron {
     float decay, th;
 };

@@ -1112,8 +1112,10 @@ __host__ __device__ inline int quad_list_entries(int nel_max, int T) {
     const int e = nel_max + kListPad > T ? nel_max + kListPad : T;
     return (e + 3) & ~3;
 }
-__host__ __device__ inline int quad_wave_words(int nel_max, int T) {
-    return (2 * quad_list_entries(nel_max, T) + (T + 1) + T + 2 * 9 + 3) & ~3;
+// LDS words of one k_stream_quad wave: rows, alphas (not for the CuLIF
+// neuron, whose inputs are unscaled), bin starts, cursors, tap table
+__host__ __device__ inline int quad_wave_words(int nel_max, int T, bool alphas = true) {
+    return ((alphas ? 2 : 1) * quad_list_entries(nel_max, T) + (T + 1) + T + 2 * 9 + 3) & ~3;
 }
 
 // Packed event of quad_build: bin (bits 0..6, 0x7F: no event), decay-LUT
@@ -1126,7 +1128,7 @@ __host__ __device__ inline int quad_wave_words(int nel_max, int T) {
 // SIMD, CuLIF-7 conv2 4.46 -> 4.08 ms), and so do the 18-chunk builds (120
 // -> 79 VGPRs); the VALU-bound 9-chunk LUT kernels keep the hoisted values
 // (VGG-16 conv 1 +0.7% with it).
-template <int NB, bool OPAQUE>
+template <int NB, bool OPAQUE, bool ALPHA>
 __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
                                           int* alph, int* bs) {
     constexpr int KMAX = 9;
@@ -1248,8 +1250,10 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     wave_sync();
     // pass 2: event (chunk c, rank) of bin b goes to cur[b] + rank
     float al[NB];
+    if constexpr (ALPHA) {
 #pragma unroll
-    for (int c = 0; c < NB; ++c) al[c] = a.alpha[(pk[c] >> 7) & 0x7F];  // index 0 where no event
+        for (int c = 0; c < NB; ++c) al[c] = a.alpha[(pk[c] >> 7) & 0x7F];  // index 0 where no event
+    }
 #pragma unroll
     for (int c = 0; c < NB; ++c) {
         if (c < n_chunks) {  // uniform
@@ -1258,7 +1262,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             if (b != 0x7F) {
                 const int pos = cur[b] + rank;
                 rows[pos] = (int)__umul24((unsigned)pk[c] >> 21, (unsigned)a.rowbytes);  // row < 2^11, <= 512 B
-                alph[pos] = __float_as_int(al[c]);
+                if constexpr (ALPHA) alph[pos] = __float_as_int(al[c]);
             }
             wave_sync();
             if ((pk[c] >> 20) & 1) cur[b] += rank + 1;
@@ -1269,7 +1273,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     if (lane < kListPad) {
         const int z = vzero();
         rows[total + lane] = z;
-        alph[total + lane] = z;
+        if constexpr (ALPHA) alph[total + lane] = z;
     }
     return total;
 }
@@ -1284,11 +1288,13 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
     typedef float f4 __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) int lds_words[];
     const int wave = uniform(threadIdx.x >> 6);
+    // the CuLIF neuron adds its weights unscaled (alpha = 1, the reference's
+    // acc + w), so its lists hold rows only
     const int E = quad_list_entries(nel_max, a.T);
-    int* region = lds_words + wave * quad_wave_words(nel_max, a.T);
+    int* region = lds_words + wave * quad_wave_words(nel_max, a.T, !CULIF);
     int* rows = region;
-    int* alph = region + E;
-    int* bs = alph + E;
+    int* alph = region + E;  // not used by the CuLIF neuron
+    int* bs = region + (CULIF ? 1 : 2) * E;
     int* cur = bs + a.T + 1;
     int* kinfo = cur + a.T;
     const int lane = lane_id();
@@ -1317,7 +1323,7 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)quad_build<NB, (CULIF || NB > 9)>(m, pix, cur, kinfo, rows, alph, bs);
+        (void)quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
         const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
@@ -1335,7 +1341,7 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
         int bend = __builtin_amdgcn_readlane(v_end, 0);
         // GEO 2 reads a group's alphas when it consumes the group rather than
         // with its loads: 8 fewer registers in flight (5 waves per SIMD, not 4)
-        constexpr bool AL_AHEAD = GEO == 4;
+        constexpr bool AL_AHEAD = GEO == 4 && !CULIF;
         struct Raw {
             u4 x[LPG];
             f4 al[AL_AHEAD ? 2 : 1];
@@ -1427,31 +1433,36 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
                     w[2 * k + 1][OWN - 1] = __uint_as_float(c3);
                 }
             }
-            f4 a0, a1;
-            if constexpr (AL_AHEAD) {
-                a0 = g.al[0];
-                a1 = g.al[AL_AHEAD ? 1 : 0];
-            } else {
-                a0 = *reinterpret_cast<const f4*>(alph + j);
-                a1 = *reinterpret_cast<const f4*>(alph + j + 4);
-            }
+            if constexpr (!CULIF) {
+                f4 a0, a1;
+                if constexpr (AL_AHEAD) {
+                    a0 = g.al[0];
+                    a1 = g.al[AL_AHEAD ? 1 : 0];
+                } else {
+                    a0 = *reinterpret_cast<const f4*>(alph + j);
+                    a1 = *reinterpret_cast<const f4*>(alph + j + 4);
+                }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                al[i] = a0[i];
-                al[4 + i] = a1[i];
+                for (int i = 0; i < 4; ++i) {
+                    al[i] = a0[i];
+                    al[4 + i] = a1[i];
+                }
             }
+            // event i: fma(w, alpha, acc); the CuLIF neuron's acc + w
+            auto integ = [&](int i) {
+#pragma unroll
+                for (int v = 0; v < OWN; ++v)
+                    acc[v] = CULIF ? acc[v] + w[i][v] : __builtin_fmaf(w[i][v], al[i], acc[v]);
+            };
             if (bend >= j + 8) {  // all eight in the open bin
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-#pragma unroll
-                    for (int v = 0; v < OWN; ++v) acc[v] = __builtin_fmaf(w[i][v], al[i], acc[v]);
+                for (int i = 0; i < 8; ++i) integ(i);
                 return false;
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (bend <= j + i && close_to(j + i)) return true;
-#pragma unroll
-                for (int v = 0; v < OWN; ++v) acc[v] = __builtin_fmaf(w[i][v], al[i], acc[v]);
+                integ(i);
             }
             return false;
         };
@@ -2804,7 +2815,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
             // 4.08 -> 3.31 ms with 1 (4.23 with 2), VGG conv 1 -0.8% and
             // conv 2 -1.4% with 1, conv 0 +1.4% with 1
             const int qw = (epi != 2 && nel_max <= 64) ? kQuadWaves : 1;
-            const size_t qlds = (size_t)qw * quad_wave_words(nel_max, m.T) * sizeof(int);
+            const size_t qlds = (size_t)qw * quad_wave_words(nel_max, m.T, culif == nullptr) * sizeof(int);
             const int64_t qblocks = (n_pix + qw * a.ppw - 1) / (qw * a.ppw);
 #define VD_LAUNCH_QUAD(G, NB, L)                                                                           \
     hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)qblocks), dim3(64 * qw), qlds, \
