@@ -1110,12 +1110,19 @@ __global__ __launch_bounds__(256) void k_stream_dense(DenseMergeArgs m, StreamAr
 // T cursors, the tap table.
 __host__ __device__ inline int quad_list_entries(int nel_max, int T) {
     const int e = nel_max + kListPad > T ? nel_max + kListPad : T;
-    return (e + 3) & ~3;
+    return (e + 7) & ~7;
 }
-// LDS words of one k_stream_quad wave: rows, alphas (not for the CuLIF
-// neuron, whose inputs are unscaled), bin starts, cursors, tap table
+// LDS words of one k_stream_quad wave: the list, bin starts, cursors, tap
+// table.  With alphas an entry is a 16-bit row index and an alpha (6 bytes);
+// the CuLIF neuron's inputs are unscaled, so its entries are row byte offsets
+// (4 bytes).  Either way the list region holds pass 1's 2T mask words before
+// the cursors (entries >= T).
+__host__ __device__ inline int quad_list_words(int nel_max, int T, bool alphas) {
+    const int E = quad_list_entries(nel_max, T);
+    return alphas ? E / 2 + E : E;
+}
 __host__ __device__ inline int quad_wave_words(int nel_max, int T, bool alphas = true) {
-    return ((alphas ? 2 : 1) * quad_list_entries(nel_max, T) + (T + 1) + T + 2 * 9 + 3) & ~3;
+    return (quad_list_words(nel_max, T, alphas) + (T + 1) + T + 2 * 9 + 3) & ~3;
 }
 
 // Packed event of quad_build: bin (bits 0..6, 0x7F: no event), decay-LUT
@@ -1261,7 +1268,10 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int rank = (pk[c] >> 14) & 0x3F;
             if (b != 0x7F) {
                 const int pos = cur[b] + rank;
-                rows[pos] = (int)__umul24((unsigned)pk[c] >> 21, (unsigned)a.rowbytes);  // row < 2^11, <= 512 B
+                if constexpr (ALPHA)
+                    reinterpret_cast<unsigned short*>(rows)[pos] = (unsigned short)((unsigned)pk[c] >> 21);  // < 2^11
+                else
+                    rows[pos] = (int)__umul24((unsigned)pk[c] >> 21, (unsigned)a.rowbytes);  // row < 2^11, <= 512 B
                 if constexpr (ALPHA) alph[pos] = __float_as_int(al[c]);
             }
             wave_sync();
@@ -1272,7 +1282,10 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     // zeroed tail: the stream reads up to 16 entries past the end
     if (lane < kListPad) {
         const int z = vzero();
-        rows[total + lane] = z;
+        if constexpr (ALPHA)
+            reinterpret_cast<unsigned short*>(rows)[total + lane] = (unsigned short)z;
+        else
+            rows[total + lane] = z;
         if constexpr (ALPHA) alph[total + lane] = z;
     }
     return total;
@@ -1288,13 +1301,15 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
     typedef float f4 __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) int lds_words[];
     const int wave = uniform(threadIdx.x >> 6);
-    // the CuLIF neuron adds its weights unscaled (alpha = 1, the reference's
-    // acc + w), so its lists hold rows only
+    // entries: 16-bit row indices and alphas; the CuLIF neuron adds its
+    // weights unscaled (alpha = 1, the reference's acc + w), so its lists
+    // hold row byte offsets only
     const int E = quad_list_entries(nel_max, a.T);
     int* region = lds_words + wave * quad_wave_words(nel_max, a.T, !CULIF);
     int* rows = region;
-    int* alph = region + E;  // not used by the CuLIF neuron
-    int* bs = region + (CULIF ? 1 : 2) * E;
+    const unsigned short* rows16 = reinterpret_cast<const unsigned short*>(region);
+    int* alph = region + E / 2;  // not used by the CuLIF neuron
+    int* bs = region + quad_list_words(nel_max, a.T, !CULIF);
     int* cur = bs + a.T + 1;
     int* kinfo = cur + a.T;
     const int lane = lane_id();
@@ -1349,8 +1364,9 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
         auto load = [&](int j, Raw& g) {
 #pragma unroll
             for (int k = 0; k < LPG; ++k) {
-                const int row = rows[j + GEO * k + q];
-                g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, row + voff, 0, 0);
+                const int off = CULIF ? rows[j + GEO * k + q] + voff
+                                      : (int)__umul24((unsigned)rows16[j + GEO * k + q], (unsigned)m.rowbytes) + voff;
+                g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
             }
             if constexpr (AL_AHEAD) {
                 g.al[0] = *reinterpret_cast<const f4*>(alph + j);
