@@ -258,13 +258,14 @@ def test_culif_engine_conv1_inputs_and_weights(gpu_ctx_factory):
             np.testing.assert_array_equal(pred, rpred)
 
 
-@pytest.mark.parametrize("decay,th", [(0.9, 1.0), (0.85, 0.6), (-0.8, 0.3), (0.95, 1.0)])
+@pytest.mark.parametrize("decay,th", [(0.9, 1.0), (0.85, 0.6), (-0.8, 0.3), (0.95, 1.0), (0.5, 0.0), (0.5, -0.5)])
 def test_culif_engine_tail_steps(gpu_ctx_factory, decay, th):
     """Slow decays keep V rising long after a pixel's last input, so neurons
     fire in the input-free steps the fused conv streams close after the list
     ends (C_in 64 and 128, C_out 64 and 128, decay < 0 too): every layer
-    equals the oracle, and for decay > 0 some spikes come after the pixel's
-    last input."""
+    equals the oracle, and for decay > 0 and th > 0 some spikes come after
+    the pixel's last input.  Pixels with no input skip their steps: with
+    th <= 0 their neurons fire at step 0, otherwise never."""
     say(f"culif engine tail steps decay={decay} th={th}")
     H = W = 16
     k = models.kaiming
@@ -275,8 +276,9 @@ def test_culif_engine_tail_steps(gpu_ctx_factory, decay, th):
          vdttfs.CulifLayerSpec(vdttfs.CULIF_POOL, 128, H, W, 128, None, None, 0.5, 1.0),
          vdttfs.CulifLayerSpec(vdttfs.CULIF_FC, 128 * 8 * 8, 1, 1, 11, k(9, 4, (11, 128 * 64), 128 * 64), None,
                                0.5, 1.0)]
+    # th <= 0: sparser events, so that some conv2 pixels see no input at all
     w = models.CulifWorkload("tail", vdttfs.task3_consts(T=64, delta=32), L, (2, H, W), 11, 9,
-                             meta={"decay": 0.5, "th": 1.0, "density": 0.05, "sigma_px": 4.0,
+                             meta={"decay": 0.5, "th": 1.0, "density": 0.05 if th > 0 else 0.01, "sigma_px": 4.0,
                                    "vmax_px_per_step": 0.5})
     B = 2
     ev = models.dvs_events(w, B)
@@ -295,8 +297,15 @@ def test_culif_engine_tail_steps(gpu_ctx_factory, decay, th):
             y = o.reshape(B, -1, H, W)
             tail_fires += int(np.sum((y < INF) & (y > last[:, None])))
     np.testing.assert_array_equal(pred, rpred)
-    if decay > 0:  # an alternating I (decay < 0) rarely lifts V after its last input
+    if decay > 0 and th > 0:  # an alternating I (decay < 0) rarely lifts V after its last input
         assert tail_fires > 0
+    if th <= 0:  # conv2 pixels whose 3x3 field has no input at all (their neurons fire at step 0)
+        x = ref[0].reshape(B, -1, H, W)
+        p = np.zeros((B, H + 2, W + 2), bool)
+        p[:, 1:-1, 1:-1] = ((x >= 0) & (x < 64)).any(axis=1)
+        field = np.max([p[:, dy:dy + H, dx:dx + W] for dy in range(3) for dx in range(3)], axis=0)
+        assert np.any(~field)
+        assert np.all(ref[1].reshape(B, -1, H, W).transpose(0, 2, 3, 1)[~field] == 0)
 
 
 def test_culif_config4_full(gpu_ctx_factory):

@@ -1338,8 +1338,17 @@ __global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs 
     for (int pq = 0; pq < a.ppw; ++pq) {
         const int64_t pix = pix0 + pq;
         if (pix >= a.n_pix) return;  // uniform per wave
-        (void)quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
+        const int total = quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
         wave_sync();
+        if (CULIF && total == 0) {  // uniform
+            // no input: I and V stay 0, so a neuron fires at step 0 when
+            // 0 >= th (T3V:50-62) and never otherwise; the 64 steps are skipped
+            const float o = 0.0f >= a.th ? 0.0f : kInfTime;
+#pragma unroll
+            for (int v = 0; v < OWN; ++v)
+                if (ok[v]) out[pix * a.C_out + co + v] = o;
+            continue;
+        }
         const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
         int res[OWN];  // bins closed with the neuron still alive: its spike bin once it fired
