@@ -1134,7 +1134,9 @@ __host__ __device__ inline int quad_wave_words(int nel_max, int T, bool alphas =
 // takes it (k_stream_quad<2, 9, true>: 91 -> 67 VGPRs, 5 -> 7 waves per
 // SIMD, CuLIF-7 conv2 4.46 -> 4.08 ms), and so do the 18-chunk builds (120
 // -> 79 VGPRs); the VALU-bound 9-chunk LUT kernels keep the hoisted values
-// (VGG-16 conv 1 +0.7% with it).
+// (VGG-16 conv 1 +0.7% with it).  ALPHA: entries are 16-bit rows beside
+// alphas (the LUT neuron); without, row byte offsets (the CuLIF neuron), and
+// a field without events returns 0 before the passes.
 template <int NB, bool OPAQUE, bool ALPHA>
 __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
                                           int* alph, int* bs) {
@@ -1208,6 +1210,15 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             pk[c] = ev ? (rw[c] << 21) | (ai << 7) | tb : 0x7F;
             __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: fewer live registers
         }
+    }
+    if constexpr (!ALPHA) {
+        // the CuLIF kernel skips the stream of a pixel without events, so a
+        // silent field returns here, before the passes (bs and the list are
+        // not written)
+        bool any = false;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) any |= (pk[c] & 0x7F) != 0x7F;
+        if (__ballot(any) == 0) return 0;
     }
     // pass 1: ranks within each chunk's bins, counts per bin
     const uint64_t lt = lanemask_lt();
