@@ -96,9 +96,12 @@ int launch_integrate_ref(vdttfs_ctx* ctx, float* out, const int32_t* cin, const 
 // CuLIF neuron constants (T3V:24-27 per layer; one decay and threshold).
 // Integration with a CuLIF neuron adds weights unscaled (the reference's
 // acc + w): its callers pass an all-ones alpha LUT, and the fused kernel
-// (k_stream_quad) does not read it.
+// (k_stream_quad) does not read it.  fired: nullable, one byte per input
+// site (NHWC pixel of the input map), nonzero exactly where some channel of
+// the site holds a spike; the fused build then skips silent fields unread.
 struct CulifNeuron {
     float decay, th;
+    const uint8_t* fired = nullptr;
 };
 
 struct IntegShape {
@@ -163,9 +166,11 @@ int check_culif_consts(const vdttfs_ctx* ctx);
 // conv1_raw from per-site masks of nonzero steps (finite weights only; mask
 // [N*C_in*H*W][ceil(T/64)] uint64, nonbin the same shape in uint32).
 bool culif_conv1_mask_ok(int C_in);
+// fired: nullable [N*H*W] bytes, 1 where some neuron of the pixel fired
+// (C_out <= 64).
 int launch_culif_conv1_mask(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N, int C_in,
                             int C_out, int H, int Wd, int nhwc_out, float decay, float th, uint64_t* mask,
-                            uint32_t* nonbin);
+                            uint32_t* nonbin, uint8_t* fired = nullptr);
 int launch_culif_conv1_raw(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N,
                            int C_in, int C_out, int H, int Wd, int nhwc_out, float decay, float th);
 // Reference layout; site s = (n, hw), element c at (n*C + c)*HW + hw (FC: HW = 1).

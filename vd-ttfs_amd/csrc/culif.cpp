@@ -68,6 +68,7 @@ struct vdttfs_culif_net {
     FcSortScratch fcs{};           // FC_REC inputs sorted by arrival step
     uint64_t* raw_mask = nullptr;  // conv1_raw event masks (finite weights, C_in <= 4)
     uint32_t* raw_nonbin = nullptr;
+    uint8_t* raw_fired = nullptr;  // per conv1 output pixel: some neuron fired (mask kernel, C_out <= 64)
     bool timing = false;
     std::vector<hipEvent_t> pool;      // 2 per layer per timed forward
     size_t pool_used = 0;
@@ -89,7 +90,7 @@ void destroy_impl(vdttfs_culif_net* net) {
             if (q) (void)hipFree(q);
     for (void* q : {(void*)net->ones, (void*)net->ev, (void*)net->off, (void*)net->list,
                     (void*)net->bstart, (void*)net->rcin, (void*)net->rtin, (void*)net->roff,
-                    (void*)net->flat, (void*)net->cur, (void*)net->raw_mask, (void*)net->raw_nonbin,
+                    (void*)net->flat, (void*)net->cur, (void*)net->raw_mask, (void*)net->raw_nonbin, (void*)net->raw_fired,
                     (void*)net->fcs.counts, (void*)net->fcs.offs, (void*)net->fcs.binstart, (void*)net->fcs.list})
         if (q) (void)hipFree(q);
     delete net;
@@ -177,6 +178,8 @@ int create_impl(vdttfs_culif_net* net, const vdttfs_culif_layer* layers, int n) 
                     const size_t units = (size_t)B * d.C_in * d.H_in * d.W_in * ((T + 63) / 64);
                     VD_TRY(dalloc((void**)&net->raw_mask, units * sizeof(uint64_t)));
                     VD_TRY(dalloc((void**)&net->raw_nonbin, units * sizeof(uint32_t)));
+                    if (d.C_out <= 64)
+                        VD_TRY(dalloc((void**)&net->raw_fired, (size_t)B * d.H_in * d.W_in));
                 }
                 break;
             }
@@ -272,12 +275,13 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
     vdttfs_ctx* ctx = net->ctx;
     const int B = net->B;
     const float* cur = nullptr;
+    const uint8_t* cur_fired = nullptr;  // per-site flags of `cur` (conv1's mask kernel), or null
     int cur_nhwc = 0, cH = 1, cW = 1, cC = 0;
     const bool timed = net->timing && !counts;
     for (size_t i = 0; i < net->L.size(); ++i) {
         CLayer& l = net->L[i];
         const vdttfs_culif_layer& d = l.d;
-        CulifNeuron nrn{d.decay, d.th};
+        CulifNeuron nrn{d.decay, d.th, d.kind == VDTTFS_CULIF_CONV ? cur_fired : nullptr};
         hipEvent_t e0 = nullptr, e1 = nullptr;  // consecutive pool slots 2k, 2k+1
         if (timed) VD_TRY(mark(net, &e0));
         const bool count_here = counts && d.kind == VDTTFS_CULIF_CONV;
@@ -295,7 +299,8 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
             case VDTTFS_CULIF_RAW_CONV:
                 if (net->raw_mask)
                     VD_TRY(launch_culif_conv1_mask(ctx, d_data, l.out, l.W, B, d.C_in, d.C_out, d.H_in,
-                                                   d.W_in, 1, d.decay, d.th, net->raw_mask, net->raw_nonbin));
+                                                   d.W_in, 1, d.decay, d.th, net->raw_mask, net->raw_nonbin,
+                                                   net->raw_fired));
                 else
                     VD_TRY(launch_culif_conv1_raw(ctx, d_data, l.out, l.W, B, d.C_in, d.C_out, d.H_in,
                                                   d.W_in, 1, d.decay, d.th));
@@ -351,6 +356,7 @@ int forward_impl(vdttfs_culif_net* net, const float* d_data, int32_t* d_pred, ui
             net->pending_layer.push_back((int)i);
         }
         cur = l.out;
+        cur_fired = (d.kind == VDTTFS_CULIF_RAW_CONV && net->raw_mask) ? net->raw_fired : nullptr;
         cur_nhwc = l.nhwc;
         cH = l.H_out;
         cW = l.W_out;

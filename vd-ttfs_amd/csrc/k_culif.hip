@@ -42,6 +42,7 @@ struct RawArgs {
     int C_in, C_out, H, Wd, T, n_cblk;
     int64_t sN, sC, sY, sX;  // output strides
     float decay, th;
+    uint8_t* fired;     // k_culif_conv1_mask, one c_out block: per pixel, 1 when some neuron fired (or null)
 };
 
 // Tiled variant for few input channels (C_in <= kTileMaxCin): a block of 4
@@ -317,7 +318,8 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
         };
         float I = 0.0f, V = 0.0f;
         int lived = 0;  // steps survived: the spike step once the lane fired
-        uint64_t alive = __ballot(ok);
+        const uint64_t all = __ballot(ok);
+        uint64_t alive = all;
         for (int tb = 0; tb < nblk && alive; ++tb) {
             // lane k's tap: its mask of steps with input, and whether a
             // nonzero input is not 1.0
@@ -403,6 +405,7 @@ __global__ __launch_bounds__(256) void k_culif_conv1_mask(RawArgs a, const uint6
         if (ok)
             a.out[(int64_t)n * a.sN + (int64_t)c * a.sC + (int64_t)y * a.sY + (int64_t)x * a.sX] =
                 __builtin_amdgcn_inverse_ballot_w64(alive) ? kInfTime : (float)lived;
+        if (a.fired && lane == 0) a.fired[pix] = (all & ~alive) != 0 ? 1 : 0;
     }
 }
 
@@ -1023,13 +1026,15 @@ bool culif_conv1_mask_ok(int C_in) { return C_in >= 1 && C_in <= kMaskMaxCin; }
 
 int launch_culif_conv1_mask(vdttfs_ctx* ctx, const float* data, float* out, const float* W, int N, int C_in,
                             int C_out, int H, int Wd, int nhwc_out, float decay, float th, uint64_t* mask,
-                            uint32_t* nonbin) {
+                            uint32_t* nonbin, uint8_t* fired) {
     VD_TRY(check_culif_consts(ctx));
     if (N <= 0 || C_in <= 0 || C_out <= 0 || H <= 0 || Wd <= 0)
         return set_error(VDTTFS_E_INVALID, "culif_conv1_mask: non-positive shape");
     if (!culif_conv1_mask_ok(C_in))
         return set_error(VDTTFS_E_UNSUPPORTED, "culif_conv1_mask: C_in %d > %d", C_in, kMaskMaxCin);
-    const RawArgs a = raw_args(ctx, data, out, W, N, C_in, C_out, H, Wd, nhwc_out, decay, th);
+    RawArgs a = raw_args(ctx, data, out, W, N, C_in, C_out, H, Wd, nhwc_out, decay, th);
+    if (fired && a.n_cblk != 1) return set_error(VDTTFS_E_INVALID, "culif_conv1_mask: fired flags need C_out <= 64");
+    a.fired = fired;
     const int nblk = (a.T + 63) / 64;
     const int64_t sites = (int64_t)N * C_in * H * Wd;
     if (a.n_pix >= (INT64_C(1) << 31) || sites >= (INT64_C(1) << 31))

@@ -205,6 +205,7 @@ struct DenseMergeArgs {
     int H_in, W_in, C_in, H_out, W_out, K_h, K_w, pad_h, pad_w;
     int rowbytes;          // C_out * 4
     float inv_cin;         // 1 / C_in
+    const uint8_t* fired;  // CuLIF: per input site, nonzero where a channel spiked (or null)
     FastDiv div_w, div_h;  // by W_out, H_out (n_pix < 2^31)
     int in_bytes;          // bytes of `in` (k_stream_quad: below 2^31), else 0
 };
@@ -1158,6 +1159,11 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             col = (img * a.H_in + hi) * a.W_in + wi;
         }
         const uint64_t m = __ballot(v);
+        if constexpr (!ALPHA) {
+            // the producer's per-site flags: a field of silent sites has no
+            // event, and the CuLIF kernel skips the pixel's stream
+            if (a.fired && __ballot(v && a.fired[col] != 0) == 0) return 0;
+        }
         nk = uniform(__popcll(m));
         if (v) {
             const int slot = __popcll(m & lanemask_lt());
@@ -2819,6 +2825,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.pad_w = sh.pad_w;
     m.rowbytes = sh.C_out * 4;
     m.inv_cin = 1.0f / (float)sh.C_in;
+    m.fired = culif ? culif->fired : nullptr;
     if (n_pix >= (INT64_C(1) << 31)) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: 2^31 output pixels or more");
     m.div_w = make_fastdiv(sh.W_out);
     m.div_h = make_fastdiv(sh.H_out);
