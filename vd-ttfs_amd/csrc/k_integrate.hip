@@ -1309,8 +1309,13 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
 }
 
 template <int GEO, int NB, bool CULIF>
-__global__ __launch_bounds__(64 * kQuadWaves) void k_stream_quad(DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
-                                                     const float* __restrict__ theta, int nel_max) {
+// The CuLIF pair kernel with 9 chunks (CuLIF-7 conv2, VALU-bound) is held to
+// 8 waves per SIMD: its 104 scalar registers would allow 7, and the 27 it
+// spills to VGPR lanes cost less than the wave (A/B on one box: 2.38 -> 2.29
+// ms).  The other instantiations keep the compiler's own choice.
+__global__ __launch_bounds__(64 * kQuadWaves)
+__attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void k_stream_quad(
+    DenseMergeArgs m, StreamArgs a, float* __restrict__ out, const float* __restrict__ theta, int nel_max) {
     static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
     constexpr int OWN = 4 / GEO;  // c_out per lane
     constexpr int LPG = 8 / GEO;  // loads per group of 8 events
