@@ -5,15 +5,19 @@
 * one bin: every input spikes in the first arrival bin (the largest
   possible collision: the whole receptive field in one bin's fma chain);
 * last bin: every input spikes in the window's last arrival bin;
-* past window: every input arrives after the window (all dropped).
+* past window: every input arrives after the window (all dropped);
+* dense: every input spikes, at random times over the window (the longest
+  lists, spread over all bins).
 
 Each case must equal the oracle bit for bit through the drop-in pair
 (reference-layout bucketize + integrate) and through the engine path with
 and without work counters (counts equal too).  The shapes put one layer on
 each path: fused list in LDS (one and two events per load, and past the
-dense path's C_in limit), bucketize + merge
-+ dwordx4 gather, the narrow stream, the register path and the generic
-integrator (> 25 taps).
+dense path's C_in limit), the shared-list kernel (64 and 128 c_out per wave,
+conv and FC, with fields larger than its list capacity, so that the one-bin
+and dense cases stream their lists in several windows: one split inside
+bin 0, the other inside later bins), the narrow stream, the register path
+and the generic integrator (> 25 taps).
 """
 import sys
 import zlib
@@ -33,13 +37,16 @@ SHAPES = [
     ("fused-c64", 64, 32.0, True, False, 2, 6, 6, 16, 64, 3),
     ("fused-pair-c128", 64, 32.0, True, False, 2, 5, 5, 32, 128, 3),
     ("fused-wide-c128", 64, 32.0, True, False, 2, 5, 5, 128, 128, 3),
-    ("bins-x4-c256", 64, 0.0, False, False, 2, 6, 6, 96, 256, 3),
+    ("shared-c256", 64, 0.0, False, False, 2, 6, 6, 96, 256, 3),
+    ("shared-win-c512", 64, 32.0, True, False, 1, 4, 4, 512, 512, 3),
+    ("shared-win-pair-c256", 64, 32.0, True, False, 2, 5, 5, 256, 256, 3),
+    ("shared-win-fc-4096", 32, 0.0, False, True, 3, 1, 1, 4096, 256, 1),
     ("narrow-c10", 64, 0.0, False, False, 3, 8, 8, 6, 10, 5),
     ("reg-c3-o16", 64, 32.0, True, False, 2, 7, 7, 3, 16, 3),
     ("fc-512-96", 32, 0.0, False, True, 5, 1, 1, 512, 96, 1),
     ("generic-k7", 16, 0.0, False, False, 1, 9, 9, 4, 40, 7),
 ]
-KINDS = ["silent", "one-bin", "last-bin", "past-window"]
+KINDS = ["silent", "one-bin", "last-bin", "past-window", "dense"]
 
 
 def say(msg):
@@ -47,7 +54,9 @@ def say(msg):
     sys.stdout.flush()
 
 
-def spike_times(kind, n, T, tfs):
+def spike_times(kind, n, T, tfs, rng):
+    if kind == "dense":
+        return np.floor(rng.random(n) * (T + tfs)).astype(np.float32)
     if kind == "silent":
         v = INF
     elif kind == "one-bin":
@@ -74,7 +83,7 @@ def test_degenerate_inputs_match_oracle(gpu_ctx_factory, shape, kind):
         ho, wo = (H, W) if task2 else (H - K + 1, W - K + 1)
         n_cols, kshape = B * H * W, (K, K, C_in, C_out)
         sh = dict(B=B, H_in=H, W_in=W, C_in=C_in, H_out=ho, W_out=wo, C_out=C_out, K_h=K, K_w=K)
-    sp = spike_times(kind, n_cols * C_in, T, tfs)
+    sp = spike_times(kind, n_cols * C_in, T, tfs, rng)
     fan = int(np.prod(kshape[:-1]))
     Wt = (rng.standard_normal(int(np.prod(kshape))) * np.sqrt(2.0 / fan)).astype(np.float32)
     # biases large enough that some neurons fire on the bias alone

@@ -32,19 +32,24 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
     net = make_net(ctx, w, 16)
     try:
         got = [net.get_plan(i) for i in range(len(w.layers))]
-        exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (FUSED, 2, 1), 4: (FUSED, 2, 1), 6: (BINS, 4, 1),
-               10: (BINS, 4, 1), 16: (BINS, 4, 1), 18: (BINS, 2, 1)}
+        # every weighted layer builds its lists in LDS: per wave up to 128 inputs
+        # and 128 outputs (conv 0-3), shared by a workgroup's waves beyond, at
+        # 128 c_out per wave up to 256 outputs and 64 past that
+        exp = {0: (FUSED, 1, 1), 1: (FUSED, 1, 1), 3: (FUSED, 2, 1), 4: (FUSED, 2, 1), 6: (FUSED, 2, 1),
+               10: (FUSED, 1, 1), 16: (FUSED, 1, 1), 18: (FUSED, 1, 1)}
         for i, p in exp.items():
             assert got[i] == p, f"layer {i}: {got[i]}"
         assert got[2] == (0, 0, 0) and got[19] == (0, 0, 0)  # pool, vmem
-        bad = [(18, FUSED, 0, 0),   # FC layers have no dense path
+        bad = [(18, DENSE, 0, 0),   # FC layers have no dense path
+               (18, FUSED, 4, 0),   # the shared-list kernel gathers 64 or 128 c_out per wave
+               (10, FUSED, 0, 2),   # ... and takes one pixel per workgroup
                (0, 0, 0, 9),        # at most 8 pixels per wave
                (0, 6, 0, 0),        # unknown path
                (4, DENSE, 0, 0),    # dense merge needs C_in <= 64
                (1, FUSED, 4, 0),    # the fused kernels gather one c_out per lane or two events per load
                (3, FUSED, 4, 0),    # ... and C_out <= 128
                (4, FUSED, 4, 0),    # ... also past the dense path's C_in limit (128 -> 128)
-               (6, FUSED, 0, 0),    # 128 -> 256: no fused kernel gathers 256 c_out
+               (6, FUSED, 4, 0),    # 128 -> 256: no fused kernel gathers 256 c_out per wave
                (0, 0, 3, 0),        # gather is 1, 2 or 4
                (2, BINS, 0, 0),     # pools have no integrator
                (1, REG, 0, 0),      # 9 * 64 receptive elements do not fit in registers
@@ -70,7 +75,7 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
         assert net.get_plan(0) == (REG, 1, 10)     # C_out 6: 10 pixels per wave
         assert net.get_plan(2) == (DENSE, 1, 4)    # 150 receptive elements: a list
         assert net.get_plan(6) == (BINS, 1, 6)     # FC 84 -> 10
-        assert net.get_plan(4) == (BINS, 2, 1)     # FC 256 -> 120
+        assert net.get_plan(4) == (FUSED, 2, 1)    # FC 256 -> 120: the shared-list kernel
         with pytest.raises(vdttfs.VdttfsError):
             net.set_plan(0, 0, 0, 2)
         with pytest.raises(vdttfs.VdttfsError):
@@ -129,8 +134,9 @@ def test_every_plan_matches_oracle_vgg(gpu_ctx_factory):
     img = models.images_for(w, B)
     ref = oracle_ref(w, B, img)
     n = sweep_all_plans(gpu_ctx_factory(w.consts), w, B, img, ref, check_counts=True)
-    # layer 10 (3x3, 256 -> 512) and the FC layer: bins and window paths x 3 gathers x 3 pixel counts
-    assert n[0] >= 10 and n[10] == 18 and n[18] == 18
+    # layer 10 (3x3, 256 -> 512) and the FC layer: bins and window paths x 3 gathers x 3 pixel
+    # counts, and the shared-list fused kernel at gathers 1 and 2
+    assert n[0] >= 10 and n[10] == 20 and n[18] == 20
     net = make_net(gpu_ctx_factory(w.consts), w, B)
     try:
         net.set_plan(18, vdttfs.PATH_WINDOW)
@@ -242,17 +248,23 @@ def test_register_path_forced_matches_oracle(gpu_ctx_factory, case):
 
 
 def test_builtin_pixels_per_wave_follow_residency(gpu_ctx_factory):
-    """VGG-16 at B=256: two pixels per wave exactly where one pixel per wave
-    needs between one and two rounds of resident waves (the 4x4 layers,
-    8,192 waves) and two fit in one; four on the one-chunk fused conv 0; one
-    elsewhere."""
+    """VGG-16 at B=256: the built-in fused plans take four pixels per wave on
+    the one-chunk conv 0 and one elsewhere (the shared-list kernel runs one
+    pixel per workgroup).  On the bins path, two pixels per wave exactly
+    where one pixel per wave needs between one and two rounds of resident
+    waves (the 4x4 layers, 8,192 waves) and two fit in one."""
     say("plans: VGG-16 B=256 pixels per wave from residency")
     w = models.vgg16()
     ctx = gpu_ctx_factory(w.consts)
     net = make_net(ctx, w, 256)
+    weighted = (0, 1, 3, 4, 6, 7, 8, 10, 11, 12, 14, 15, 16, 18)
     try:
-        ppw = {i: net.get_plan(i)[2] for i in (0, 1, 3, 4, 6, 7, 8, 10, 11, 12, 14, 15, 16, 18)}
+        ppw = {i: net.get_plan(i)[2] for i in weighted}
         # conv 0: the one-chunk fused kernel takes four pixels per wave at 2^18 pixels
-        assert ppw == {0: 4, 1: 1, 3: 1, 4: 1, 6: 1, 7: 1, 8: 1, 10: 2, 11: 2, 12: 2, 14: 1, 15: 1, 16: 1, 18: 1}, ppw
+        assert ppw == {i: (4 if i == 0 else 1) for i in weighted}, ppw
+        for i in weighted[4:]:
+            net.set_plan(i, BINS, 4 if i < 18 else 2)
+        ppw = {i: net.get_plan(i)[2] for i in weighted[4:]}
+        assert ppw == {6: 1, 7: 1, 8: 1, 10: 2, 11: 2, 12: 2, 14: 1, 15: 1, 16: 1, 18: 1}, ppw
     finally:
         net.close()

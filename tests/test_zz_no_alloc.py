@@ -3,8 +3,8 @@ library's static per-GPU scratch must give exactly what vdttfs_layer_forward
 (context scratch grown with hipMalloc) gives, on two calls in a row -- the
 second with a smaller input, so stale scratch from the first call cannot
 leak into it -- on every list path (fused with one or two events per load,
-dense, bins, narrow, register, FC), and reject a layer whose scratch exceeds
-the buffer."""
+the shared-list fused kernel, dense, bins, narrow, register, FC), and reject
+a layer whose scratch exceeds the buffer."""
 import sys
 import zlib
 
@@ -21,8 +21,9 @@ INF = np.float32(9999.0)
 CASES = [
     ("fused 32->64 3x3", True, False, (5, 2), 12, 12, 32, 64, 3),
     ("fused pair 16->128 3x3", True, False, (4, 3), 16, 16, 16, 128, 3),
-    ("dense 24->256 3x3", True, False, (3, 2), 8, 8, 24, 256, 3),
-    ("bins 130->256 3x3", True, False, (3, 1), 8, 8, 130, 256, 3),
+    ("fused shared 24->256 3x3", True, False, (3, 2), 8, 8, 24, 256, 3),
+    ("fused shared 130->256 3x3", True, False, (3, 1), 8, 8, 130, 256, 3),
+    ("bins 80->64 5x5", True, False, (3, 1), 8, 8, 80, 64, 5),
     ("fused wide 96->128 3x3", True, False, (3, 2), 10, 10, 96, 128, 3),
     ("narrow 6->16 5x5 valid", False, False, (40, 7), 12, 12, 6, 16, 5),
     ("register 1->6 5x5 valid", False, False, (50, 9), 28, 28, 1, 6, 5),
@@ -83,19 +84,19 @@ def test_noalloc_matches_layer_forward(gpu_ctx_factory, case):
 
 
 def test_noalloc_rejects_oversized_layer(gpu_ctx_factory):
-    """A 128->256 conv at 64x32x32 (bins path) needs ~0.7 GB of bucketize
-    output and merged lists: refused with VDTTFS_E_UNSUPPORTED before any
-    launch, the output left untouched."""
+    """A 5x5 128->256 conv at 64x32x32 (bins path: 25 taps) needs ~2 GB of
+    bucketize output and merged lists: refused with VDTTFS_E_UNSUPPORTED
+    before any launch, the output left untouched."""
     say("noalloc oversized layer")
     tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
     ctx = gpu_ctx_factory(tc)
     B, H, W, C_in, C_out = 64, 32, 32, 128, 256
     d_in = ctx.empty(B * H * W * C_in).fill(0)
     d_out = ctx.empty(B * H * W * C_out).fill(0x7F)
-    d_W, d_b = ctx.empty(9 * C_in * C_out).fill(0), ctx.empty(C_out).fill(0)
+    d_W, d_b = ctx.empty(25 * C_in * C_out).fill(0), ctx.empty(C_out).fill(0)
     d_a, d_t = ctx.empty(65).fill(0), ctx.empty(64).fill(0)
     rc = vdttfs.lib().vdttfs_layer_forward_noalloc(ctx.handle, d_out.ptr, d_in.ptr, d_W.ptr, d_b.ptr, d_a.ptr,
-                                                    d_t.ptr, 0, B, H, W, C_in, H, W, C_out, 3, 3, 0)
+                                                    d_t.ptr, 0, B, H, W, C_in, H, W, C_out, 5, 5, 0)
     assert rc == _lib.E_UNSUPPORTED
     assert "scratch" in _lib.last_error()
     out = d_out.download()

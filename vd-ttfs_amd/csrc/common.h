@@ -145,6 +145,11 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& s);
 // Conv layers past those limits (C_in <= 128) that the fused plan still
 // builds from the dense map when no counters are asked for.
 bool quad_wide_ok(const vdttfs_ctx* ctx, const IntegShape& s);
+// Layers the shared-list fused kernel takes under gather 1 or 2 (conv with
+// at most 9 taps or FC, T <= 64, no counters), and which fused kernel a
+// fused plan with this gather runs: 1 per-wave lists, 2 shared lists, 0 none.
+bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& s, int gather);
+int fused_kind(const vdttfs_ctx* ctx, const IntegShape& s, int gather);
 // Whether a layer under resolved plan p takes launch_integrate_dense (its
 // lists built from the dense map) rather than bucketize +
 // launch_integrate_bins, with or without counters.

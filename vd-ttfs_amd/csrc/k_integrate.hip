@@ -1308,6 +1308,272 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
     return total;
 }
 
+// ---------------------------------------------------------------------------
+// Shared-list build (k_stream_quad<GEO, 0, CULIF>).  Past the per-wave
+// kernels' limits -- more than 128 inputs per tap (a 3x3 pixel of 512 inputs
+// has 4,608 receptive elements, 72 chunks of 64) or more c_out than one wave
+// gathers -- one workgroup of W waves takes one output pixel: the W waves
+// build the pixel's merged list together in the workgroup's LDS, then each
+// streams it for its own c_out block.  The build is quad_build's stable
+// counting sort of the receptive elements in (kh, kw, cin) order, with the
+// chunks split over the waves in contiguous ranges, so that a bin's events
+// stay in element order across waves:
+//  pass 1  each wave counts its chunks' events per bin: bin 0, where the fire
+//          start (T2V:59-60) puts most events, from ballots, the others with
+//          LDS atomics;
+//  scan    lane b sums bin b's counts over the waves, and a wave scan gives
+//          the bin ends (the stream's v_end) and each wave's cursor: the bin's
+//          start plus the counts of the lower waves;
+//  pass 2  each wave reloads its chunks (L1/L2 hits) and places every event
+//          at its bin's cursor plus its rank among the chunk's lanes of the
+//          same bin: a ballot for bin 0 (its cursor stays in a scalar), the
+//          LDS bit masks of quad_build for the other bins.
+// Entries are as in k_stream_quad's per-wave lists: 16-bit weight rows and
+// alphas (the LUT neuron), or row byte offsets (the CuLIF neuron).  LDS of a
+// workgroup: the list (quad_list_words, rounded up to 4 words), then per
+// wave 64 counts, 64 cursors, 128 mask words and the tap table.
+constexpr int kSharedMaxWaves = 4;
+constexpr int kSharedWaveWords = 64 + 64 + 128 + 32;
+constexpr int kSharedBatch = 8;  // chunk loads a wave issues before using any
+
+__host__ __device__ inline int shared_list_words(int nel_max, int T, bool alphas) {
+    return (quad_list_words(nel_max, T, alphas) + 3) & ~3;
+}
+__host__ __device__ inline int shared_block_words(int nel_max, int T, bool alphas, int waves) {
+    return shared_list_words(nel_max, T, alphas) + kSharedWaveWords * waves;
+}
+
+// Builds pixel `pix`'s list with the W waves of the workgroup (every wave
+// calls it; it ends with a workgroup barrier) and returns its length; v_end
+// gets, in lane b < T, the end of bin b, INT_MAX elsewhere.  al_lane holds
+// alpha[lane] for lane <= T and al_64 alpha[64] (T = 64); ALPHA selects the
+// entry form.
+// Keeps the compiler from moving LDS accesses across this point without
+// making the wave wait: a wave's LDS instructions execute in program order,
+// so a read issued after a write or atomic of the same wave sees its effect.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
+// Receptive element f = 64 c + lane of the shared-list build: tap k =
+// f / C_in (the float quotient's fractional part is >= 0.5 / C_in, far above
+// its rounding error for the C_in this kernel takes), cin ci; its spike time
+// t and weight row.  A chunk of a layer with C_in >= 64 (or one tap) spans at
+// most two taps, k0 = the tap of its first element and k0 + 1, whose table
+// entries come from readlane; otherwise from the wave's LDS tap table.
+// Elements past the end load the map's first word and are no event.
+__device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, int nel, int nk, int tcol, int trow,
+                                               const int* ktab, float& t, int& row) {
+    const int lane = lane_id();
+    const int f = c * 64 + lane;
+    const bool in = f < nel;
+    const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
+    const int ci = f - k * a.C_in;
+    int co, ro;
+    if (a.C_in >= 64 || nk == 1) {  // uniform
+        const int k0 = __builtin_amdgcn_readfirstlane(k);  // lane 0's element 64 c is in the field
+        const int k1 = k0 + 1 < nk ? k0 + 1 : k0;
+        const bool lo = k == k0;
+        co = lo ? __builtin_amdgcn_readlane(tcol, k0) : __builtin_amdgcn_readlane(tcol, k1);
+        ro = lo ? __builtin_amdgcn_readlane(trow, k0) : __builtin_amdgcn_readlane(trow, k1);
+    } else {
+        co = ktab[k];
+        ro = ktab[16 + k];
+    }
+    row = ro + ci;
+    const __amdgpu_buffer_rsrc_t rin =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+    t = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? (co + ci) * 4 : 0, 0, 0));
+    if (!in) t = kInfTime;
+}
+
+// Arrival bin floor(max(t - tfs, 0)), -1 for no spike or past the window.
+__device__ __forceinline__ int shared_bin(const DenseMergeArgs& a, float t) {
+    const int tb = (int)floorf(fmaxf(t - a.tfs, 0.0f));
+    return (t < kInfTime && tb < a.T) ? tb : -1;
+}
+
+// Pass 1 and the scan of the shared-list build, with every wave of the
+// workgroup (it ends with a workgroup barrier).  Returns the pixel's list
+// length; v_end gets, in lane b < T, the end of bin b (INT_MAX elsewhere);
+// nk, tcol and trow describe the in-bounds taps for shared_place: lane
+// s < nk holds tap s's input element offset col * C_in and first weight row
+// tap * C_in (taps compacted in (kh, kw) order).
+__device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, int W, int wave, int* tables,
+                                            int& v_end, int& nk, int& tcol, int& trow) {
+    const int lane = lane_id();
+    const int T = a.T;
+    int* mine = tables + kSharedWaveWords * wave;
+    int* cnt = mine;                                         // events per bin
+    unsigned* msk = reinterpret_cast<unsigned*>(mine + 128);  // rank masks, two words per bin
+    int* ktab = mine + 256;                                  // tap table: offsets [0, 9), rows [16, 25)
+    const int qd = fdiv(pix, a.div_w);
+    const int w_out = pix - qd * a.W_out;
+    const int img = fdiv(qd, a.div_h);
+    const int h_out = qd - img * a.H_out;
+    {
+        bool v = false;
+        int col = 0;
+        if (lane < a.K_h * a.K_w) {
+            const int kh = lane / a.K_w, kx = lane - kh * a.K_w;
+            const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kx;
+            v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
+            col = (img * a.H_in + hi) * a.W_in + wi;
+        }
+        const uint64_t m = __ballot(v);
+        nk = uniform(__popcll(m));
+        if (v) {
+            const int slot = __popcll(m & lanemask_lt());
+            ktab[slot] = col * a.C_in;
+            ktab[16 + slot] = lane * a.C_in;
+        }
+        const int z = vzero();
+        cnt[lane] = z;
+        msk[lane] = z;
+        msk[64 + lane] = z;
+    }
+    wave_sync();
+    tcol = lane < nk ? ktab[lane] : 0;
+    trow = lane < nk ? ktab[16 + lane] : 0;
+    const int nel = nk * a.C_in;
+    const int n_chunks = (nel + 63) >> 6;
+    const int c_lo = (int)((unsigned)(n_chunks * wave) / (unsigned)W);
+    const int c_hi = (int)((unsigned)(n_chunks * (wave + 1)) / (unsigned)W);
+    // pass 1: this wave's events per bin (bin 0 from ballots; the counting
+    // atomics return nothing, so nothing waits on them)
+    int n0 = 0;
+    for (int c0 = c_lo; c0 < c_hi; c0 += kSharedBatch) {  // uniform
+        float t[kSharedBatch];
+        int rw[kSharedBatch];
+#pragma unroll
+        for (int i = 0; i < kSharedBatch; ++i) {
+            t[i] = kInfTime;
+            rw[i] = 0;
+            if (c0 + i < c_hi) shared_element(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kSharedBatch; ++i) {
+            if (c0 + i < c_hi) {
+                const int b = shared_bin(a, t[i]);
+                n0 += __popcll(__ballot(b == 0));
+                if (b > 0) atomicAdd(&cnt[b], 1);
+            }
+        }
+    }
+    lds_order();
+    if (lane == 0) cnt[0] = n0;
+    __syncthreads();
+    int tot = 0;
+    for (int w2 = 0; w2 < W; ++w2) tot += lane < T ? tables[kSharedWaveWords * w2 + lane] : 0;
+    const int incl = wave_incl_scan(tot);
+    v_end = lane < T ? incl : INT_MAX;
+    return __builtin_amdgcn_readlane(incl, 63);
+}
+
+// Pass 2 of the shared-list build for the list window [P0, P0 + cap): every
+// wave places its chunks' events whose list position falls in the window at
+// position - P0 (16-bit weight rows and alphas, or row byte offsets), and
+// the positions from the window's end (or the list's) get 32 zeroed
+// entries.  Every wave of the workgroup calls it; it ends with a workgroup
+// barrier.  The cursors restart from the counts of pass 1, so a window's
+// positions do not depend on the windows before it.  NBAT chunk loads are
+// issued together.
+template <bool ALPHA, int NBAT>
+__device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int wave, int* rows, int* alph,
+                                             int* tables, int P0, int cap, int total, int nk, int tcol,
+                                             int trow, float al_lane, float al_64) {
+    const int lane = lane_id();
+    const int T = a.T;
+    int* mine = tables + kSharedWaveWords * wave;
+    int* cur = mine + 64;                                    // cursors
+    unsigned* msk = reinterpret_cast<unsigned*>(mine + 128);  // rank masks, two words per bin (clear)
+    int* ktab = mine + 256;
+    // this wave's cursor in bin b: the bin's start plus the lower waves' counts
+    int tot = 0, below = 0;
+    for (int w2 = 0; w2 < W; ++w2) {
+        const int x = lane < T ? tables[kSharedWaveWords * w2 + lane] : 0;
+        tot += x;
+        below += w2 < wave ? x : 0;
+    }
+    const int incl = wave_incl_scan(tot);
+    cur[lane] = incl - tot + below;
+    int cur0 = __builtin_amdgcn_readfirstlane(incl - tot + below);  // bin 0's cursor
+    const int n_w = total - P0 < cap ? total - P0 : cap;
+    if (wave == 0 && lane < kListPad) {
+        const int z = vzero();
+        if constexpr (ALPHA) {
+            reinterpret_cast<unsigned short*>(rows)[n_w + lane] = (unsigned short)z;
+            alph[n_w + lane] = z;
+        } else {
+            rows[n_w + lane] = z;
+        }
+    }
+    lds_order();
+    const int nel = nk * a.C_in;
+    const int n_chunks = (nel + 63) >> 6;
+    const int c_lo = (int)((unsigned)(n_chunks * wave) / (unsigned)W);
+    const int c_hi = (int)((unsigned)(n_chunks * (wave + 1)) / (unsigned)W);
+    // Per chunk with events past bin 0 one round trip: OR the lane bits into
+    // the bins' masks, read the masks and the cursors back; the bin's last
+    // lane in the chunk then advances the cursor and clears the mask (no
+    // result, no wait).
+    const uint64_t lt = lanemask_lt();
+    const unsigned bit = 1u << (lane & 31);
+    for (int c0 = c_lo; c0 < c_hi; c0 += NBAT) {  // uniform
+        float t[NBAT];
+        int rw[NBAT];
+#pragma unroll
+        for (int i = 0; i < NBAT; ++i) {
+            t[i] = kInfTime;
+            rw[i] = 0;
+            if (c0 + i < c_hi) shared_element(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < NBAT; ++i) {
+            if (c0 + i < c_hi) {  // uniform
+                const int b = shared_bin(a, t[i]);
+                float al = 0.0f;
+                int ai = 0;
+                if constexpr (ALPHA) {
+                    // decay-LUT index: the bin, or clamp((int)t, 0, T) by spike time
+                    ai = b < 0 ? 0 : (a.alpha_by_time ? (int)fminf(fmaxf(t[i], 0.0f), (float)T) : b);
+                    al = __shfl(al_lane, ai & 63, 64);
+                }
+                const uint64_t z0 = __ballot(b == 0);
+                int pos = cur0 + __popcll(z0 & lt);
+                cur0 += __popcll(z0);
+                const bool oth = b > 0;
+                if (__ballot(oth) != 0) {  // uniform
+                    if (oth) atomicOr(&msk[2 * b + (lane >> 5)], bit);
+                    lds_order();
+                    uint64_t mm = 0;
+                    int cb = 0;
+                    if (oth) {
+                        mm = *reinterpret_cast<const uint64_t*>(&msk[2 * b]);
+                        cb = cur[b];
+                    }
+                    lds_order();
+                    if (oth) pos = cb + __popcll(mm & lt);
+                    if (oth && (mm >> lane) == 1ull) {  // the bin's last lane in this chunk
+                        atomicAdd(&cur[b], __popcll(mm));
+                        const int z = vzero();
+                        *reinterpret_cast<int2*>(&msk[2 * b]) = make_int2(z, z);
+                    }
+                    lds_order();
+                }
+                const int q = pos - P0;
+                if (b >= 0 && q >= 0 && q < cap) {
+                    if constexpr (ALPHA) {
+                        reinterpret_cast<unsigned short*>(rows)[q] = (unsigned short)rw[i];
+                        alph[q] = __float_as_int(ai == 64 ? al_64 : al);
+                    } else {
+                        rows[q] = (int)__umul24((unsigned)rw[i], (unsigned)a.rowbytes);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 template <int GEO, int NB, bool CULIF>
 // The CuLIF pair kernel with 9 chunks (CuLIF-7 conv2, VALU-bound) is held to
 // 8 waves per SIMD: its 104 scalar registers would allow 7, and the 27 it
@@ -1319,6 +1585,13 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
     static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
     constexpr int OWN = 4 / GEO;  // c_out per lane
     constexpr int LPG = 8 / GEO;  // loads per group of 8 events
+    // NB <= 0: one pixel per workgroup, its list shared by the workgroup's
+    // waves (shared_count, shared_place), wave w streaming c_out block
+    // grp * W + w
+    constexpr bool SHARED = NB <= 0;
+    // NB = -1: the list may exceed the workgroup's capacity (nel_max entries)
+    // and then comes in windows (below); NB = 0: it always fits
+    constexpr bool WINDOWS = NB < 0;
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
     typedef float f4 __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) int lds_words[];
@@ -1327,7 +1600,7 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
     // weights unscaled (alpha = 1, the reference's acc + w), so its lists
     // hold row byte offsets only
     const int E = quad_list_entries(nel_max, a.T);
-    int* region = lds_words + wave * quad_wave_words(nel_max, a.T, !CULIF);
+    int* region = SHARED ? lds_words : lds_words + wave * quad_wave_words(nel_max, a.T, !CULIF);
     int* rows = region;
     const unsigned short* rows16 = reinterpret_cast<const unsigned short*>(region);
     int* alph = region + E / 2;  // not used by the CuLIF neuron
@@ -1340,8 +1613,27 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
     // loads c_out 4r..4r+3 of event q and owns c_out 4r+2q, 4r+2q+1
     const int q = GEO == 4 ? lane >> 4 : lane >> 5;
     const int r = GEO == 4 ? (lane & 15) : (lane & 31);
-    const int co = GEO == 4 ? 4 * r + q : 4 * r + 2 * q;  // first c_out of the lane
-    const int voff = 16 * r;
+    int cb = 0;           // SHARED: this wave's c_out block (64 or 128 wide)
+    int64_t spix = 0;     // SHARED: the workgroup's pixel
+    if constexpr (SHARED) {
+        // Workgroups are dealt to the 8 XCDs round-robin.  Block bi takes
+        // c_out group bi % n_grp, so where n_grp divides 8 every XCD
+        // integrates one group and its L2 holds only that group's share of
+        // the weights.  The S = 8 / n_grp XCDs of a group each take a
+        // contiguous range of pixels, so the input columns that neighbouring
+        // pixels share meet in one L2.
+        const int W = blockDim.x >> 6;
+        const int n_grp = (a.n_cblk + W - 1) / W;
+        const int bi = blockIdx.x;
+        const int j = bi / n_grp;
+        const int n = (int)a.n_pix;
+        const int S = (8 % n_grp == 0) ? 8 / n_grp : 1;
+        const int mbr = j % S, per = n / S, rem = n - per * S;
+        spix = mbr * per + (mbr < rem ? mbr : rem) + j / S;
+        cb = (bi - j * n_grp) * W + wave;
+    }
+    const int co = (GEO == 4 ? 4 * r + q : 4 * r + 2 * q) + cb * (GEO == 4 ? 64 : 128);  // first c_out of the lane
+    const int voff = 16 * r + cb * (GEO == 4 ? 256 : 512);
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
     const int T = a.T;
@@ -1356,12 +1648,26 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
         ok[v] = co + v < a.C_out;
         bias[v] = (ok[v] && !CULIF) ? a.bias[co + v] : 0.0f;  // the CuLIF neuron starts at V = 0
     }
-    const int64_t pix0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave) * a.ppw;
-    for (int pq = 0; pq < a.ppw; ++pq) {
+    float al_lane = 0.0f, al_64 = 0.0f;  // SHARED: the decay LUT, alpha[lane] and alpha[64]
+    if constexpr (SHARED && !CULIF) {
+        if (lane <= T) al_lane = m.alpha[lane];
+        if (T == 64) al_64 = m.alpha[64];
+    }
+    const int64_t pix0 = SHARED ? spix : ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave) * a.ppw;
+    for (int pq = 0; pq < (SHARED ? 1 : a.ppw); ++pq) {
         const int64_t pix = pix0 + pq;
-        if (pix >= a.n_pix) return;  // uniform per wave
-        const int total = quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
-        wave_sync();
+        if (pix >= a.n_pix) return;  // uniform per wave (SHARED: per workgroup)
+        int total, sv_end = 0;
+        int snk = 0, stcol = 0, strow = 0;  // SHARED: the pixel's taps
+        int* tables = lds_words + shared_list_words(nel_max, T, !CULIF);
+        if constexpr (SHARED) {
+            total = shared_count(m, (int)pix, blockDim.x >> 6, wave, tables, sv_end, snk, stcol, strow);
+            shared_place<!CULIF, kSharedBatch>(m, blockDim.x >> 6, wave, rows, alph, tables, 0, nel_max, total,
+                                               snk, stcol, strow, al_lane, al_64);
+        } else {
+            total = quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
+            wave_sync();
+        }
         if (CULIF && total == 0) {  // uniform
             // no input: I and V stay 0, so a neuron fires at step 0 when
             // 0 >= th (T3V:50-62) and never otherwise; the 64 steps are skipped
@@ -1371,7 +1677,7 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
                 if (ok[v]) out[pix * a.C_out + co + v] = o;
             continue;
         }
-        const int v_end = lane < T ? bs[lane + 1] : INT_MAX;  // end of bin `lane`
+        int v_end = SHARED ? sv_end : (lane < T ? bs[lane + 1] : INT_MAX);  // end of bin `lane`
         float carry[OWN], acc[OWN], cur[OWN];  // cur: the CuLIF current I
         int res[OWN];  // bins closed with the neuron still alive: its spike bin once it fired
         uint64_t alive[OWN];
@@ -1515,14 +1821,57 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
         };
         // the next group's loads are issued before this group's wait
         Raw g0, g1;
-        load(0, g0);
-        for (int j = 0;; j += 16) {
-            load(j + 8, g1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (consume(j, g0)) break;
-            load(j + 16, g0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (consume(j + 8, g1)) break;
+        if constexpr (!WINDOWS) {
+            if (SHARED && cb >= a.n_cblk) continue;  // a wave past the last c_out block only helps build
+            load(0, g0);
+            for (int j = 0;; j += 16) {
+                load(j + 8, g1);
+                __builtin_amdgcn_sched_barrier(0);
+                if (consume(j, g0)) break;
+                load(j + 16, g0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (consume(j + 8, g1)) break;
+            }
+        } else {
+            // Windows of at most nel_max list entries: positions are window-
+            // relative (v_end shifted by the window's start P0), and a window
+            // that more follow stops its stream at its end (jlim) with the
+            // open bin and the neuron state kept; the next window then goes
+            // on from its first entry.  Waves past the last c_out block only
+            // help build.  Later windows place one chunk at a time: their
+            // placement runs beside the live neuron state, and a batch of
+            // loads there cost the kernel its eighth wave per SIMD.
+            bool live = cb < a.n_cblk;
+            int P0 = 0;
+            for (;;) {
+                const int jlim = total - P0 > nel_max ? nel_max : INT_MAX;
+                if (live) {
+                    load(0, g0);
+                    for (int j = 0;; j += 16) {
+                        if (j >= jlim) break;
+                        load(j + 8, g1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (consume(j, g0)) {
+                            live = false;
+                            break;
+                        }
+                        if (j + 8 >= jlim) break;
+                        load(j + 16, g0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (consume(j + 8, g1)) {
+                            live = false;
+                            break;
+                        }
+                    }
+                }
+                if (jlim == INT_MAX) break;  // uniform: the last window
+                P0 += nel_max;
+                __syncthreads();  // every wave is done with this window
+                shared_place<!CULIF, 1>(m, blockDim.x >> 6, wave, rows, alph, tables, P0, nel_max, total, snk,
+                                        stcol, strow, al_lane, al_64);
+                if (lane < T) v_end = sv_end - P0;
+                if (live) bend = __builtin_amdgcn_readlane(v_end, b);
+            }
         }
 #pragma unroll
         for (int v = 0; v < OWN; ++v)
@@ -2407,6 +2756,78 @@ int launch_stream_window(vdttfs_ctx* ctx, const MergeArgs& m, float* out, const 
     return VDTTFS_OK;
 }
 
+// Most receptive elements of one output pixel: an output row meets at most
+// min(K_h, H_in) input rows whatever the padding (a 3x3 kernel on a 2x2 map
+// reaches 4 taps), likewise columns.
+int64_t shared_nel_max(const IntegShape& sh) {
+    if (sh.is_fc) return sh.C_in;
+    const int kh = sh.K_h < sh.H_in ? sh.K_h : sh.H_in;
+    const int kw = sh.K_w < sh.W_in ? sh.K_w : sh.W_in;
+    return (int64_t)kh * kw * sh.C_in;
+}
+
+// Waves of one shared-list workgroup: one per c_out block, at most four.
+// Wider layers take several workgroups per pixel (c_out groups), which the
+// kernel pins to XCDs: VGG-16's 512-wide layers at 64 c_out per wave take
+// two groups, so that an XCD's L2 holds half of a 9.4 MB weight tensor
+// (measured on conv 8, 512 -> 512 at 4x4: L2 hit rate 0.69 with one group of
+// four 128-wide waves, 0.99 with two groups).
+int shared_waves(int64_t n_cblk) { return (int)(n_cblk < kSharedMaxWaves ? n_cblk : kSharedMaxWaves); }
+
+// List capacity of a shared-list workgroup, in entries: the pixel's most
+// receptive elements, but at most what keeps the workgroup's LDS near 5 KB
+// per wave (eight waves per SIMD on the 160 KB of a CU), rounded to 16.  A
+// pixel with more events streams its list in windows of this size (VGG-16
+// conv 8: 4,608 receptive elements, ~2,150 events per interior pixel, a
+// capacity of 2,640 at four waves: 0.633 -> 0.533 ms against lists sized to
+// the field).
+constexpr int kSharedLdsPerWave = 5 * 1024;
+int shared_cap(int64_t nel_max, int waves, bool alphas) {
+    const int64_t per = alphas ? 6 : 4;  // 16-bit row and alpha, or row byte offset
+    const int64_t lim = (((int64_t)kSharedLdsPerWave - 4 * kSharedWaveWords) * waves / per) & ~INT64_C(15);
+    const int64_t want = (nel_max + 15) & ~INT64_C(15);
+    return (int)(want < lim ? want : lim);
+}
+// The shared-list kernel: one workgroup per (output pixel, group of up to
+// four c_out blocks), the W waves building the pixel's list together and
+// each streaming one c_out block (64 c_out at epi 1, 128 at epi 2).
+int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
+                         const float* theta, int64_t nel_max, int epi, bool culif) {
+    const int waves = shared_waves(a.n_cblk);
+    const int64_t n_grp = (a.n_cblk + waves - 1) / waves;
+    const int64_t blocks = a.n_pix * n_grp;
+    if (blocks <= 0) return VDTTFS_OK;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    const int cap = shared_cap(nel_max, waves, !culif);
+    const size_t lds = (size_t)shared_block_words(cap, m.T, !culif, waves) * sizeof(int);
+    if (lds > kFusedMaxLds) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: shared list exceeds LDS");
+#define VD_LAUNCH_SHARED(G, NB, L)                                                                      \
+    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)blocks), dim3(64 * waves), lds, ctx->stream, \
+                       m, a, out, theta, cap)
+#define VD_LAUNCH_SHARED_NB(G, L)       \
+    do {                                \
+        if (cap < nel_max)              \
+            VD_LAUNCH_SHARED(G, -1, L); \
+        else                            \
+            VD_LAUNCH_SHARED(G, 0, L);  \
+    } while (0)
+    if (epi == 2) {
+        if (culif)
+            VD_LAUNCH_SHARED_NB(2, true);
+        else
+            VD_LAUNCH_SHARED_NB(2, false);
+    } else {
+        if (culif)
+            VD_LAUNCH_SHARED_NB(4, true);
+        else
+            VD_LAUNCH_SHARED_NB(4, false);
+    }
+#undef VD_LAUNCH_SHARED_NB
+#undef VD_LAUNCH_SHARED
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
 int launch_stream_narrow(vdttfs_ctx* ctx, float* out, const int2* list, int64_t cap, const int32_t* bstart,
                          const float* W, int64_t wbytes, const float* bias, const float* theta, int t_min,
                          const IntegShape& sh, unsigned long long* counters, const CulifNeuron* culif) {
@@ -2466,15 +2887,62 @@ bool quad_wide_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
            in_bytes < (INT64_C(1) << 31) && (sh.C_out <= 64 || (sh.C_out <= 128 && sh.C_out % 4 == 0));
 }
 
+namespace {
+bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather);
+
+}  // namespace
+
+// Layers whose lists the shared-list kernel builds (k_stream_quad<GEO, 0>,
+// one output pixel per workgroup of up to four waves that share its list):
+// conv with at most 9 taps or FC, T <= 64, gather 1 (64 c_out per wave) or 2
+// (128 per wave, C_out % 4 == 0), weight rows below 2^16 (16-bit entries),
+// 32-bit input offsets and a workgroup's list within the LDS limit.  No
+// counters: a counting forward takes bucketize + merge + stream.
+bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
+    int64_t wbytes;
+    const int taps = sh.is_fc ? 1 : sh.K_h * sh.K_w;
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
+    const int64_t nel_max = shared_nel_max(sh);
+    if (ctx->c.T > kBlockBins || taps > 9 || narrow_path_ok(sh, &wbytes) || !wave_path_ok(sh, &wbytes) ||
+        in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF)
+        return false;
+    if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0)) return false;
+    const int64_t n_cblk = (sh.C_out + (gather == 2 ? 127 : 63)) / (gather == 2 ? 128 : 64);
+    const int waves = shared_waves(n_cblk);
+    const int cap = shared_cap(nel_max, waves, true);
+    return (size_t)shared_block_words(cap, ctx->c.T, true, waves) * sizeof(int) <= kFusedMaxLds;
+}
+
+// The shared-list kernel's built-in gather: 128 c_out per wave (two events
+// per load, fewer transposes per byte) up to 256 c_out, where one group of
+// waves covers the layer; 64 per wave (four events per load) past that, so
+// that each c_out group of four waves holds a smaller share of the weights
+// in its XCD's L2, and where C_out <= 64 or is not a multiple of 4.
+int shared_gather(const IntegShape& sh) {
+    return (sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 256) ? 2 : 1;
+}
+
+// The kernel a fused plan with this gather runs: 1 the per-wave kernels
+// (k_stream_quad's own lists, k_stream_dense), 2 the shared-list kernel,
+// 0 none.
+int fused_kind(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
+    if ((integrate_dense_ok(ctx, sh) || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, gather)) return 1;
+    return shared_ok(ctx, sh, gather) ? 2 : 0;
+}
+
 bool plan_from_dense(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters) {
     if (plan_bins(p)) return false;
-    return integrate_dense_ok(ctx, sh) || (!counters && p.path == VDTTFS_PATH_FUSED && quad_wide_ok(ctx, sh));
+    return integrate_dense_ok(ctx, sh) ||
+           (!counters && p.path == VDTTFS_PATH_FUSED && fused_kind(ctx, sh, p.gather) != 0);
 }
 
 bool plan_lds_list(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters, bool culif) {
     if (p.path == VDTTFS_PATH_WINDOW) return true;
     if (p.path == VDTTFS_PATH_REG) return !counters && !culif;
     if (p.path != VDTTFS_PATH_FUSED) return false;
+    // the shared-list kernel runs no counters: a counting forward takes
+    // k_merge_dense + stream (C_in <= 64) or bucketize + merge + stream
+    if (fused_kind(ctx, sh, p.gather) == 2) return !counters;
     // past the dense limits a counting forward takes bucketize + merge + stream
     if (counters && !integrate_dense_ok(ctx, sh)) return false;
     // two events per load: k_stream_quad only (no counters, 32-bit input
@@ -2601,6 +3069,13 @@ int64_t cu_count(const vdttfs_ctx* ctx) {
     return nc;
 }
 
+// Whether the built-in plan takes the shared-list kernel where it applies.
+bool shared_builtin(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    (void)ctx;
+    (void)sh;
+    return true;
+}
+
 int plan_error(const IntegShape& sh, const char* what) {
     return set_error(VDTTFS_E_UNSUPPORTED, "plan: %s (layer %dx%dx%d -> %d, %dx%d taps%s)", what, sh.H_in, sh.W_in,
                      sh.C_in, sh.C_out, sh.K_h, sh.K_w, sh.is_fc ? ", fc" : "");
@@ -2671,6 +3146,13 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         // the pair, 0.047; the 2x2 conv L14's 2,048 keep four)
         const int64_t simds = 4 * cu_count(ctx);
         if (p.gather == 4 && sh.is_fc && simds > 0 && n_pixels(sh) * ((sh.C_out + 255) / 256) < simds) p.gather = 2;
+        // where no per-wave fused kernel serves, the shared-list kernel's
+        // gather (shared_gather)
+        const int pw = (dense || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, p.gather) ? 1 : 0;
+        if ((req.path == 0 || req.path == VDTTFS_PATH_FUSED) && !pw) {
+            const int g = shared_gather(sh);
+            if (shared_ok(ctx, sh, g) && (req.path == VDTTFS_PATH_FUSED || shared_builtin(ctx, sh))) p.gather = g;
+        }
     }
     // measured: 2 pixels per wave pays at >= 2^20 pixels (CuLIF conv2 at
     // 128x128 x 64 samples: 9.16 -> 8.56 ms) and loses on smaller layers
@@ -2681,14 +3163,20 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     // 8,192 waves against 5,120 resident, 0.42 -> 0.39 ms each): the second
     // round would run mostly empty.
     if (req.ppw > kMaxPixPerWave) return plan_error(sh, "at most 8 pixels per wave");
-    const bool fused = (dense || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, p.gather);
+    const int kind = fused_kind(ctx, sh, p.gather);
+    const bool fused = kind == 1 || (kind == 2 && (req.path == VDTTFS_PATH_FUSED || shared_builtin(ctx, sh)));
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
-        return plan_error(sh, "fused path needs the dense limits, T <= 64 and gather 1 (C_out <= 64) or 2 (C_out <= 128)");
+        return plan_error(sh, "fused path needs T <= 64, at most 9 taps (or FC), gather 1 or 2 (C_out % 4 == 0), "
+                              "and the pixel's list within the LDS limit");
     if (req.path == VDTTFS_PATH_WINDOW && !window_ok(ctx, sh))
         return plan_error(sh, "window path needs T <= 64 and at most 9 taps (or an FC layer)");
     p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
-    if (req.ppw) {
+    if (p.path == VDTTFS_PATH_FUSED && kind == 2) {
+        // the shared-list kernel: one output pixel per workgroup
+        if (req.ppw > 1) return plan_error(sh, "the shared-list fused kernel takes one pixel per workgroup");
+        p.ppw = 1;
+    } else if (req.ppw) {
         p.ppw = req.ppw;
     } else {
         const int64_t n_pix = n_pixels(sh);
@@ -2723,7 +3211,8 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
     // a fused plan past the dense limits falls back here for counting forwards
-    if (plan && plan->path && !plan_bins(*plan) && !(plan->path == VDTTFS_PATH_FUSED && quad_wide_ok(ctx, sh)))
+    if (plan && plan->path && !plan_bins(*plan) &&
+        !(plan->path == VDTTFS_PATH_FUSED && (quad_wide_ok(ctx, sh) || fused_kind(ctx, sh, p.gather) == 2)))
         return set_error(VDTTFS_E_INVALID, "integrate_bins: the plan asks for a dense path");
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
@@ -2783,10 +3272,13 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
     const bool wide = !integrate_dense_ok(ctx, sh) && quad_wide_ok(ctx, sh);
-    if ((!integrate_dense_ok(ctx, sh) && !(wide && !counters)) || (!narrow && !wave_path_ok(sh, &wbytes)))
-        return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, sh, plan ? *plan : LaunchPlan{}, &p));
+    // the shared-list kernel: any conv (<= 9 taps) or FC layer in its limits
+    const bool shared = !counters && p.path == VDTTFS_PATH_FUSED && fused_kind(ctx, sh, p.gather) == 2;
+    if (!shared && ((!integrate_dense_ok(ctx, sh) && !(wide && !counters)) || (!narrow && !wave_path_ok(sh, &wbytes))))
+        return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: conv layers of the merged-list path only");
+    if (shared) (void)wave_path_ok(sh, &wbytes);
     if (wide && p.path != VDTTFS_PATH_FUSED)
         return set_error(VDTTFS_E_UNSUPPORTED, "integrate_dense: past C_in %d only the fused path builds from the map",
                          kDenseMaxCin);
@@ -2855,6 +3347,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int nel_max = nk_max * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
     if (p.path == VDTTFS_PATH_FUSED && lds_list) {
+        if (shared) return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), epi, culif != nullptr);
         // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
         if (!counters && m.in_bytes > 0) {
