@@ -1356,15 +1356,27 @@ __device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
 // Receptive element f = 64 c + lane of the shared-list build: tap k =
 // f / C_in (the float quotient's fractional part is >= 0.5 / C_in, far above
 // its rounding error for the C_in this kernel takes), cin ci; its spike time
-// t and weight row.  A chunk of a layer with C_in >= 64 (or one tap) spans at
-// most two taps, k0 = the tap of its first element and k0 + 1, whose table
-// entries come from readlane; otherwise from the wave's LDS tap table.
-// Elements past the end load the map's first word and are no event.
+// t and weight row.  With C_in a multiple of 64 a chunk lies in one tap,
+// whose table entries are scalars (readlane); a chunk of a layer with
+// C_in >= 64 (or one tap) spans at most two taps, k0 = the tap of its first
+// element and k0 + 1, chosen per lane; otherwise the entries come from the
+// wave's LDS tap table.  Elements past the end load the map's first word and
+// are no event.
 __device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, int nel, int nk, int tcol, int trow,
                                                const int* ktab, float& t, int& row) {
     const int lane = lane_id();
     const int f = c * 64 + lane;
     const bool in = f < nel;
+    const __amdgpu_buffer_rsrc_t rin =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+    if ((a.C_in & 63) == 0) {  // uniform: the chunk lies in one tap, k0 = 64 c / C_in
+        const int k0 = __builtin_amdgcn_readfirstlane((int)(((float)(c * 64) + 0.5f) * a.inv_cin));
+        const int ci = c * 64 - k0 * a.C_in + lane;
+        row = __builtin_amdgcn_readlane(trow, k0) + ci;
+        t = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rin, (__builtin_amdgcn_readlane(tcol, k0) + ci) * 4, 0, 0));
+        return;  // f < nel: nel is a multiple of 64
+    }
     const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
     const int ci = f - k * a.C_in;
     int co, ro;
@@ -1379,8 +1391,6 @@ __device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, i
         ro = ktab[16 + k];
     }
     row = ro + ci;
-    const __amdgpu_buffer_rsrc_t rin =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
     t = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? (co + ci) * 4 : 0, 0, 0));
     if (!in) t = kInfTime;
 }
@@ -2766,13 +2776,16 @@ int64_t shared_nel_max(const IntegShape& sh) {
     return (int64_t)kh * kw * sh.C_in;
 }
 
-// Waves of one shared-list workgroup: one per c_out block, at most four.
-// Wider layers take several workgroups per pixel (c_out groups), which the
-// kernel pins to XCDs: VGG-16's 512-wide layers at 64 c_out per wave take
-// two groups, so that an XCD's L2 holds half of a 9.4 MB weight tensor
-// (measured on conv 8, 512 -> 512 at 4x4: L2 hit rate 0.69 with one group of
-// four 128-wide waves, 0.99 with two groups).
-int shared_waves(int64_t n_cblk) { return (int)(n_cblk < kSharedMaxWaves ? n_cblk : kSharedMaxWaves); }
+// Waves of one shared-list workgroup: one per c_out block, covering at most
+// 256 c_out (four 64-wide or two 128-wide blocks).  Wider layers take several
+// workgroups per pixel (c_out groups), which the kernel pins to XCDs:
+// VGG-16's 512-wide layers take two groups, so that an XCD's L2 holds half
+// of a 9.4 MB weight tensor (measured on conv 8, 512 -> 512 at 4x4: L2 hit
+// rate 0.69 with one group of four 128-wide waves, 0.99 with two groups).
+int shared_waves(int64_t n_cblk, int gather) {
+    const int64_t most = gather == 2 ? 2 : kSharedMaxWaves;
+    return (int)(n_cblk < most ? n_cblk : most);
+}
 
 // List capacity of a shared-list workgroup, in entries: the pixel's most
 // receptive elements, but at most what keeps the workgroup's LDS near 5 KB
@@ -2793,7 +2806,7 @@ int shared_cap(int64_t nel_max, int waves, bool alphas) {
 // each streaming one c_out block (64 c_out at epi 1, 128 at epi 2).
 int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
                          const float* theta, int64_t nel_max, int epi, bool culif) {
-    const int waves = shared_waves(a.n_cblk);
+    const int waves = shared_waves(a.n_cblk, epi == 2 ? 2 : 1);
     const int64_t n_grp = (a.n_cblk + waves - 1) / waves;
     const int64_t blocks = a.n_pix * n_grp;
     if (blocks <= 0) return VDTTFS_OK;
@@ -2908,7 +2921,7 @@ bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
         return false;
     if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0)) return false;
     const int64_t n_cblk = (sh.C_out + (gather == 2 ? 127 : 63)) / (gather == 2 ? 128 : 64);
-    const int waves = shared_waves(n_cblk);
+    const int waves = shared_waves(n_cblk, gather);
     const int cap = shared_cap(nel_max, waves, true);
     return (size_t)shared_block_words(cap, ctx->c.T, true, waves) * sizeof(int) <= kFusedMaxLds;
 }
