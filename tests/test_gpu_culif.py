@@ -309,15 +309,14 @@ def test_culif_engine_tail_steps(gpu_ctx_factory, decay, th):
 
 
 def test_culif_config4_full(gpu_ctx_factory):
-    """Config 4 at full size (2x128x128, T=64, B=64): the first 16 samples
-    equal the oracle at every layer; Delta in {16, 64} gives bit-identical
-    maps."""
+    """Config 4 at full size (2x128x128, T=64, B=64): all 64 samples equal
+    the oracle at every layer; Delta in {16, 64} gives bit-identical maps."""
     w = models.culif7()
     B = 64
     ev = models.dvs_events(w, B)
     say("culif config 4 B=64 delta=32")
     outs, pred = run_engine(gpu_ctx_factory(w.consts), w, B, ev)
-    k = 16
+    k = B
     ref, rpred = oracle.culif_net_forward(w.layers, ev[:k], k, w.consts.T, w.consts.delta)
     for i, (g, o) in enumerate(zip(outs, ref)):
         o = o.reshape((k,) + g.shape[1:])

@@ -111,8 +111,8 @@ def test_vgg16_b256_every_layer_vs_oracle(gpu_ctx_factory):
 @pytest.mark.parametrize("density", [0.01, 0.05, 0.2, 0.5])
 def test_fc_sweep_config5(gpu_ctx_factory, density):
     """Config 5 layer at every T' of the sweep (16, 32, 64): B=512 on the
-    GPU, the first 64 images against the oracle, and bit-identical outputs
-    across Delta in {8, 16, 32} (Delta > T' is one chunk cut at T')."""
+    GPU, all 512 images against the oracle, and bit-identical outputs across
+    Delta in {8, 16, 32} (Delta > T' is one chunk cut at T')."""
     say(f"FC 4096x4096 sweep density={density}")
     B, cin, cout = 512, 4096, 4096
     layer = models.fc_sweep_layer()
@@ -134,7 +134,7 @@ def test_fc_sweep_config5(gpu_ctx_factory, density):
         np.testing.assert_array_equal(outs[0], outs[1])
         np.testing.assert_array_equal(outs[0], outs[2])
         c = oracle.Consts(Tp, 0.0, 8, False)
-        nb = 64
+        nb = B
         cin_, tin_, off_ = oracle.bucketize(c, sp[:nb], nb, cin)
         exp, _, _ = oracle.integrate(c, cin_, tin_, off_, layer.kernel, layer.bias, alpha, theta, 0,
                                      nb, 1, 1, cin, 1, 1, cout, 1, 1, 0, True)
