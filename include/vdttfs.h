@@ -142,11 +142,15 @@ int vdttfs_layer_forward(vdttfs_ctx* ctx, float* d_out, const float* d_in,
  * scratch in a 64 MiB device buffer that the library holds per GPU until the
  * process ends, instead of context scratch grown with hipMalloc.  The call
  * allocates and frees nothing.  A layer whose scratch exceeds 64 MiB fails
- * with VDTTFS_E_UNSUPPORTED (the LDS-list and register paths need none; a
- * 3x3 conv needs about (9*C_in + 32)*8 + 4*(T+1) bytes per output pixel).
- * Every call on one GPU shares that GPU's buffer: calls that overlap on one
- * GPU (two streams, two host threads, or two contexts on the same device)
- * race and must be serialised by the caller. */
+ * with VDTTFS_E_UNSUPPORTED (the LDS-list and register paths need none: every
+ * layer of the VGG-16 and LeNet-5 configurations runs; a layer on the
+ * bucketize + merge path, e.g. a 5x5 conv with C_in > 64, needs about
+ * (25*C_in + 32)*8 + 4*(T+1) bytes per output pixel).  Every call on one GPU
+ * shares that GPU's buffer, so calls that use it are ordered on the device in
+ * the order they are made, across contexts, streams and host threads (each
+ * waits on a per-device event the previous one recorded).  A call on a
+ * stream under graph capture records no such event: replays of captured
+ * graphs that use the buffer must be ordered by the caller. */
 int vdttfs_layer_forward_noalloc(vdttfs_ctx* ctx, float* d_out, const float* d_in, const float* d_kernel,
                                  const float* d_bias, const float* d_lut_decay, const float* d_lut_th, int t_min,
                                  int B, int H_in, int W_in, int C_in, int H_out, int W_out, int C_out, int K_h,

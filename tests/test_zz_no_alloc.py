@@ -3,8 +3,10 @@ library's static per-GPU scratch must give exactly what vdttfs_layer_forward
 (context scratch grown with hipMalloc) gives, on two calls in a row -- the
 second with a smaller input, so stale scratch from the first call cannot
 leak into it -- on every list path (fused with one or two events per load,
-the shared-list fused kernel, dense, bins, narrow, register, FC), and reject
-a layer whose scratch exceeds the buffer."""
+the shared-list fused kernel, dense, bins, narrow, register, FC) and on
+VGG-16's conv 4-9 shapes at B=256; reject a layer whose scratch exceeds the
+buffer; leave the device's free memory unchanged on a fresh context; and
+order calls from two contexts that share the buffer."""
 import sys
 import zlib
 
@@ -28,6 +30,11 @@ CASES = [
     ("narrow 6->16 5x5 valid", False, False, (40, 7), 12, 12, 6, 16, 5),
     ("register 1->6 5x5 valid", False, False, (50, 9), 28, 28, 1, 6, 5),
     ("fc 600->300", True, True, (40, 13), 1, 1, 600, 300, 1),
+    # VGG-16's conv 4-9 shapes at the benchmark batch: lists in LDS, no scratch
+    ("vgg conv4 128->256 8x8 B=256", True, False, (256, 64), 8, 8, 128, 256, 3),
+    ("vgg conv5 256->256 8x8 B=256", True, False, (256, 64), 8, 8, 256, 256, 3),
+    ("vgg conv7 256->512 4x4 B=256", True, False, (256, 64), 4, 4, 256, 512, 3),
+    ("vgg conv8 512->512 4x4 B=256", True, False, (256, 64), 4, 4, 512, 512, 3),
 ]
 
 
@@ -101,3 +108,89 @@ def test_noalloc_rejects_oversized_layer(gpu_ctx_factory):
     assert "scratch" in _lib.last_error()
     out = d_out.download()
     assert np.all(out.view(np.uint32) == 0x7F7F7F7F)
+
+
+def hip_free_bytes():
+    """Free device memory of the current device, from the HIP runtime."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def bins_layer(rng, tc, B, C_in=80, C_out=64, H=8, K=5):
+    """A 5x5 conv past the dense path's C_in limit: bucketize + merge lists in
+    the scratch buffer (about 1 MB per image)."""
+    fan = K * K * C_in
+    Wt = (rng.standard_normal(fan * C_out) * np.sqrt(2.0 / fan)).astype(np.float32)
+    bias = (rng.standard_normal(C_out) * 0.05).astype(np.float32)
+    sp, sh = layer(rng, tc, False, B, H, H, C_in, C_out, K)
+    return Wt, bias, sp, sh
+
+
+def test_noalloc_fresh_context_allocates_nothing(gpu_ctx_factory):
+    """On a fresh context the scratch-free call on a bins-path layer (about
+    50 MB of lists in the static buffer) leaves the device's free memory
+    unchanged, while vdttfs_layer_forward on the same layer grows the
+    context's scratch by about as much."""
+    say("noalloc fresh context, device memory")
+    tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
+    ctx = gpu_ctx_factory(tc)
+    rng = np.random.default_rng(zlib.crc32(b"noalloc-fresh"))
+    Wt, bias, sp, sh = bins_layer(rng, tc, 48)
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    d_W, d_b, d_a, d_t = ctx.to_device(Wt), ctx.to_device(bias), ctx.to_device(alpha), ctx.to_device(theta)
+    d_in = ctx.to_device(sp)
+    n_out = 48 * sh["H_out"] * sh["W_out"] * sh["C_out"]
+    d_new, d_ref = ctx.empty(n_out), ctx.empty(n_out)
+    args = [sh[k] for k in ("B", "H_in", "W_in", "C_in", "H_out", "W_out", "C_out", "K_h", "K_w")]
+    L = vdttfs.lib()
+
+    def noalloc():
+        assert L.vdttfs_layer_forward_noalloc(ctx.handle, d_new.ptr, d_in.ptr, d_W.ptr, d_b.ptr, d_a.ptr, d_t.ptr,
+                                              1, *args, 0) == 0, _lib.last_error()
+        ctx.synchronize()
+
+    noalloc()  # the first launches load the kernels' code
+    before = hip_free_bytes()
+    for _ in range(3):
+        noalloc()
+    assert hip_free_bytes() == before
+    ctx.layer_forward(d_ref, d_in, d_W, d_b, d_a, d_t, 1, is_fc=False, **sh)
+    ctx.synchronize()
+    assert before - hip_free_bytes() >= 32 << 20, "layer_forward grows context scratch (the check is sensitive)"
+    np.testing.assert_array_equal(d_new.download(), d_ref.download())
+
+
+def test_noalloc_two_contexts_in_call_order(gpu_ctx_factory):
+    """Two contexts (two streams) enqueue scratch-using calls back to back
+    with no synchronisation between them; every result equals
+    vdttfs_layer_forward's."""
+    say("noalloc two contexts")
+    tc = vdttfs.task2_consts(T=64, delta=8, tfs=32.0)
+    ca, cb = gpu_ctx_factory(tc), gpu_ctx_factory(tc)
+    rng = np.random.default_rng(zlib.crc32(b"noalloc-two"))
+    alpha, theta = vdttfs.build_luts_host(tc, 16.0, 0.0, 16.0, 0.0)
+    L = vdttfs.lib()
+    jobs = []
+    for ctx, B, C_in in ((ca, 40, 80), (cb, 24, 96), (ca, 16, 72), (cb, 32, 88)):
+        Wt, bias, sp, sh = bins_layer(rng, tc, B, C_in=C_in)
+        dev = [ctx.to_device(x) for x in (Wt, bias, alpha, theta, sp)]
+        n_out = B * sh["H_out"] * sh["W_out"] * sh["C_out"]
+        d_ref, d_new = ctx.empty(n_out), ctx.empty(n_out).fill(0xFF)
+        ctx.layer_forward(d_ref, dev[4], dev[0], dev[1], dev[2], dev[3], 1, is_fc=False, **sh)
+        ctx.synchronize()
+        jobs.append((ctx, sh, dev, d_ref, d_new))
+    for rnd in range(3):
+        for ctx, sh, dev, _, d_new in (jobs if rnd % 2 == 0 else jobs[::-1]):
+            args = [sh[k] for k in ("B", "H_in", "W_in", "C_in", "H_out", "W_out", "C_out", "K_h", "K_w")]
+            rc = L.vdttfs_layer_forward_noalloc(ctx.handle, d_new.ptr, dev[4].ptr, dev[0].ptr, dev[1].ptr,
+                                                 dev[2].ptr, dev[3].ptr, 1, *args, 0)
+            assert rc == 0, _lib.last_error()
+        ca.synchronize()
+        cb.synchronize()
+        for i, (_, _, _, d_ref, d_new) in enumerate(jobs):
+            np.testing.assert_array_equal(d_new.download(), d_ref.download(), err_msg=f"round {rnd} job {i}")
+            d_new.fill(0xFF)

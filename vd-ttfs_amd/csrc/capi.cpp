@@ -153,7 +153,9 @@ int vdttfs_create(const vdttfs_consts* consts, int device, vdttfs_ctx** out) {
     if (device < 0 || device >= n)
         return set_error(VDTTFS_E_INVALID, "device %d out of range (%d devices)", device, n);
     VD_HIP(hipSetDevice(device));
-    VD_TRY(noalloc_setup(device));
+    // the scratch-free entry point's per-device set-up; only that entry point
+    // needs it, and it retries and reports a failure itself
+    if (noalloc_setup(device) != VDTTFS_OK) (void)hipGetLastError();
     vdttfs_ctx* ctx = new (std::nothrow) vdttfs_ctx();
     if (!ctx) return set_error(VDTTFS_E_NOMEM, "context allocation failed");
     ctx->c = *consts;

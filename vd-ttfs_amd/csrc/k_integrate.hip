@@ -213,6 +213,9 @@ struct DenseMergeArgs {
 constexpr int kDenseMaxBins = 256;
 constexpr int kDenseMaxCin = 64;
 constexpr int kQuadMaxCin = 128;  // k_stream_quad's list build: 18 chunks of 64 per 3x3 pixel
+// quad_build packs an event's weight row (tap * C_in + cin < 9 * kQuadMaxCin)
+// into bits 21..31 of its register
+static_assert(9 * kQuadMaxCin <= (1 << 11), "quad_build's 11-bit weight-row field");
 constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 
 // Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
@@ -1197,7 +1200,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int f = c * 64 + lane;
             const bool in = f < nel;
             const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
-            const int ci = f - (int)__umul24((unsigned)k, (unsigned)a.C_in);  // k <= 8, C_in <= 64
+            const int ci = f - (int)__umul24((unsigned)k, (unsigned)a.C_in);  // k <= 8, C_in <= 128
             rw[c] = kinfo[KMAX + k] + ci;
             const int off = (kinfo[k] + ci) * 4;
             xs[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? off : 0, 0, 0));

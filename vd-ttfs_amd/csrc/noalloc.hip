@@ -7,10 +7,17 @@
 // runs on (held until the process ends).  In host code the array's name is a
 // host-side stand-in, not a device address: each device's copy is looked up
 // once with hipGetSymbolAddress when a context is created on it
-// (noalloc_setup, called by vdttfs_create) and only that pointer is ever
-// passed to kernels.  No kernel needs the scratch cleared: every entry a
-// stream kernel reads (list, zero tail, bin starts, bucket offsets) is
-// written by the list builders of the same call.
+// (noalloc_setup, called by vdttfs_create; if that fails the entry point
+// retries and reports it) and only that pointer is ever passed to kernels.
+// No kernel needs the scratch cleared: every entry a stream kernel reads
+// (list, zero tail, bin starts, bucket offsets) is written by the list
+// builders of the same call.
+//
+// Calls that use the scratch are ordered on the device in the order they are
+// made, whatever their context or stream: under one lock, each waits on a
+// per-device event recorded after the previous such call's kernels, then
+// records it after its own.  A call on a stream under graph capture skips
+// the event (the captured graph's replays are ordered by the caller).
 #include <mutex>
 
 #include "common.h"
@@ -25,25 +32,41 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
-void* g_ptr[kMaxDevices];  // device address of `scratch` per device, set once
+void* g_ptr[kMaxDevices];         // device address of `scratch` per device, set once
+hipEvent_t g_done[kMaxDevices];   // recorded after each scratch-using call's kernels
+bool g_recorded[kMaxDevices];     // g_done has been recorded at least once
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-}  // namespace
-
-// Called by vdttfs_create with `device` current.
-int noalloc_setup(int device) {
+// With g_mu held and `device` current.
+int setup_locked(int device) {
     if (device < 0 || device >= kMaxDevices)
         return set_error(VDTTFS_E_UNSUPPORTED, "device %d beyond the scratch table (%d)", device, kMaxDevices);
-    std::lock_guard<std::mutex> lk(g_mu);
     if (g_ptr[device]) return VDTTFS_OK;
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr)
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();
         return set_error(VDTTFS_E_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
                          hipGetErrorString(e));
+    }
+    e = hipEventCreateWithFlags(&g_done[device], hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(VDTTFS_E_HIP, "event for the scratch order on device %d: %s", device, hipGetErrorString(e));
+    }
     g_ptr[device] = p;
     return VDTTFS_OK;
+}
+
+}  // namespace
+
+// Called by vdttfs_create with `device` current.  Only the scratch-free entry
+// point needs what it sets up, so a failure here does not fail the context:
+// the entry point retries and returns the error.
+int noalloc_setup(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return setup_locked(device);
 }
 
 size_t noalloc_scratch_bytes() { return kScratchBytes; }
@@ -75,13 +98,10 @@ extern "C" int vdttfs_layer_forward_noalloc(vdttfs_ctx* ctx, float* d_out, const
     s.pad_h = same ? K_h / 2 : 0;
     s.pad_w = same ? K_w / 2 : 0;
     VD_TRY(check_integ_shape(ctx, s));
-    void* base = nullptr;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (ctx->device >= 0 && ctx->device < kMaxDevices) base = g_ptr[ctx->device];
-    }
-    if (!base)
-        return set_error(VDTTFS_E_INVALID, "layer_forward_noalloc: no scratch set up for device %d", ctx->device);
+    // held until this call's kernels are enqueued and its event recorded
+    std::lock_guard<std::mutex> lk(g_mu);
+    VD_TRY(setup_locked(ctx->device));
+    void* base = g_ptr[ctx->device];
     LaunchPlan p;
     VD_TRY(resolve_plan(ctx, s, LaunchPlan{}, &p));
     const int64_t cols = s.is_fc ? s.B : (int64_t)s.B * s.H_in * s.W_in;
@@ -105,10 +125,28 @@ extern "C" int vdttfs_layer_forward_noalloc(vdttfs_ctx* ctx, float* d_out, const
     int32_t* bstart = bs_b ? reinterpret_cast<int32_t*>(sp + list_b) : nullptr;
     vd_event* ev = ev_b ? reinterpret_cast<vd_event*>(sp + list_b + bs_b) : nullptr;
     int32_t* off = off_b ? reinterpret_cast<int32_t*>(sp + list_b + bs_b + ev_b) : nullptr;
-    if (dense)
+    if (need == 0)  // lists in LDS: the scratch is not touched, nothing to order
         return launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, list, cap, bstart, d_kernel, d_bias,
                                       d_lut_th, t_min, s, nullptr, nullptr, &p);
-    VD_TRY(launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, ev, off, nullptr));
-    return launch_integrate_bins(ctx, d_out, ev, off, list, cap, bstart, d_kernel, d_bias, d_lut_th, t_min, s,
-                                 nullptr, nullptr, &p);
+    // after the previous scratch-using call on this GPU, in call order
+    const int dev = ctx->device;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VD_HIP(hipStreamIsCapturing(ctx->stream, &cs));
+    const bool order = cs == hipStreamCaptureStatusNone;
+    if (order && g_recorded[dev]) VD_HIP(hipStreamWaitEvent(ctx->stream, g_done[dev], 0));
+    int rc;
+    if (dense) {
+        rc = launch_integrate_dense(ctx, d_out, d_in, d_lut_decay, list, cap, bstart, d_kernel, d_bias, d_lut_th,
+                                    t_min, s, nullptr, nullptr, &p);
+    } else {
+        rc = launch_bucketize_bins(ctx, d_in, cols, C_in, d_lut_decay, ev, off, nullptr);
+        if (rc == VDTTFS_OK)
+            rc = launch_integrate_bins(ctx, d_out, ev, off, list, cap, bstart, d_kernel, d_bias, d_lut_th, t_min,
+                                       s, nullptr, nullptr, &p);
+    }
+    if (order) {
+        VD_HIP(hipEventRecord(g_done[dev], ctx->stream));
+        g_recorded[dev] = true;
+    }
+    return rc;
 }
