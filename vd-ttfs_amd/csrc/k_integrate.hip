@@ -3085,11 +3085,16 @@ int64_t cu_count(const vdttfs_ctx* ctx) {
     return nc;
 }
 
-// Whether the built-in plan takes the shared-list kernel where it applies.
+// Whether the built-in plan takes the shared-list kernel where it applies:
+// where a pixel's c_out fit at most two workgroups.  Each workgroup builds
+// the pixel's list itself, so wider layers (config 5's 4096-wide FC: 16
+// groups of 256 c_out) keep bucketize + merge, which build it once.
 bool shared_builtin(const vdttfs_ctx* ctx, const IntegShape& sh) {
     (void)ctx;
-    (void)sh;
-    return true;
+    const int g = shared_gather(sh);
+    const int64_t n_cblk = (sh.C_out + (g == 2 ? 127 : 63)) / (g == 2 ? 128 : 64);
+    const int waves = shared_waves(n_cblk, g);
+    return (n_cblk + waves - 1) / waves <= 2;
 }
 
 int plan_error(const IntegShape& sh, const char* what) {
