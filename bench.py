@@ -524,15 +524,16 @@ def bench_ttfs(args) -> int:
             "unit": "GB/s",
             "frac": hbm / HBM_PEAK_GBS if tr else None,
             "traffic": tr["per_step"] / tr["launches"] if tr else None,
-            "kernel": "integrator = one layer's list build + stream: k_stream_quad (conv, <= 9 taps, "
-                      "C_in <= 128, 32 <= C_out <= 128: merged list built in LDS, four events per dwordx4 load "
-                      "up to 64 c_out, two up to 128), k_merge_dense + k_stream_lean (other conv, C_in <= 64) or "
-                      "k_bucketize + k_merge + k_stream_lean (wider conv; FC) with pair or four-c_out-per-lane "
-                      "dwordx4 gathers (k_stream for one c_out per lane); layers with C_out < 32 stream with "
-                      "k_stream_narrow, or with k_conv_small when the receptive field has <= 32 elements.  A "
-                      "launch is one layer's integrate; achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE bytes of "
-                      "the integrator dispatches of one forward / the live HIP-event integrator time of a "
-                      "forward",
+            "kernel": "integrator = one layer's list build + stream: k_stream_quad, the merged list built in "
+                      "LDS, per wave (conv, <= 9 taps, C_in <= 128, 32 <= C_out <= 128: four events per dwordx4 "
+                      "load up to 64 c_out, two up to 128) or shared by a workgroup of up to four waves (every "
+                      "other conv with <= 9 taps and FC layer whose pixel takes at most two workgroups: 64 or 128 "
+                      "c_out per wave, c_out groups pinned to XCDs); otherwise k_merge_dense + k_stream_lean or "
+                      "k_bucketize + k_merge + k_stream_lean (e.g. config 5's 4096-wide FC); layers with C_out < "
+                      "32 stream with k_stream_narrow, or with k_conv_small when the receptive field has <= 32 "
+                      "elements.  A launch is one layer's integrate; achieved = rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                      "bytes of the integrator dispatches of one forward / the live HIP-event integrator time of "
+                      "a forward",
             "traffic_per_step": tr["per_step"] if tr else None,
             "traffic_source": (os.path.relpath(traffic_file(tag), ROOT) if tr else
                                f"no counter summary for {key} in profiles/"),

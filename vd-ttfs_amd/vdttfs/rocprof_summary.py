@@ -42,7 +42,7 @@ COPY_BYTES_DEFAULT = 1 << 30  # bench.py --copy-calibration moves 2^28 floats ea
 
 
 def short_name(n: str) -> str:
-    m = re.search(r"(k_\w+(<[\w, ]+>)?)", n)
+    m = re.search(r"(k_\w+(<[\w, -]+>)?)", n)
     if m:
         return m.group(1)
     return n.split("(")[0][-48:]
