@@ -1595,7 +1595,8 @@ template <int GEO, int NB, bool CULIF>
 __global__ __launch_bounds__(64 * kQuadWaves)
 __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void k_stream_quad(
     DenseMergeArgs m, StreamArgs a, float* __restrict__ out, const float* __restrict__ theta, int nel_max) {
-    static_assert(GEO == 4 || GEO == 2, "four events per load (64 c_out) or two (128 c_out)");
+    static_assert(GEO == 4 || GEO == 2 || (GEO == 1 && NB <= 0),
+                  "four events per load (64 c_out), two (128 c_out), or one (256 c_out, shared lists)");
     constexpr int OWN = 4 / GEO;  // c_out per lane
     constexpr int LPG = 8 / GEO;  // loads per group of 8 events
     // NB <= 0: one pixel per workgroup, its list shared by the workgroup's
@@ -1623,9 +1624,10 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
     const int lane = lane_id();
     // GEO 4: lane (q, r) = (lane / 16, lane % 16) loads c_out 4r..4r+3 of
     // event q and owns c_out 4r+q; GEO 2: lane (q, r) = (lane / 32, lane % 32)
-    // loads c_out 4r..4r+3 of event q and owns c_out 4r+2q, 4r+2q+1
-    const int q = GEO == 4 ? lane >> 4 : lane >> 5;
-    const int r = GEO == 4 ? (lane & 15) : (lane & 31);
+    // loads c_out 4r..4r+3 of event q and owns c_out 4r+2q, 4r+2q+1; GEO 1:
+    // lane r loads and owns c_out 4r..4r+3 of every event (no exchange)
+    const int q = GEO == 4 ? lane >> 4 : (GEO == 2 ? lane >> 5 : 0);
+    const int r = GEO == 4 ? (lane & 15) : (GEO == 2 ? (lane & 31) : lane);
     int cb = 0;           // SHARED: this wave's c_out block (64 or 128 wide)
     int64_t spix = 0;     // SHARED: the workgroup's pixel
     if constexpr (SHARED) {
@@ -1645,8 +1647,9 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
         spix = mbr * per + (mbr < rem ? mbr : rem) + j / S;
         cb = (bi - j * n_grp) * W + wave;
     }
-    const int co = (GEO == 4 ? 4 * r + q : 4 * r + 2 * q) + cb * (GEO == 4 ? 64 : 128);  // first c_out of the lane
-    const int voff = 16 * r + cb * (GEO == 4 ? 256 : 512);
+    const int co = (GEO == 4 ? 4 * r + q : (GEO == 2 ? 4 * r + 2 * q : 4 * r)) +
+                   cb * (64 * (4 / GEO));  // first c_out of the lane
+    const int voff = 16 * r + cb * (256 * (4 / GEO));
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
     const int T = a.T;
@@ -1712,11 +1715,37 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
             f4 al[AL_AHEAD ? 2 : 1];
         };
         auto load = [&](int j, Raw& g) {
+            if constexpr (GEO == 1) {
+                // one event per load, its row wave-uniform: the eight rows
+                // come with one or two broadcast LDS reads, and each row's
+                // byte offset goes to the load's scalar offset
+                unsigned so[8];
+                if constexpr (CULIF) {
+                    const u4 ra = *reinterpret_cast<const u4*>(rows + j);
+                    const u4 rb = *reinterpret_cast<const u4*>(rows + j + 4);
 #pragma unroll
-            for (int k = 0; k < LPG; ++k) {
-                const int off = CULIF ? rows[j + GEO * k + q] + voff
-                                      : (int)__umul24((unsigned)rows16[j + GEO * k + q], (unsigned)m.rowbytes) + voff;
-                g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+                    for (int k = 0; k < 4; ++k) {
+                        so[k] = __builtin_amdgcn_readfirstlane(ra[k]);
+                        so[4 + k] = __builtin_amdgcn_readfirstlane(rb[k]);
+                    }
+                } else {
+                    const u4 rr = *reinterpret_cast<const u4*>(rows16 + j);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const unsigned pr = __builtin_amdgcn_readfirstlane(rr[k]);
+                        so[2 * k] = (pr & 0xFFFFu) * (unsigned)m.rowbytes;
+                        so[2 * k + 1] = (pr >> 16) * (unsigned)m.rowbytes;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < LPG; ++k) g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, (int)so[k], 0);
+            } else {
+#pragma unroll
+                for (int k = 0; k < LPG; ++k) {
+                    const int off = CULIF ? rows[j + GEO * k + q] + voff
+                                          : (int)__umul24((unsigned)rows16[j + GEO * k + q], (unsigned)m.rowbytes) + voff;
+                    g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+                }
             }
             if constexpr (AL_AHEAD) {
                 g.al[0] = *reinterpret_cast<const f4*>(alph + j);
@@ -1772,6 +1801,13 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
             float w[8][OWN], al[8];
 #pragma unroll
             for (int k = 0; k < LPG; ++k) {
+                if constexpr (GEO == 1) {  // the lane's own four c_out of event k
+                    w[k][0] = __uint_as_float(g.x[k].x);
+                    w[k][1 % OWN] = __uint_as_float(g.x[k].y);
+                    w[k][2 % OWN] = __uint_as_float(g.x[k].z);
+                    w[k][3 % OWN] = __uint_as_float(g.x[k].w);
+                    continue;
+                }
                 unsigned c0 = g.x[k].x, c1 = g.x[k].y, c2 = g.x[k].z, c3 = g.x[k].w;
                 // permlane32_swap(x, y): x's lanes 32..63 <-> y's lanes 0..31
                 auto p = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
@@ -2780,13 +2816,13 @@ int64_t shared_nel_max(const IntegShape& sh) {
 }
 
 // Waves of one shared-list workgroup: one per c_out block, covering at most
-// 256 c_out (four 64-wide or two 128-wide blocks).  Wider layers take several
+// 256 c_out (four 64-wide, two 128-wide or one 256-wide block).  Wider layers take several
 // workgroups per pixel (c_out groups), which the kernel pins to XCDs:
 // VGG-16's 512-wide layers take two groups, so that an XCD's L2 holds half
 // of a 9.4 MB weight tensor (measured on conv 8, 512 -> 512 at 4x4: L2 hit
 // rate 0.69 with one group of four 128-wide waves, 0.99 with two groups).
 int shared_waves(int64_t n_cblk, int gather) {
-    const int64_t most = gather == 2 ? 2 : kSharedMaxWaves;
+    const int64_t most = gather == 4 ? 1 : (gather == 2 ? 2 : kSharedMaxWaves);
     return (int)(n_cblk < most ? n_cblk : most);
 }
 
@@ -2798,9 +2834,13 @@ int shared_waves(int64_t n_cblk, int gather) {
 // capacity of 2,640 at four waves: 0.633 -> 0.533 ms against lists sized to
 // the field).
 constexpr int kSharedLdsPerWave = 5 * 1024;
-int shared_cap(int64_t nel_max, int waves, bool alphas) {
+// A 256-wide wave (one event per load) keeps 16 loads in flight, so fewer of
+// them hide the gathers' latency: about 16 KB of list per wave.
+constexpr int kSharedLdsPerLeanWave = 16 * 1024;
+int shared_cap(int64_t nel_max, int waves, bool alphas, int gather) {
     const int64_t per = alphas ? 6 : 4;  // 16-bit row and alpha, or row byte offset
-    const int64_t lim = (((int64_t)kSharedLdsPerWave - 4 * kSharedWaveWords) * waves / per) & ~INT64_C(15);
+    const int64_t budget = gather == 4 ? kSharedLdsPerLeanWave : kSharedLdsPerWave;
+    const int64_t lim = ((budget - 4 * kSharedWaveWords) * waves / per) & ~INT64_C(15);
     const int64_t want = (nel_max + 15) & ~INT64_C(15);
     return (int)(want < lim ? want : lim);
 }
@@ -2808,13 +2848,13 @@ int shared_cap(int64_t nel_max, int waves, bool alphas) {
 // four c_out blocks), the W waves building the pixel's list together and
 // each streaming one c_out block (64 c_out at epi 1, 128 at epi 2).
 int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
-                         const float* theta, int64_t nel_max, int epi, bool culif) {
-    const int waves = shared_waves(a.n_cblk, epi == 2 ? 2 : 1);
+                         const float* theta, int64_t nel_max, int gather, bool culif) {
+    const int waves = shared_waves(a.n_cblk, gather);
     const int64_t n_grp = (a.n_cblk + waves - 1) / waves;
     const int64_t blocks = a.n_pix * n_grp;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-    const int cap = shared_cap(nel_max, waves, !culif);
+    const int cap = shared_cap(nel_max, waves, !culif, gather);
     const size_t lds = (size_t)shared_block_words(cap, m.T, !culif, waves) * sizeof(int);
     if (lds > kFusedMaxLds) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: shared list exceeds LDS");
 #define VD_LAUNCH_SHARED(G, NB, L)                                                                      \
@@ -2827,7 +2867,12 @@ int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamA
         else                            \
             VD_LAUNCH_SHARED(G, 0, L);  \
     } while (0)
-    if (epi == 2) {
+    if (gather == 4) {  // one event per load, four c_out per lane
+        if (culif)
+            VD_LAUNCH_SHARED_NB(1, true);
+        else
+            VD_LAUNCH_SHARED_NB(1, false);
+    } else if (gather == 2) {
         if (culif)
             VD_LAUNCH_SHARED_NB(2, true);
         else
@@ -2922,10 +2967,13 @@ bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     if (ctx->c.T > kBlockBins || taps > 9 || narrow_path_ok(sh, &wbytes) || !wave_path_ok(sh, &wbytes) ||
         in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF)
         return false;
-    if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0)) return false;
-    const int64_t n_cblk = (sh.C_out + (gather == 2 ? 127 : 63)) / (gather == 2 ? 128 : 64);
+    // gather 4 (256 c_out per wave) for layers wider than 128 only
+    if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0) && !(gather == 4 && sh.C_out % 4 == 0 && sh.C_out > 128))
+        return false;
+    const int cw = gather == 4 ? 256 : (gather == 2 ? 128 : 64);
+    const int64_t n_cblk = (sh.C_out + cw - 1) / cw;
     const int waves = shared_waves(n_cblk, gather);
-    const int cap = shared_cap(nel_max, waves, true);
+    const int cap = shared_cap(nel_max, waves, true, gather);
     return (size_t)shared_block_words(cap, ctx->c.T, true, waves) * sizeof(int) <= kFusedMaxLds;
 }
 
@@ -3092,7 +3140,8 @@ int64_t cu_count(const vdttfs_ctx* ctx) {
 bool shared_builtin(const vdttfs_ctx* ctx, const IntegShape& sh) {
     (void)ctx;
     const int g = shared_gather(sh);
-    const int64_t n_cblk = (sh.C_out + (g == 2 ? 127 : 63)) / (g == 2 ? 128 : 64);
+    const int cw = g == 4 ? 256 : (g == 2 ? 128 : 64);
+    const int64_t n_cblk = (sh.C_out + cw - 1) / cw;
     const int waves = shared_waves(n_cblk, g);
     return (n_cblk + waves - 1) / waves <= 2;
 }
@@ -3368,7 +3417,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int nel_max = nk_max * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
     if (p.path == VDTTFS_PATH_FUSED && lds_list) {
-        if (shared) return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), epi, culif != nullptr);
+        if (shared)
+            return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), p.gather, culif != nullptr);
         // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
         if (!counters && m.in_bytes > 0) {
