@@ -145,7 +145,7 @@ bool integrate_dense_ok(const vdttfs_ctx* ctx, const IntegShape& s);
 // Conv layers past those limits (C_in <= 128) that the fused plan still
 // builds from the dense map when no counters are asked for.
 bool quad_wide_ok(const vdttfs_ctx* ctx, const IntegShape& s);
-// Layers the shared-list fused kernel takes under gather 1 or 2 (conv with
+// Layers the shared-list fused kernel takes under gather 1, 2 or 4 (conv with
 // at most 9 taps or FC, T <= 64, no counters), and which fused kernel a
 // fused plan with this gather runs: 1 per-wave lists, 2 shared lists, 0 none.
 bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& s, int gather);

@@ -2955,8 +2955,9 @@ bool fused_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather);
 
 // Layers whose lists the shared-list kernel builds (k_stream_quad<GEO, 0>,
 // one output pixel per workgroup of up to four waves that share its list):
-// conv with at most 9 taps or FC, T <= 64, gather 1 (64 c_out per wave) or 2
-// (128 per wave, C_out % 4 == 0), weight rows below 2^16 (16-bit entries),
+// conv with at most 9 taps or FC, T <= 64, gather 1 (64 c_out per wave), 2
+// (128 per wave, C_out % 4 == 0) or 4 (one event per load, 256 c_out per
+// wave, C_out > 128), weight rows below 2^16 (16-bit entries),
 // 32-bit input offsets and a workgroup's list within the LDS limit.  No
 // counters: a counting forward takes bucketize + merge + stream.
 bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
@@ -3237,7 +3238,7 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
     const bool fused = kind == 1 || (kind == 2 && (req.path == VDTTFS_PATH_FUSED || shared_builtin(ctx, sh)));
     if (req.path == VDTTFS_PATH_DENSE && !dense) return plan_error(sh, "dense path outside its limits");
     if (req.path == VDTTFS_PATH_FUSED && !fused)
-        return plan_error(sh, "fused path needs T <= 64, at most 9 taps (or FC), gather 1 or 2 (C_out % 4 == 0), "
+        return plan_error(sh, "fused path needs T <= 64, at most 9 taps (or FC), gather 1, 2 or 4 (C_out % 4 == 0), "
                               "and the pixel's list within the LDS limit");
     if (req.path == VDTTFS_PATH_WINDOW && !window_ok(ctx, sh))
         return plan_error(sh, "window path needs T <= 64 and at most 9 taps (or an FC layer)");
