@@ -287,12 +287,16 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  *   path:   VDTTFS_PATH_BINS (bucketize + per-pixel merge), VDTTFS_PATH_DENSE
  *           (merge straight from the spike map; conv layers with <= 9 taps,
  *           C_in <= 64, or narrow layers with <= 25 taps), VDTTFS_PATH_FUSED
- *           (merge and integrate in one kernel, the list kept in LDS; dense
- *           layers, and conv layers with <= 9 taps and C_in <= 128, with
- *           T <= 64 and gather 1 with C_out <= 64, four events per 16-byte
- *           load, or gather 2 with C_out <= 128; counting forwards of a
- *           gather-2 layer run it as DENSE, of a layer past C_in 64 as
- *           BINS), VDTTFS_PATH_REG (no
+ *           (merge and integrate in one kernel, the list kept in LDS, T <=
+ *           64: per wave for dense layers and conv layers with <= 9 taps and
+ *           C_in <= 128, gather 1 with C_out <= 64, four events per 16-byte
+ *           load, or gather 2 with C_out <= 128; past those limits one
+ *           pixel's list shared by a workgroup's waves, conv layers with <= 9
+ *           taps and FC layers, gather 1, 2 or 4 (C_out > 128), ppw 1; with
+ *           gather 4 and ppw 4, one position of four images per wave, each
+ *           weight row applied to every image holding the event (selectable,
+ *           slower); counting forwards of a gather-2 layer run it as DENSE,
+ *           of a layer past C_in 64 as BINS), VDTTFS_PATH_REG (no
  *           list: each lane keeps its receptive field in registers; conv
  *           layers with K_h*K_w*C_in <= 32, C_out <= 64, T <= 64; gather 1,
  *           ppw 64 / C_out; counting forwards run it as DENSE or FUSED),

@@ -1930,6 +1930,451 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
 }
 
 // ---------------------------------------------------------------------------
+// k_stream_multi: weight rows reused across images.  One wave integrates one
+// output position of kMultiImages = 4 consecutive images over a block of 256
+// c_out (four per lane, one 16-byte load per weight row, no transposes), so a
+// weight row gathered once serves every image that holds the same (tap, cin)
+// event in the same bin.  The fire start (T2V:59-60) puts most events in bin
+// 0, where the images' events coincide often: at a bin-0 density d0 an
+// element is a bin-0 event of at least one of the four images with
+// probability 1 - (1 - d0)^4, against 4 d0 events (d0 = 0.35: 1.7 events per
+// row load).
+//  bin 0   the wave walks the receptive elements in (kh, kw, cin) order, 64
+//          per chunk, lane = element: a lane reads the element's spike time
+//          in the four images and forms the mask of images whose event falls
+//          in bin 0 and their alphas; the chunk's elements with a nonzero
+//          mask go, in element order, to a ring in LDS (row and mask, four
+//          alphas), and the stream takes the ring four entries at a time:
+//          one row load, then for each image of the entry's mask (a
+//          wave-uniform branch) four fmas into that image's bin sum.  An
+//          image absent from an entry is never touched, so each image's
+//          bin-0 chain is its own events in (kh, kw, cin) order, the
+//          reference's per-bin order (T2V:135-152);
+//  counts  the same pass counts every image's events of the later bins
+//          (LDS atomics that return nothing); a scan gives the bin ends;
+//  later   a second pass over the chunks places the later events, stable in
+//          (chunk, image, lane) order, at the bin's cursor plus the rank
+//          among the lanes of the same bin (shared_place's LDS bit masks), so
+//          within a bin each image's events stay in element order; entries
+//          hold the 16-bit row, the image (one-hot) and the alpha index.
+//          The stream closes bins in time order between entries as the
+//          per-wave kernels do, each entry's fmas going to its image.
+// A later list longer than the wave's capacity streams in windows (as the
+// shared-list kernel's NB = -1): the second pass runs once per window.
+// Measured on VGG-16 (per-layer HIP events, bit-identical maps): slower than
+// the shared-list kernel on every layer it takes.  B=256: the 8x8 layers
+// 0.39/0.56/0.56 -> 0.59/0.89/0.91 ms, the 4x4 layers 0.36/0.53/0.53 ->
+// 0.62/0.91/1.04, the 2x2 layers 4-5x, the FC 9x: a wave holds four images
+// x 256 c_out, so the 4x4 layers have 2,048 waves (two per SIMD) and the
+// FC 128, and each wave's entries wait on an LDS read, a readfirstlane and
+// the row's scalar offset before its load.  B=1024 (16,384 waves on the 8x8
+// layers): about even on conv 4, 5-15% slower on conv 5-6, 20-45% on the
+// 4x4 layers.  The union saves row loads (0.68 per event at input density
+// 0.48); each entry pays instead an LDS read of its row and mask, a
+// readfirstlane, four alphas and a branch per image.  So it is a plan the
+// caller may select (VDTTFS_PATH_FUSED, gather 4, 4 pixels per wave), not
+// the built-in one.
+constexpr int kMultiImages = 4;
+constexpr int kMultiRing = 128;  // bin-0 ring entries (a chunk adds at most 64 past the 8 ahead)
+constexpr int kMultiFixedWords = kMultiRing * 5 + 64 + 64 + 128 + 32;  // ring, counts, cursors, masks, taps
+
+__host__ __device__ inline int multi_wave_words(int cap) { return kMultiFixedWords + cap + kListPad; }
+
+// Three waves per SIMD: its LDS (about 12 KB per wave) allows about as many,
+// and the compiler then keeps the sixteen neurons' state in registers.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_stream_multi(
+    DenseMergeArgs m, StreamArgs a, float* __restrict__ out,
+                                                     const float* __restrict__ theta, int cap, int n_pos,
+                                                     int n_img) {
+    constexpr int NI = kMultiImages;
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) int lds_words[];
+    f4* al4 = reinterpret_cast<f4*>(lds_words);             // ring alphas, one f4 per entry
+    unsigned* rm = reinterpret_cast<unsigned*>(lds_words + 4 * kMultiRing);  // ring (row << 4) | mask
+    int* cnt = lds_words + 5 * kMultiRing;                   // later events per bin
+    int* cur = cnt + 64;                                     // later-bin cursors
+    unsigned* msk = reinterpret_cast<unsigned*>(cur + 64);   // rank masks, two words per bin
+    int* ktab = reinterpret_cast<int*>(msk + 128);           // tap table: offsets [0, 9), rows [16, 25)
+    unsigned* list = reinterpret_cast<unsigned*>(ktab + 32);  // later entries of the window
+    const int lane = lane_id();
+    const int T = a.T;
+    // block -> (c_out block, problem): blocks are dealt to the 8 XCDs
+    // round-robin, so block b's c_out block b % n_cblk pins each XCD to one
+    // block where n_cblk divides 8; the S = 8 / n_cblk XCDs of a block take
+    // contiguous ranges of problems (consecutive positions of one image
+    // group share input columns)
+    const int n_cblk = a.n_cblk;
+    const int n_prob = ((n_img + NI - 1) / NI) * n_pos;
+    const int bi = blockIdx.x;
+    const int cb = bi % n_cblk;
+    const int j0 = bi / n_cblk;
+    const int S = (8 % n_cblk == 0) ? 8 / n_cblk : 1;
+    const int mbr = j0 % S, per = n_prob / S, rem = n_prob - per * S;
+    const int prob = mbr * per + (mbr < rem ? mbr : rem) + j0 / S;
+    if (prob >= n_prob) return;
+    const int grp = prob / n_pos;
+    const int pos = prob - grp * n_pos;
+    const int img0 = grp * NI;
+    const int n_live = (n_img - img0) < NI ? (n_img - img0) : NI;  // images of this group
+    const int h_out = pos / m.W_out;
+    const int w_out = pos - h_out * m.W_out;
+    const int istride = m.H_in * m.W_in * m.C_in;  // one image's map (elements)
+    const int co = 4 * lane + cb * 256;
+    const int voff = 16 * lane + cb * 1024;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rin =
+        __builtin_amdgcn_make_buffer_rsrc((void*)m.in, (short)0, m.in_bytes, 0x00020000);
+    // lane d: theta[d] where a spike may occur in bin d (d >= t_min,
+    // theta[d] >= 1e-5), else NaN, which no carry compares >= to
+    const float th_d = lane < T ? theta[lane] : 0.0f;
+    const float v_th = (lane < T && lane >= a.t_min && th_d >= 1e-5f) ? th_d : __builtin_nanf("");
+    const float al_lane = lane <= T ? m.alpha[lane] : 0.0f;  // the decay LUT: alpha[lane], alpha[64]
+    const float al_64 = T == 64 ? m.alpha[64] : 0.0f;
+    const bool ok = co < a.C_out;  // C_out % 4 == 0: the lane's four c_out are all in or all out
+    float bias[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) bias[v] = ok ? a.bias[co + v] : 0.0f;
+    // taps of the position (the same in every image): lane s < nk holds tap
+    // s's input element offset in image img0 and its first weight row
+    int nk, tcol, trow;
+    {
+        bool vt = false;
+        int col = 0;
+        if (lane < m.K_h * m.K_w) {
+            const int kh = lane / m.K_w, kx = lane - kh * m.K_w;
+            const int hi = h_out - m.pad_h + kh, wi = w_out - m.pad_w + kx;
+            vt = hi >= 0 && hi < m.H_in && wi >= 0 && wi < m.W_in;
+            col = (img0 * m.H_in + hi) * m.W_in + wi;
+        }
+        const uint64_t mt = __ballot(vt);
+        nk = uniform(__popcll(mt));
+        if (vt) {
+            const int slot = __popcll(mt & lanemask_lt());
+            ktab[slot] = col * m.C_in;
+            ktab[16 + slot] = lane * m.C_in;
+        }
+        const int z = vzero();
+        cnt[lane] = z;
+        msk[lane] = z;
+        msk[64 + lane] = z;
+        wave_sync();
+        tcol = lane < nk ? ktab[lane] : 0;
+        trow = lane < nk ? ktab[16 + lane] : 0;
+    }
+    const int nel = nk * m.C_in;
+    const int n_chunks = (nel + 63) >> 6;
+    // chunk c's element per lane: its offset in image img0's map (-1 past
+    // the field) and its weight row (as shared_element)
+    auto element = [&](int c, int& eo, int& row) {
+        const int f = c * 64 + lane;
+        if ((m.C_in & 63) == 0) {  // uniform: the chunk lies in one tap
+            const int k0 = __builtin_amdgcn_readfirstlane((int)(((float)(c * 64) + 0.5f) * m.inv_cin));
+            const int ci = c * 64 - k0 * m.C_in + lane;
+            row = __builtin_amdgcn_readlane(trow, k0) + ci;
+            eo = __builtin_amdgcn_readlane(tcol, k0) + ci;
+            return;
+        }
+        const bool in = f < nel;
+        const int k = in ? (int)(((float)f + 0.5f) * m.inv_cin) : 0;
+        const int ci = f - k * m.C_in;
+        int c0, r0;
+        if (m.C_in >= 64 || nk == 1) {  // uniform
+            const int k0 = __builtin_amdgcn_readfirstlane(k);
+            const int k1 = k0 + 1 < nk ? k0 + 1 : k0;
+            const bool lo = k == k0;
+            c0 = lo ? __builtin_amdgcn_readlane(tcol, k0) : __builtin_amdgcn_readlane(tcol, k1);
+            r0 = lo ? __builtin_amdgcn_readlane(trow, k0) : __builtin_amdgcn_readlane(trow, k1);
+        } else {
+            c0 = ktab[k];
+            r0 = ktab[16 + k];
+        }
+        row = r0 + ci;
+        eo = in ? c0 + ci : -1;
+    };
+    // the element's spike times in the group's images (no event: kInfTime)
+    auto times = [&](int eo, float (&t)[NI]) {
+#pragma unroll
+        for (int p = 0; p < NI; ++p) {
+            const bool v = eo >= 0 && p < n_live;
+            t[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, v ? (eo + p * istride) * 4 : 0, 0, 0));
+            if (!v) t[p] = kInfTime;
+        }
+    };
+    auto alpha_of = [&](float t, int b) -> int {
+        return m.alpha_by_time ? (int)fminf(fmaxf(t, 0.0f), (float)T) : b;
+    };
+    // neuron state per (image, c_out of the lane): V (carry), the open bin's
+    // sum, the spike bin (kNoSpike while it has not fired; -1 for no neuron).
+    // The spike bins live in VGPRs, not as SGPR masks: sixteen 64-bit masks
+    // would take a third of the wave's scalar registers.
+    constexpr int kNoSpike = 0x7F;
+    float carry[NI][4], acc[NI][4];
+    int fb[NI][4];
+#pragma unroll
+    for (int p = 0; p < NI; ++p) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            carry[p][v] = bias[v];
+            acc[p][v] = 0.0f;
+            fb[p][v] = (p < n_live && ok) ? kNoSpike : -1;
+        }
+    }
+    // ---- bin 0: produce ring entries from the chunks, stream them ----
+    int tail = 0;  // ring entries produced
+    int c = 0;     // next chunk to produce
+    int eo_n = -1, row_n = 0;
+    float t_n[NI];
+    const uint64_t lt = lanemask_lt();
+    if (n_chunks > 0) {
+        element(0, eo_n, row_n);
+        times(eo_n, t_n);
+    }
+    auto produce = [&]() {
+        float t[NI];
+#pragma unroll
+        for (int p = 0; p < NI; ++p) t[p] = t_n[p];
+        const int row = row_n;
+        if (c + 1 < n_chunks) {  // uniform: the next chunk's loads go out first
+            element(c + 1, eo_n, row_n);
+            times(eo_n, t_n);
+        }
+        ++c;
+        unsigned mk = 0;
+        f4 al;
+#pragma unroll
+        for (int p = 0; p < NI; ++p) {
+            const int b = shared_bin(m, t[p]);
+            if (b > 0) atomicAdd(&cnt[b], 1);
+            const int ai = b == 0 ? alpha_of(t[p], 0) : 0;
+            const float x = __shfl(al_lane, ai & 63, 64);
+            al[p] = ai == 64 ? al_64 : x;
+            mk |= (b == 0 ? 1u : 0u) << p;
+        }
+        const uint64_t any = __ballot(mk != 0);
+        const int q = (tail + __popcll(any & lt)) & (kMultiRing - 1);
+        if (mk != 0) {
+            rm[q] = ((unsigned)row << 4) | mk;
+            al4[q] = al;
+        }
+        lds_order();
+        tail += __popcll(any);
+    };
+    auto ensure = [&](int upto) {
+        while (c < n_chunks && tail < upto) produce();  // uniform
+    };
+    struct Raw {
+        u4 x[4];
+        unsigned mk;  // four 4-bit image masks
+    };
+    auto load0 = [&](int j, Raw& g) {
+        const u4 e = *reinterpret_cast<const u4*>(rm + (j & (kMultiRing - 1)));
+        g.mk = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned s = __builtin_amdgcn_readfirstlane(e[i]);
+            const bool in = j + i < tail;
+            g.mk |= (in ? (s & 15u) : 0u) << (4 * i);
+            const int so = in ? (int)((s >> 4) * (unsigned)m.rowbytes) : 0;
+            g.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, so, 0);
+        }
+    };
+    auto consume0 = [&](int j, Raw& g) {
+        f4 A[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] = al4[(j + i) & (kMultiRing - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float w[4] = {__uint_as_float(g.x[i].x), __uint_as_float(g.x[i].y), __uint_as_float(g.x[i].z),
+                                __uint_as_float(g.x[i].w)};
+#pragma unroll
+            for (int p = 0; p < NI; ++p) {
+                if ((g.mk >> (4 * i + p)) & 1u) {  // uniform
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[p][v] = __builtin_fmaf(w[v], A[i][p], acc[p][v]);
+                }
+            }
+        }
+    };
+    {
+        Raw g0, g1;
+        ensure(8);
+        int j = 0;
+        if (tail > 0) {
+            load0(0, g0);
+            for (;;) {
+                ensure(j + 8);
+                load0(j + 4, g1);
+                __builtin_amdgcn_sched_barrier(0);
+                consume0(j, g0);
+                j += 4;
+                if (j >= tail) break;  // uniform: every chunk is produced (ensure)
+                ensure(j + 8);
+                load0(j + 4, g0);
+                __builtin_amdgcn_sched_barrier(0);
+                consume0(j, g1);
+                j += 4;
+                if (j >= tail) break;
+            }
+        }
+        while (c < n_chunks) produce();  // chunks without bin-0 events still count
+    }
+    // ---- later bins: ends, close bin 0, place and stream ----
+    lds_order();
+    const int tot = (lane >= 1 && lane < T) ? cnt[lane] : 0;
+    const int incl = wave_incl_scan(tot);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    int v_end = lane < T ? incl : INT_MAX;  // end of bin `lane` in the later list (bin 0: 0)
+    int b = 0;
+    int bend = 0;
+    // close bin b and the empty bins after it that end by position p; true
+    // when the stream is over
+    auto close_to = [&](int p) -> bool {
+#pragma unroll
+        for (int q = 0; q < NI; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                carry[q][v] = carry[q][v] + acc[q][v];
+                acc[q][v] = 0.0f;
+            }
+        const int stop = __popcll(__builtin_amdgcn_ballot_w64(v_end <= p));
+        uint64_t any;
+        do {
+            const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), b));
+            any = 0;
+#pragma unroll
+            for (int q = 0; q < NI; ++q)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint64_t fire = __ballot(carry[q][v] >= th);
+                    const uint64_t live = __ballot(fb[q][v] == kNoSpike);
+                    fb[q][v] = __builtin_amdgcn_inverse_ballot_w64(fire & live) ? b : fb[q][v];
+                    any |= live & ~fire;
+                }
+        } while (++b < stop);
+        if (b >= T || any == 0) return true;
+        bend = __builtin_amdgcn_readlane(v_end, b);
+        return false;
+    };
+    bool done = close_to(0);
+    // pass 2: place the later events of window [P0, P0 + cap)
+    auto place = [&](int P0) {
+        cur[lane] = incl - tot;
+        const int n_w = total - P0 < cap ? total - P0 : cap;
+        if (lane < kListPad) list[n_w + lane] = (unsigned)vzero();
+        lds_order();
+        const unsigned bit = 1u << (lane & 31);
+        for (int cc = 0; cc < n_chunks; ++cc) {  // uniform
+            int eo, row;
+            float t[NI];
+            element(cc, eo, row);
+            times(eo, t);
+#pragma unroll
+            for (int p = 0; p < NI; ++p) {
+                const int bb = shared_bin(m, t[p]);
+                const bool oth = bb > 0;
+                if (__ballot(oth) == 0) continue;  // uniform
+                if (oth) atomicOr(&msk[2 * bb + (lane >> 5)], bit);
+                lds_order();
+                uint64_t mm = 0;
+                int cbin = 0;
+                if (oth) {
+                    mm = *reinterpret_cast<const uint64_t*>(&msk[2 * bb]);
+                    cbin = cur[bb];
+                }
+                lds_order();
+                const int q = cbin + __popcll(mm & lt) - P0;
+                if (oth && (mm >> lane) == 1ull) {  // the bin's last lane in this chunk
+                    atomicAdd(&cur[bb], __popcll(mm));
+                    const int z = vzero();
+                    *reinterpret_cast<int2*>(&msk[2 * bb]) = make_int2(z, z);
+                }
+                lds_order();
+                if (oth && q >= 0 && q < cap)
+                    list[q] = (unsigned)row | (1u << (16 + p)) | ((unsigned)alpha_of(t[p], bb) << 20);
+            }
+        }
+        lds_order();
+    };
+    if (!done) {
+        const float al_64s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(al_64)));
+        struct RawL {
+            u4 x[4];
+            unsigned s[4];
+        };
+        auto loadL = [&](int j, RawL& g) {
+            const u4 e = *reinterpret_cast<const u4*>(list + j);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                g.s[i] = __builtin_amdgcn_readfirstlane(e[i]);
+                g.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, (int)((g.s[i] & 0xFFFFu) * (unsigned)m.rowbytes),
+                                                               0);
+            }
+        };
+        // integrates positions j .. j+3; true when the stream is over
+        auto consumeL = [&](int j, RawL& g) -> bool {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (bend <= j + i && close_to(j + i)) return true;
+                const unsigned s = g.s[i];
+                const int ai = (int)(s >> 20);
+                const float al = ai == 64 ? al_64s : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al_lane), ai));
+                const float w[4] = {__uint_as_float(g.x[i].x), __uint_as_float(g.x[i].y), __uint_as_float(g.x[i].z),
+                                    __uint_as_float(g.x[i].w)};
+                // the entry's image as a one-hot mask, tested bit by bit: a
+                // test on the image's index would let the compiler index the
+                // state arrays by it, which puts them in scratch memory
+#pragma unroll
+                for (int q = 0; q < NI; ++q) {
+                    if ((s >> (16 + q)) & 1u) {  // uniform
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[q][v] = __builtin_fmaf(w[v], al, acc[q][v]);
+                    }
+                }
+            }
+            return false;
+        };
+        RawL g0, g1;
+        int P0 = 0;
+        for (;;) {
+            place(P0);
+            if (lane < T) v_end = incl - P0;
+            bend = __builtin_amdgcn_readlane(v_end, b);
+            const int jlim = total - P0 > cap ? cap : INT_MAX;
+            bool over = false;
+            loadL(0, g0);
+            for (int j = 0;; j += 8) {
+                if (j >= jlim) break;
+                loadL(j + 4, g1);
+                __builtin_amdgcn_sched_barrier(0);
+                if (consumeL(j, g0)) {
+                    over = true;
+                    break;
+                }
+                if (j + 4 >= jlim) break;
+                loadL(j + 8, g0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (consumeL(j + 4, g1)) {
+                    over = true;
+                    break;
+                }
+            }
+            if (over || jlim == INT_MAX) break;  // uniform
+            P0 += cap;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < NI; ++p) {
+        if (p < n_live && ok) {
+            const int64_t pix = (int64_t)(img0 + p) * n_pos + pos;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) out[pix * a.C_out + co + v] = fb[p][v] == kNoSpike ? kInfTime : (float)fb[p][v];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // k_stream_window: k_merge and k_stream in one kernel for the bins path (the
 // layers whose columns were bucketized: conv with C_in > 64, FC), T <= 64.
 // Whole merged lists in LDS would cost occupancy (a 3x3 pixel of 512 inputs
@@ -2847,6 +3292,30 @@ int shared_cap(int64_t nel_max, int waves, bool alphas, int gather) {
 // The shared-list kernel: one workgroup per (output pixel, group of up to
 // four c_out blocks), the W waves building the pixel's list together and
 // each streaming one c_out block (64 c_out at epi 1, 128 at epi 2).
+// k_stream_multi's later-list capacity: four images' receptive elements
+// (every event of the field past bin 0), at most kMultiCapMax entries
+// (about 12 KB of LDS per wave with the ring and tables: 13 waves per CU).
+constexpr int kMultiCapMax = 2048;
+int multi_cap(int64_t nel_max) {
+    const int64_t want = (kMultiImages * nel_max + 3) & ~INT64_C(3);
+    return (int)(want < kMultiCapMax ? want : kMultiCapMax);
+}
+
+int launch_stream_multi(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
+                        const float* theta, int64_t nel_max, const IntegShape& sh) {
+    const int n_pos = sh.H_out * sh.W_out;
+    const int64_t n_prob = (int64_t)((sh.B + kMultiImages - 1) / kMultiImages) * n_pos;
+    const int64_t blocks = n_prob * a.n_cblk;
+    if (blocks <= 0) return VDTTFS_OK;
+    if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
+    const int cap = multi_cap(nel_max);
+    const size_t lds = (size_t)multi_wave_words(cap) * sizeof(int);
+    hipLaunchKernelGGL(k_stream_multi, dim3((unsigned)blocks), dim3(64), lds, ctx->stream, m, a, out, theta, cap,
+                       n_pos, sh.B);
+    VD_HIP(hipGetLastError());
+    return VDTTFS_OK;
+}
+
 int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
                          const float* theta, int64_t nel_max, int gather, bool culif) {
     const int waves = shared_waves(a.n_cblk, gather);
@@ -2965,8 +3434,11 @@ bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     const int taps = sh.is_fc ? 1 : sh.K_h * sh.K_w;
     const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
     const int64_t nel_max = shared_nel_max(sh);
+    // weight rows tap * C_in + cin go in 16 bits (the tap of the full kernel:
+    // a 3x3 conv on a 1x1 map still reads rows 4 C_in ...)
+    const int64_t rows = (int64_t)taps * sh.C_in;
     if (ctx->c.T > kBlockBins || taps > 9 || narrow_path_ok(sh, &wbytes) || !wave_path_ok(sh, &wbytes) ||
-        in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF)
+        in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF || rows > 0x10000)
         return false;
     // gather 4 (256 c_out per wave) for layers wider than 128 only
     if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0) && !(gather == 4 && sh.C_out % 4 == 0 && sh.C_out > 128))
@@ -2993,6 +3465,14 @@ int shared_gather(const IntegShape& sh) {
 int fused_kind(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     if ((integrate_dense_ok(ctx, sh) || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, gather)) return 1;
     return shared_ok(ctx, sh, gather) ? 2 : 0;
+}
+
+// Layers k_stream_multi takes (the shared-list kernel's four-c_out layers:
+// C_out > 128, C_out % 4 == 0; the LUT neuron only): plan FUSED, gather 4,
+// four pixels per wave -- the same position of four images.
+bool multi_ok(const vdttfs_ctx* ctx, const IntegShape& sh, bool culif) {
+    if (culif || fused_kind(ctx, sh, 4) != 2) return false;
+    return (size_t)multi_wave_words(multi_cap(shared_nel_max(sh))) * sizeof(int) <= kFusedMaxLds;
 }
 
 bool plan_from_dense(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, bool counters) {
@@ -3244,9 +3724,17 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         return plan_error(sh, "window path needs T <= 64 and at most 9 taps (or an FC layer)");
     p.path = req.path ? req.path : (fused ? VDTTFS_PATH_FUSED : (dense ? VDTTFS_PATH_DENSE : VDTTFS_PATH_BINS));
     if (p.path == VDTTFS_PATH_FUSED && kind == 2) {
-        // the shared-list kernel: one output pixel per workgroup
-        if (req.ppw > 1) return plan_error(sh, "the shared-list fused kernel takes one pixel per workgroup");
-        p.ppw = 1;
+        // the shared-list kernel: one output pixel per workgroup; or, with
+        // gather 4 and four pixels per wave, k_stream_multi (one position of
+        // four images per wave)
+        if (req.ppw == kMultiImages && p.gather == 4 && multi_ok(ctx, sh, false)) {
+            p.ppw = kMultiImages;
+        } else {
+            if (req.ppw > 1)
+                return plan_error(sh, "the shared-list fused kernel takes one pixel per workgroup, or four "
+                                      "(the same position of four images) with gather 4");
+            p.ppw = 1;
+        }
     } else if (req.ppw) {
         p.ppw = req.ppw;
     } else {
@@ -3418,6 +3906,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     const int nel_max = nk_max * sh.C_in;
     const size_t lds = (size_t)kMergeWaves * fused_wave_words(nel_max, m.T) * sizeof(int);
     if (p.path == VDTTFS_PATH_FUSED && lds_list) {
+        if (shared && p.ppw == kMultiImages && !culif)
+            return launch_stream_multi(ctx, m, a, out, theta, shared_nel_max(sh), sh);
         if (shared)
             return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), p.gather, culif != nullptr);
         // build the list in LDS and stream it there
