@@ -2635,8 +2635,17 @@ __device__ __forceinline__ uint64_t wave_or64(uint64_t m) {
 }
 
 // UNI: one pixel per wave (C_out > 32), so the spike times, bins and decay
-// values are wave-uniform (scalar) and only the weights are per lane.
-template <bool UNI>
+// values are wave-uniform (scalar) and only the weights are per lane.  NEL:
+// the elements the bin scan covers -- the layer's receptive field where an
+// instantiation has it, else the 32-element limit (its extra elements hold
+// bin -1).  Measured on LeNet-5's conv1 at B=1024 (25 elements, ten pixels
+// per wave; A/B on one box): 0.350 -> 0.300 ms with the scan cut to 25.
+// Tried and slower there: the fma under an exec mask (compare, save-exec,
+// fmac, restore: 0.331 ms -- the scalar unit then issues as much as the
+// vector unit saved); a wave-uniform branch skipping elements no lane holds
+// in the bin (0.318); bin sums in LDS, each element added once (0.502: 25
+// dependent LDS round trips per wave at ten waves per CU).
+template <bool UNI, int NEL>
 __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x >> 6);
@@ -2702,7 +2711,7 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
         float acc = 0.0f;
         if ((any >> t) & 1) {  // uniform; elements past nel hold bin -1
 #pragma unroll
-            for (int e = 0; e < kSmallMaxEl; ++e) acc = bin[e] == t ? __builtin_fmaf(wv[e], av[e], acc) : acc;
+            for (int e = 0; e < NEL; ++e) acc = bin[e] == t ? __builtin_fmaf(wv[e], av[e], acc) : acc;
         }
         carry = carry + acc;
         const float th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_th), t));
@@ -3557,10 +3566,22 @@ int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float*
     const int64_t blocks = (waves + 3) / 4;
     if (blocks <= 0) return VDTTFS_OK;
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "conv_small: grid too large");
-    if (a.P == 1)
-        hipLaunchKernelGGL(k_conv_small<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
-    else
-        hipLaunchKernelGGL(k_conv_small<false>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+    // the bin scan covers exactly the receptive field of LeNet-5's conv1 (25)
+    // and VGG-16's conv 0 (27), the 32-element limit otherwise
+#define VD_LAUNCH_SMALL(U, N) \
+    hipLaunchKernelGGL((k_conv_small<U, N>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a)
+    if (a.P == 1) {
+        if (a.nel == 27)
+            VD_LAUNCH_SMALL(true, 27);
+        else
+            VD_LAUNCH_SMALL(true, kSmallMaxEl);
+    } else {
+        if (a.nel == 25)
+            VD_LAUNCH_SMALL(false, 25);
+        else
+            VD_LAUNCH_SMALL(false, kSmallMaxEl);
+    }
+#undef VD_LAUNCH_SMALL
     VD_HIP(hipGetLastError());
     return VDTTFS_OK;
 }
