@@ -1215,7 +1215,8 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int tb = (int)floorf(fmaxf(t - a.tfs, 0.0f));  // t < kInfTime keeps it in range
             const bool ev = c * 64 + lane < nel && t < kInfTime && tb < a.T;
             int ai = tb;
-            if (a.alpha_by_time) ai = (int)fminf(fmaxf(t, 0.0f), (float)a.T);
+            // clamp(t, 0, T) in one med3 (NaN or t >= kInfTime: no event)
+            if (a.alpha_by_time) ai = (int)__builtin_amdgcn_fmed3f(t, 0.0f, (float)a.T);
             pk[c] = ev ? (rw[c] << 21) | (ai << 7) | tb : 0x7F;
             __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: fewer live registers
         }
