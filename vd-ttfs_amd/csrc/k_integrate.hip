@@ -399,14 +399,17 @@ struct StreamArgs {
 // XCD x only ever integrates c_out blocks x, x+8, ...: its L2 then holds
 // 1/8 of the layer's weights (the 3x3x512x512 planes are 9.4 MB, an XCD's L2
 // is 4 MB).  With 1, 2 or 4 blocks, b % n_cblk already pins XCD x to block
-// x % n_cblk.
+// x % n_cblk.  Past 8 blocks, XCD x takes its blocks x, x + 8, ... one
+// after the other, each over every pixel group (the grid is n_pg pixel
+// groups x n_cblk blocks, dealt in order), so its L2 holds one block's
+// weights at a time.
 __device__ __forceinline__ void map_block(int n_cblk, int& cb, int64_t& pg) {
     const int64_t b = blockIdx.x;
     if ((n_cblk & 7) == 0) {
-        const int per = n_cblk >> 3;
+        const int64_t n_pg = (int64_t)gridDim.x / n_cblk;
         const int64_t q = b >> 3;
-        cb = (int)(b & 7) + 8 * (int)(q % per);
-        pg = q / per;
+        cb = (int)(b & 7) + 8 * (int)(q / n_pg);
+        pg = q % n_pg;
     } else {
         cb = (int)(b % n_cblk);
         pg = b / n_cblk;
