@@ -71,6 +71,36 @@ __global__ void k_pool_min(const float* __restrict__ in, float* __restrict__ out
     }
 }
 
+// k_pool_min with four channels per thread (C % 4 == 0, 16-byte aligned
+// maps, fewer than 2^31 outputs): 16-byte loads and stores, and 32-bit
+// divisions by invariant divisors in place of 64-bit ones.  Every window
+// lies inside the map (h < H_in / 2, w < W_in / 2), and each channel keeps
+// the reference's order and compare: m = t where t < m, from kInfTime, over
+// (0,0), (0,1), (1,0), (1,1).
+__global__ void k_pool_min4(const float4* __restrict__ in, float4* __restrict__ out, int n4, int H_in, int W_in,
+                            int C4, FastDiv div_c4, FastDiv div_w_out, FastDiv div_h_out) {
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < n4; idx += gridDim.x * blockDim.x) {
+        const int pix = fdiv(idx, div_c4);
+        const int c4 = idx - pix * C4;
+        const int q = fdiv(pix, div_w_out);
+        const int w = pix - q * div_w_out.d;
+        const int img = fdiv(q, div_h_out);
+        const int h = q - img * div_h_out.d;
+        const int64_t row = (int64_t)W_in * C4;
+        const int64_t o = (((int64_t)img * H_in + 2 * h) * W_in + 2 * w) * C4 + c4;
+        const float4 t[4] = {in[o], in[o + C4], in[o + row], in[o + row + C4]};
+        float4 m = make_float4(kInfTime, kInfTime, kInfTime, kInfTime);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (t[k].x < m.x) m.x = t[k].x;
+            if (t[k].y < m.y) m.y = t[k].y;
+            if (t[k].z < m.z) m.z = t[k].z;
+            if (t[k].w < m.w) m.w = t[k].w;
+        }
+        out[idx] = m;
+    }
+}
+
 // T2V:172-190 with one wave per image, four images per block.  Each wave
 // first turns its image's spike times into alpha factors in LDS (one validity
 // bit per input); the block stages the weights of a 64-wide output block in
@@ -273,6 +303,14 @@ int launch_encode_linear(vdttfs_ctx* ctx, const float* img, float* out, int64_t 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C) {
     const int64_t n = (int64_t)B * (H_in / 2) * (W_in / 2) * C;
     if (n <= 0) return VDTTFS_OK;
+    if (C % 4 == 0 && n < (INT64_C(1) << 31) && (((uintptr_t)in | (uintptr_t)out) & 15) == 0) {
+        const int n4 = (int)(n / 4);
+        hipLaunchKernelGGL(k_pool_min4, dim3(grid_for(n4)), dim3(kThreads), 0, ctx->stream,
+                           reinterpret_cast<const float4*>(in), reinterpret_cast<float4*>(out), n4, H_in, W_in,
+                           C / 4, make_fastdiv(C / 4), make_fastdiv(W_in / 2), make_fastdiv(H_in / 2));
+        VD_HIP(hipGetLastError());
+        return VDTTFS_OK;
+    }
     hipLaunchKernelGGL(k_pool_min, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, in, out, B,
                        H_in, W_in, C);
     VD_HIP(hipGetLastError());
