@@ -22,7 +22,7 @@ The other synthetic workloads print one line each in the same format
   python bench.py --workload vgg16-timedriven | lenet5-timedriven | culif7-timedriven
                                         # the reference's step-by-step GPU baseline (T2S / T1S / T3S)
 
-Three rooflines are reported for the integrator (a layer's list build +
+Four byte counts are reported for the integrator (a layer's list build +
 stream, the dominant kernel family):
 
 * roofline.achieved / frac / traffic -- HBM: the FETCH_SIZE + WRITE_SIZE
@@ -35,6 +35,11 @@ stream, the dominant kernel family):
 * roofline.algorithmic_hbm_* -- the bytes the algorithm must move through
   HBM in one fused pass per layer (input map, weights, bias, output map)
   over the same time.
+* roofline.b_int -- the reference-layout byte model per layer: 4 B per
+  integrated synapse under the chunk exit (E_proc), 8 B per retained event
+  and 4 B per chunk offset (the lists read once), bias and first-spike
+  writes, over the same time.  Most of it is weight gathers served from L2,
+  so it exceeds the HBM peak.
 * roofline.gathered -- the weight bytes the stream kernels gather per
   integrated synapse (4 B per event under the per-bin exit the kernels run,
   E_bin) over the same time, against the gather roof that
@@ -290,6 +295,15 @@ def dropin_scope(w, img, gpu_pred, B: int, reps: int = 4):
                      "host argmax (T2V:337-402 call for call); median of the runs after the first"}
 
 
+def b_int_bytes(l, B, eproc, n_ev, n_cols, os_):
+    """The reference-layout byte model of one layer's integrate: one fp32
+    weight per integrated synapse under the chunk-granular exit (E_proc,
+    T2V:133,151), the event lists (int32 cin + fp32 t) and the per-column
+    chunk offsets read once, the bias, and the first-spike write."""
+    n_out = B * l.C_out * (1 if l.kind == 1 else l.H_out * l.W_out)
+    return 4 * eproc + 8 * n_ev + 4 * os_ * n_cols + 4 * l.C_out + 4 * n_out
+
+
 def work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr):
     """Per integrating layer: time, E_proc / E_bin / E_noEE, skip rate, spike
     densities, launch plan and the three roof positions."""
@@ -330,7 +344,9 @@ def work_table(ctx, net, w, B, d_img, counts, layer_ms, roofs, tr):
                    "gathered_GBps": gb / (ms * 1e-3) / 1e9,
                    "gather_roof_GBps": roof["GBps"],
                    "gather_frac": gb / (ms * 1e-3) / 1e9 / roof["GBps"],
-                   "algorithmic_hbm_bytes": hbm_compulsory_bytes(l, B)}
+                   "algorithmic_hbm_bytes": hbm_compulsory_bytes(l, B),
+                   "b_int_bytes": b_int_bytes(l, B, int(eproc[i]), int(n_ev[i]), int(n_cols[i]),
+                                              w.consts.num_chunks + 1)}
             if tr and li < len(tr["layers"]):
                 hb = tr["layers"][li][0] + tr["layers"][li][1]
                 row["hbm_bytes"] = hb
@@ -490,6 +506,7 @@ def bench_ttfs(args) -> int:
     ms_step = elapsed * 1000.0 / args.steps
     integ_s = integ_ms_step * 1e-3
     alg = sum(r["algorithmic_hbm_bytes"] for r in rows)
+    b_int = sum(r["b_int_bytes"] for r in rows)
     gathered = sum(4.0 * r["ebin"] for r in rows)
     # time the layers would take at their gather roof, over the time they took
     t_roof = sum(4.0 * r["ebin"] / (r["gather_roof_GBps"] * 1e9) for r in rows)
@@ -544,6 +561,16 @@ def bench_ttfs(args) -> int:
             "algorithmic_hbm_GBps": alg / integ_s / 1e9,
             "algorithmic_hbm_frac": alg / integ_s / 1e9 / HBM_PEAK_GBS,
             "algorithmic_hbm_model": "per layer 4 B x (input map + weights + bias + output map): one fused pass",
+            "b_int": {
+                "bytes_per_step": b_int,
+                "bytes_per_launch": b_int / max(launches_per_step, 1),
+                "achieved_GBps": b_int / integ_s / 1e9,
+                "frac_of_hbm_peak": b_int / integ_s / 1e9 / HBM_PEAK_GBS,
+                "model": "per layer 4 E_proc + 8 N_ev + 4 OS N_cols + 4 C_out + 4 N_out bytes: the weight gathered "
+                         "per integrated synapse under the chunk exit (T2V:133,151), event lists and chunk "
+                         "offsets read once, bias, first-spike writes; above 1 where the weights are gathered from "
+                         "L2, not HBM",
+            },
             "gathered": {
                 "bytes_per_step": gathered,
                 "achieved_GBps": gathered / integ_s / 1e9,

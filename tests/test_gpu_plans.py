@@ -72,7 +72,7 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
     try:
         assert net.get_plan(0) == (REG, 1, 10)     # C_out 6: 10 pixels per wave
         assert net.get_plan(2) == (DENSE, 1, 4)    # 150 receptive elements: a list
-        assert net.get_plan(6) == (BINS, 1, 6)     # FC 84 -> 10
+        assert net.get_plan(6) == (FUSED, 1, 1)    # FC 84 -> 10: the shared-list kernel, one wave per image
         assert net.get_plan(4) == (FUSED, 2, 1)    # FC 256 -> 120: the shared-list kernel
         with pytest.raises(vdttfs.VdttfsError):
             net.set_plan(0, 0, 0, 2)
@@ -150,7 +150,7 @@ def test_every_plan_matches_oracle_lenet(gpu_ctx_factory):
     img = models.images_for(w, B)
     ref = oracle_ref(w, B, img)
     n = sweep_all_plans(gpu_ctx_factory(w.consts), w, B, img, ref, check_counts=True)
-    assert n[0] == 3 and n[6] == 1
+    assert n[0] == 3 and n[6] == 2  # FC 84 -> 10: the narrow bins path and the shared-list kernel
 
 
 def test_tuner_lenet(gpu_ctx_factory):

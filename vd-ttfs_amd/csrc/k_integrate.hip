@@ -3450,8 +3450,11 @@ bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
     // weight rows tap * C_in + cin go in 16 bits (the tap of the full kernel:
     // a 3x3 conv on a 1x1 map still reads rows 4 C_in ...)
     const int64_t rows = (int64_t)taps * sh.C_in;
-    if (ctx->c.T > kBlockBins || taps > 9 || narrow_path_ok(sh, &wbytes) || !wave_path_ok(sh, &wbytes) ||
-        in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF || rows > 0x10000)
+    // FC layers narrower than 32 outputs too (one 64-wide wave per image,
+    // gather 1): LeNet-5's 84 -> 10
+    const bool narrow_fc = sh.is_fc && narrow_path_ok(sh, &wbytes);
+    if (ctx->c.T > kBlockBins || taps > 9 || !(wave_path_ok(sh, &wbytes) || narrow_fc) ||
+        in_bytes >= (INT64_C(1) << 31) || nel_max > 0xFFFF || rows > 0x10000 || (narrow_fc && gather != 1))
         return false;
     // gather 4 (256 c_out per wave) for layers wider than 128 only
     if (gather != 1 && !(gather == 2 && sh.C_out % 4 == 0) && !(gather == 4 && sh.C_out % 4 == 0 && sh.C_out > 128))
@@ -3693,6 +3696,18 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         *out = p;
         return VDTTFS_OK;
     }
+    // FC layers narrower than 32 outputs: the shared-list kernel (one wave
+    // per image, the list built in LDS) where it takes them, in place of
+    // bucketize + k_merge + k_stream_narrow (LeNet-5's 84 -> 10 at B=1024:
+    // three launches of a few microseconds of work each)
+    if (narrow && sh.is_fc && shared_ok(ctx, sh, 1) && (req.path == 0 || req.path == VDTTFS_PATH_FUSED) &&
+        req.gather <= 1 && req.ppw <= 1) {
+        p.path = VDTTFS_PATH_FUSED;
+        p.gather = 1;
+        p.ppw = 1;
+        *out = p;
+        return VDTTFS_OK;
+    }
     if (narrow) {  // one pixel per C_out lanes
         const int P = 64 / sh.C_out;
         if (req.path == VDTTFS_PATH_FUSED || req.path == VDTTFS_PATH_WINDOW || (req.gather && req.gather != 1) ||
@@ -3914,7 +3929,7 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.in_bytes = in_bytes < (INT64_C(1) << 31) ? (int)in_bytes : 0;
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
-    if (narrow) {
+    if (narrow && !shared) {
         if (nk_max <= 9)
             hipLaunchKernelGGL(k_merge_dense<9>, dim3((unsigned)mblocks), dim3(64 * kMergeWaves), 0, ctx->stream,
                                m);
