@@ -308,8 +308,10 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
  *           per wave (C_out a multiple of 4); 4 four c_out per lane, 256
  *           c_out per wave (C_out a multiple of 4)
  *   ppw:    output pixels per wave, 1..8
- * Layers with C_out < 32 run one pixel per C_out lanes (gather 1, ppw =
- * 64 / C_out, paths BINS or DENSE); layers outside the merged-list limits
+ * Conv layers with C_out < 32 run one pixel per C_out lanes (gather 1, ppw =
+ * 64 / C_out, paths BINS or DENSE); FC layers with C_out < 32 run that way
+ * (BINS) or, built in where it takes them (T <= 64), on the shared-list
+ * kernel (FUSED, gather 1, ppw 1); layers outside the merged-list limits
  * (> 25 taps) take the generic integrator (path BINS, gather and ppw 0).
  * Pool and vmem layers have no plan.  set_plan(NULL) restores the built-in
  * choice; an unsupported request fails with VDTTFS_E_UNSUPPORTED and leaves
