@@ -331,6 +331,32 @@ def test_pool_vmem_readout_encode(gpu_ctx_factory):
     assert diff.size <= 2, diff
 
 
+def test_pool_min_vector_and_unaligned(gpu_ctx_factory):
+    """Channel counts that are multiples of four take the 16-byte kernel (odd
+    map sides drop the last row/column as the reference does); a map that
+    starts 4 bytes past an aligned address takes the scalar kernel.  Both
+    equal the oracle bit for bit."""
+    import ctypes
+    import types
+    say("pool_min float4 / unaligned")
+    rng = np.random.default_rng(81)
+    tc = consts(64, 32.0, 8, True)
+    ctx = gpu_ctx_factory(tc)
+    for B, H, W, Cc in ((3, 9, 7, 8), (2, 4, 4, 12), (1, 2, 2, 4), (4, 14, 14, 64)):
+        x = np.where(rng.random(B * H * W * Cc) < 0.5, rng.integers(0, 64, B * H * W * Cc), 9999)
+        x = x.astype(np.float32)
+        exp = oracle.pool_min(x, B, H, W, Cc)
+        d_o = ctx.empty(exp.size)
+        ctx.pool_min(ctx.to_device(x), d_o, B, H, W, Cc)
+        np.testing.assert_array_equal(d_o.download(), exp)
+        # the same map one float past an aligned address, in and out
+        d_in = ctx.to_device(np.concatenate([np.zeros(1, np.float32), x]))
+        d_out = ctx.empty(exp.size + 1)
+        shift = lambda d: types.SimpleNamespace(ptr=ctypes.c_void_p(d.ptr.value + 4))  # noqa: E731
+        ctx.pool_min(shift(d_in), shift(d_out), B, H, W, Cc)
+        np.testing.assert_array_equal(d_out.download()[1:], exp)
+
+
 def test_integrate_dropin_skips_foreign_events(gpu_ctx_factory):
     """The drop-in integrator over caller buckets guards what the reference
     leaves undefined (T2V:127-131 indexes delta[tb - base_t] and the weight

@@ -2604,12 +2604,11 @@ __global__ __launch_bounds__(256) void k_stream_window(MergeArgs m, StreamArgs a
 // T <= 64.  No list is built: a wave packs P = 64 / C_out pixels, lane =
 // (pixel p, c_out c), and each lane loads its pixel's receptive elements
 // straight from the spike map into registers -- arrival bin, weight and
-// decay value per element.  The wave then walks the bins in order: for a
-// bin that any lane's pixel occupies (a 64-bit mask OR-reduced over the
-// wave), each lane sums its elements of that bin in element order -- (kh,
-// kw, cin), the reference's order -- as fma(w, alpha, acc); every bin closes
-// with carry += acc and the threshold test, as in k_stream.  The wave leaves
-// when none of its neurons is alive.
+// decay value per element.  A bin's sum is the lane's elements of that bin
+// in element order -- (kh, kw, cin), the reference's order -- as fma(w,
+// alpha, acc), and closing it is carry += acc and the threshold test, as in
+// k_stream.  One pixel per wave (UNI) walks the bins in lockstep; several
+// pixels per wave walk each lane's own occupied bins (below).
 struct SmallArgs {
     const float* in;      // [n_cols][C_in] spike times (NHWC map)
     const float* alpha;   // decay LUT, T + 1 entries
@@ -2623,6 +2622,8 @@ struct SmallArgs {
     int H_in, W_in, C_in, H_out, W_out, C_out, K_h, K_w, pad_h, pad_w;
     int nel;              // K_h * K_w * C_in
     int P;                // pixels per wave: 64 / C_out
+    int in_bytes;         // bytes of `in`, below 2^31
+    FastDiv div_cout, div_w, div_h;  // C_out, W_out, H_out
 };
 constexpr int kSmallMaxEl = 32;
 constexpr int kSmallMaxBins = 64;
@@ -2638,79 +2639,190 @@ __device__ __forceinline__ uint64_t wave_or64(uint64_t m) {
            (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
 }
 
+// Threshold tests for a lane that walks its own occupied bins (bins hold
+// no event of the lane between two it visits).  Across such a run carry is
+// constant, as an empty bin adds nothing.  With theta non-increasing over
+// the window (checked once per wave; NaN fails) "carry >= theta[t]" holds
+// on a suffix of the run and "theta[t] >= 1e-5" on a prefix of the window
+// (bins below th_end), so the run fires iff carry clears theta at its last
+// bin that may fire, and then at the first bin where it does -- a binary
+// search per lane; otherwise the run is scanned bin by bin.  th points at
+// the thresholds in LDS.  Built with every lane of the wave active.
+struct RunFire {
+    const float* th;
+    int t_min, th_end;
+    bool mono;
+    __device__ RunFire(const float* th_, float v_th, int T, int t_min_) : th(th_), t_min(t_min_) {
+        const int lane = lane_id();
+        const float nxt = __shfl_down(v_th, 1, 64);
+        mono = __ballot(lane + 1 < T && !(v_th >= nxt)) == 0;
+        const uint64_t low = __ballot(lane < T && !(v_th >= 1e-5f));
+        th_end = low ? (int)__builtin_ctzll(low) : T;
+    }
+    // theta at the last bin of [0, r1) that may fire, read ahead by the caller
+    __device__ float last(int r1) const {
+        const int tb = r1 < th_end ? r1 : th_end;
+        return th[tb > 0 ? tb - 1 : 0];
+    }
+    // fire in the bins [r0, r1) (no event of the lane there) if carry
+    // reaches a threshold; th_b = last(r1)
+    __device__ void run(int r0, int r1, float th_b, float carry, float& res, bool& alive) const {
+        const int ta = r0 > t_min ? r0 : t_min;
+        if (mono) {
+            const int tb = r1 < th_end ? r1 : th_end;
+            if (ta < tb && carry >= th_b) {
+                int lo = ta, hi = tb - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    const bool le = th[mid] <= carry;
+                    hi = le ? mid : hi;
+                    lo = le ? lo : mid + 1;
+                }
+                res = (float)lo;
+                alive = false;
+            }
+        } else {
+            for (int t = ta; t < r1; ++t) {
+                const float v = th[t];
+                if (v >= 1e-5f && carry >= v) {
+                    res = (float)t;
+                    alive = false;
+                    break;
+                }
+            }
+        }
+    }
+    // close an occupied bin t: carry += the bin's sum, then the test
+    __device__ void bin(int t, float acc, float th_t, float& carry, float& res, bool& alive) const {
+        carry = carry + acc;
+        if (t >= t_min && th_t >= 1e-5f && carry >= th_t) {
+            res = (float)t;
+            alive = false;
+        }
+    }
+};
+
 // UNI: one pixel per wave (C_out > 32), so the spike times, bins and decay
 // values are wave-uniform (scalar) and only the weights are per lane.  NEL:
 // the elements the bin scan covers -- the layer's receptive field where an
 // instantiation has it, else the 32-element limit (its extra elements hold
 // bin -1).  Measured on LeNet-5's conv1 at B=1024 (25 elements, ten pixels
-// per wave; A/B on one box): 0.350 -> 0.300 ms with the scan cut to 25.
-// Tried and slower there: the fma under an exec mask (compare, save-exec,
-// fmac, restore: 0.331 ms -- the scalar unit then issues as much as the
-// vector unit saved); a wave-uniform branch skipping elements no lane holds
-// in the bin (0.318); bin sums in LDS, each element added once (0.502: 25
-// dependent LDS round trips per wave at ten waves per CU).
+// per wave; A/B on one box): 0.350 -> 0.300 ms with the scan cut to 25;
+// 0.300 -> 0.211 ms with each lane walking its own occupied bins (about 5
+// of a pixel's 25 elements hold a spike, spread over the 64 bins, while
+// the ten pixels of a wave occupy about 35 bins between them); 0.211 ->
+// 0.192 ms with every spike-time and weight load issued before any is used
+// (32-bit offsets from a per-lane base: 64-bit index arithmetic had made
+// each load wait for the previous one); 0.192 -> 0.187 ms with the bin's
+// thresholds read before its sum.  Tried and slower there: the fma under
+// an exec mask (compare, save-exec, fmac, restore: 0.331 ms -- the scalar
+// unit then issues as much as the vector unit saved); a wave-uniform branch
+// skipping elements no lane holds in the bin (0.318); bin sums in LDS, each
+// element added once (0.502: 25 dependent LDS round trips per wave at ten
+// waves per CU).
 template <bool UNI, int NEL>
 __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
+    // the thresholds, for per-lane bins (several pixels per wave)
+    __shared__ float th_lds[UNI ? 1 : kSmallMaxBins];
+    if constexpr (!UNI) {
+        if ((int)threadIdx.x < a.T) th_lds[threadIdx.x] = a.theta[threadIdx.x];
+        __syncthreads();
+    }
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x >> 6);
     const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * a.P;
     if (pix0 >= a.n_pix) return;  // uniform per wave
-    const int p = UNI ? 0 : lane / a.C_out, c = lane - p * a.C_out;
+    const int p = UNI ? 0 : fdiv(lane, a.div_cout), c = lane - p * a.C_out;
     const int64_t pix = pix0 + p;
     const bool ok = p < a.P && pix < a.n_pix && c < a.C_out;
     const bool pix_ok = UNI ? true : ok;  // the lane's pixel exists (UNI: pix0 < n_pix)
-    const int64_t px = UNI ? pix0 : (ok ? pix : pix0);
-    const int w_out = (int)(px % a.W_out);
-    const int64_t q = px / a.W_out;
-    const int h_out = (int)(q % a.H_out);
-    const int64_t img = q / a.H_out;
+    // 32-bit pixel coordinates and offsets: the launch keeps the pixel count
+    // and the map's bytes below 2^31
+    const int px = (int)(UNI ? pix0 : (ok ? pix : pix0));
+    const int qd = fdiv(px, a.div_w);
+    const int w_out = px - qd * a.W_out;
+    const int img = fdiv(qd, a.div_h);
+    const int h_out = qd - img * a.H_out;
     // the lane's receptive elements: bin (-1: none), weight, decay value.
-    // Every load is issued unconditionally at an in-range address (masked
-    // afterwards), so a lane waits for two rounds of loads, not one per
-    // element: the spike times, then the weights and decay values.
-    int bin[kSmallMaxEl];
-    float wv[kSmallMaxEl], av[kSmallMaxEl];
+    // Every spike-time and weight load is issued before any is used (no
+    // branch between them; elements outside the map load its first word and
+    // are masked), so a lane waits for two rounds of loads, not one per
+    // element: the spike times and weights, then the decay values.
+    int bin[NEL];
+    float wv[NEL], av[NEL];
+    uint32_t inm = 0;  // bit e: element e lies inside the map
     {
-        int kh = 0, kw = 0, ci = 0;  // element e = (kh*K_w + kw)*C_in + ci, wave-uniform
+        const __amdgpu_buffer_rsrc_t rin =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+        const int cc = c < a.C_out ? c : 0;
+        // the field's first element (kh = kw = ci = 0, possibly outside the
+        // map); element e lies dk + ci further, dk = (kh * W_in + kw) * C_in
+        const int h0 = h_out - a.pad_h, w0 = w_out - a.pad_w;
+        const int base = ((img * a.H_in + h0) * a.W_in + w0) * a.C_in;
+        int kh = 0, kw = 0, ci = 0, dk = 0;  // element e = (kh*K_w + kw)*C_in + ci, wave-uniform
 #pragma unroll
-        for (int e = 0; e < kSmallMaxEl; ++e) {
-            av[e] = kInfTime;  // spike time until the second round
-            if (e < a.nel) {   // uniform
-                const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
-                const bool inb = pix_ok && hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
-                const int64_t idx = inb ? ((img * a.H_in + hi) * a.W_in + wi) * a.C_in + ci : 0;
-                const float t = a.in[idx];
-                av[e] = inb ? t : kInfTime;
-                if (++ci == a.C_in) {
-                    ci = 0;
-                    if (++kw == a.K_w) {
-                        kw = 0;
-                        ++kh;
-                    }
-                }
-            }
+        for (int e = 0; e < NEL; ++e) {
+            const bool inb = e < a.nel && pix_ok && (unsigned)(h0 + kh) < (unsigned)a.H_in &&
+                             (unsigned)(w0 + kw) < (unsigned)a.W_in;
+            const int off = inb ? (base + dk + ci) * 4 : 0;
+            av[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, 0, 0));
+            wv[e] = a.W[(e < a.nel ? e : 0) * a.C_out + cc];
+            inm |= (inb ? 1u : 0u) << e;
+            ci += 1;
+            const bool wrap_c = ci == a.C_in;
+            ci = wrap_c ? 0 : ci;
+            kw += wrap_c ? 1 : 0;
+            dk += wrap_c ? a.C_in : 0;
+            const bool wrap_w = kw == a.K_w;
+            kw = wrap_w ? 0 : kw;
+            kh += wrap_w ? 1 : 0;
+            dk += wrap_w ? (a.W_in - a.K_w) * a.C_in : 0;
         }
     }
     uint64_t occ = 0;
 #pragma unroll
-    for (int e = 0; e < kSmallMaxEl; ++e) {
-        bin[e] = -1;
-        wv[e] = 0.0f;
-        if (e < a.nel) {  // uniform
-            const float t = av[e];
-            const int b = arrival_bin(t, a.tfs, a.T);
-            const int ai = b >= 0 ? alpha_index(t, b, a.alpha_by_time, a.T) : 0;
-            wv[e] = a.W[(int64_t)e * a.C_out + (c < a.C_out ? c : 0)];
-            av[e] = a.alpha[ai];
-            bin[e] = b;
-            occ |= b >= 0 ? (1ull << b) : 0ull;
-        }
+    for (int e = 0; e < NEL; ++e) {
+        const float t = (inm >> e) & 1u ? av[e] : kInfTime;
+        const int b = arrival_bin(t, a.tfs, a.T);
+        const int ai = b >= 0 ? alpha_index(t, b, a.alpha_by_time, a.T) : 0;
+        av[e] = a.alpha[ai];
+        bin[e] = b;
+        occ |= b >= 0 ? (1ull << b) : 0ull;
     }
-    const uint64_t any = wave_or64(occ);
     const float v_th = lane < a.T ? a.theta[lane] : 0.0f;
     float carry = ok ? a.bias[c] : 0.0f;
     float res = kInfTime;
     bool alive = ok;
+    if constexpr (!UNI) {
+        // Each lane walks only its own pixel's occupied bins, in order (the
+        // lowest set bit of its mask), and settles the empty bins between
+        // them with RunFire.  The wave takes as many steps as its busiest
+        // pixel has occupied bins, not one per bin that any of its pixels
+        // occupies.
+        const RunFire rf(th_lds, v_th, a.T, a.t_min);
+        uint64_t rem = occ;  // the lane's occupied bins not yet integrated
+        int t_done = 0;      // bins below are closed
+        while (__ballot(alive && rem != 0) != 0) {
+            if (alive && rem != 0) {
+                const int tn = (int)__builtin_ctzll(rem);
+                // both thresholds are read before the bin's sum, which hides
+                // the LDS latency; the sum is dropped if the lane fires in the
+                // empty bins before tn
+                const float th_n = th_lds[tn], th_b = rf.last(tn);
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < NEL; ++e) acc = bin[e] == tn ? __builtin_fmaf(wv[e], av[e], acc) : acc;
+                rf.run(t_done, tn, th_b, carry, res, alive);
+                if (alive) rf.bin(tn, acc, th_n, carry, res, alive);
+                rem &= rem - 1;
+                t_done = tn + 1;
+            }
+        }
+        if (alive) rf.run(t_done, a.T, rf.last(a.T), carry, res, alive);
+        if (ok) a.out[pix * a.C_out + c] = res;
+        return;
+    }
+    const uint64_t any = wave_or64(occ);
     for (int t = 0; t < a.T; ++t) {
         float acc = 0.0f;
         if ((any >> t) & 1) {  // uniform; elements past nel hold bin -1
@@ -3537,8 +3649,10 @@ bool window_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
 
 // k_conv_small's limits (the receptive field and the bins fit in registers)
 bool small_ok(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
     return !sh.is_fc && sh.K_h * sh.K_w * sh.C_in <= kSmallMaxEl && sh.C_out <= 64 &&
-           ctx->c.T <= kSmallMaxBins && integrate_dense_ok(ctx, sh);
+           ctx->c.T <= kSmallMaxBins && integrate_dense_ok(ctx, sh) && in_bytes < (INT64_C(1) << 31) &&
+           n_pixels(sh) < (INT64_C(1) << 31);
 }
 
 int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, const float* W,
@@ -3567,8 +3681,14 @@ int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float*
     a.pad_w = sh.pad_w;
     a.nel = sh.K_h * sh.K_w * sh.C_in;
     a.P = 64 / sh.C_out;
-    if (a.nel > kSmallMaxEl || sh.C_out > 64 || a.T > kSmallMaxBins)
+    const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
+    if (a.nel > kSmallMaxEl || sh.C_out > 64 || a.T > kSmallMaxBins || in_bytes >= (INT64_C(1) << 31) ||
+        a.n_pix >= (INT64_C(1) << 31))
         return set_error(VDTTFS_E_UNSUPPORTED, "conv_small: layer outside its limits");
+    a.in_bytes = (int)in_bytes;
+    a.div_cout = make_fastdiv(sh.C_out);
+    a.div_w = make_fastdiv(sh.W_out);
+    a.div_h = make_fastdiv(sh.H_out);
     const int64_t waves = (a.n_pix + a.P - 1) / a.P;
     const int64_t blocks = (waves + 3) / 4;
     if (blocks <= 0) return VDTTFS_OK;
