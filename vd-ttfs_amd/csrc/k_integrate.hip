@@ -2609,6 +2609,7 @@ __global__ __launch_bounds__(256) void k_stream_window(MergeArgs m, StreamArgs a
 // alpha, acc), and closing it is carry += acc and the threshold test, as in
 // k_stream.  One pixel per wave (UNI) walks the bins in lockstep; several
 // pixels per wave walk each lane's own occupied bins (below).
+constexpr int kSmallMaxEl = 32;
 struct SmallArgs {
     const float* in;      // [n_cols][C_in] spike times (NHWC map)
     const float* alpha;   // decay LUT, T + 1 entries
@@ -2623,9 +2624,12 @@ struct SmallArgs {
     int nel;              // K_h * K_w * C_in
     int P;                // pixels per wave: 64 / C_out
     int in_bytes;         // bytes of `in`, below 2^31
+    int w_bytes;          // bytes of W
     FastDiv div_cout, div_w, div_h;  // C_out, W_out, H_out
+    // element e's offset from its field's first element, (kh * W_in + kw) *
+    // C_in + ci (0 past nel): the k_conv_small<.., .., true> form
+    int dk[kSmallMaxEl];
 };
-constexpr int kSmallMaxEl = 32;
 constexpr int kSmallMaxBins = 64;
 
 __device__ __forceinline__ uint64_t wave_or64(uint64_t m) {
@@ -2714,13 +2718,17 @@ struct RunFire {
 // 0.192 ms with every spike-time and weight load issued before any is used
 // (32-bit offsets from a per-lane base: 64-bit index arithmetic had made
 // each load wait for the previous one); 0.192 -> 0.187 ms with the bin's
-// thresholds read before its sum.  Tried and slower there: the fma under
+// thresholds read before its sum; 0.187 -> 0.137 ms where every tap lies
+// inside the map (no padding): element offsets from a host table as the
+// loads' scalar offsets, no bounds tests, and the bins and decay indices
+// without branches (the preamble went from about 870 vector and 900 scalar
+// instructions per wave to 440 and 200).  Tried and slower there: the fma under
 // an exec mask (compare, save-exec, fmac, restore: 0.331 ms -- the scalar
 // unit then issues as much as the vector unit saved); a wave-uniform branch
 // skipping elements no lane holds in the bin (0.318); bin sums in LDS, each
 // element added once (0.502: 25 dependent LDS round trips per wave at ten
 // waves per CU).
-template <bool UNI, int NEL>
+template <bool UNI, int NEL, bool VALID>
 __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     // the thresholds, for per-lane bins (several pixels per wave)
     __shared__ float th_lds[UNI ? 1 : kSmallMaxBins];
@@ -2748,10 +2756,31 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     // branch between them; elements outside the map load its first word and
     // are masked), so a lane waits for two rounds of loads, not one per
     // element: the spike times and weights, then the decay values.
+    // an instantiation whose NEL is not the 32-element limit runs only for
+    // fields of exactly NEL elements
+    constexpr bool EXACT = NEL != kSmallMaxEl;
     int bin[NEL];
     float wv[NEL], av[NEL];
     uint32_t inm = 0;  // bit e: element e lies inside the map
-    {
+    if constexpr (VALID) {
+        // every tap of every output pixel lies inside the map (no padding):
+        // element e sits a.dk[e] past the field's first element, so a load's
+        // per-lane offset is the field's base and its scalar offset the
+        // table entry -- no per-element address or bounds arithmetic
+        const __amdgpu_buffer_rsrc_t rin =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rw =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.w_bytes, 0x00020000);
+        const int vb = (((img * a.H_in + h_out) * a.W_in + w_out) * a.C_in) * 4;
+        const int vc = (c < a.C_out ? c : 0) * 4;
+#pragma unroll
+        for (int e = 0; e < NEL; ++e) {
+            av[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, vb, a.dk[e] * 4, 0));
+            wv[e] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rw, vc, (EXACT || e < a.nel ? e : 0) * a.C_out * 4, 0));
+        }
+        (void)inm;
+    } else {
         const __amdgpu_buffer_rsrc_t rin =
             __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
         const int cc = c < a.C_out ? c : 0;
@@ -2780,14 +2809,35 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
         }
     }
     uint64_t occ = 0;
+    if constexpr (UNI) {
 #pragma unroll
-    for (int e = 0; e < NEL; ++e) {
-        const float t = (inm >> e) & 1u ? av[e] : kInfTime;
-        const int b = arrival_bin(t, a.tfs, a.T);
-        const int ai = b >= 0 ? alpha_index(t, b, a.alpha_by_time, a.T) : 0;
-        av[e] = a.alpha[ai];
-        bin[e] = b;
-        occ |= b >= 0 ? (1ull << b) : 0ull;
+        for (int e = 0; e < NEL; ++e) {
+            const float t = (inm >> e) & 1u ? av[e] : kInfTime;
+            const int b = arrival_bin(t, a.tfs, a.T);
+            const int ai = b >= 0 ? alpha_index(t, b, a.alpha_by_time, a.T) : 0;
+            av[e] = a.alpha[ai];
+            bin[e] = b;
+            occ |= b >= 0 ? (1ull << b) : 0ull;
+        }
+    } else {
+        // arrival_bin and alpha_index without branches, as quad_build: bin
+        // floor(max(t - tfs, 0)), an event if t < kInfTime and the bin is
+        // below T; LUT index the bin, or clamp(t, 0, T) by spike time (one
+        // med3).  The table form loads every lane's field (lanes past the
+        // last pixel load the wave's first), and only elements past nel are
+        // masked: a lane without a pixel is never alive.
+        const __amdgpu_buffer_rsrc_t ral =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.alpha, (short)0, (a.T + 1) * 4, 0x00020000);
+#pragma unroll
+        for (int e = 0; e < NEL; ++e) {
+            const float t = VALID ? av[e] : ((inm >> e) & 1u ? av[e] : kInfTime);
+            const int tb = (int)floorf(fmaxf(t - a.tfs, 0.0f));
+            const bool ev = (!VALID || EXACT || e < a.nel) && t < kInfTime && tb < a.T;
+            const int ai = a.alpha_by_time ? (int)__builtin_amdgcn_fmed3f(t, 0.0f, (float)a.T) : tb;
+            av[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ral, (ev ? ai : 0) * 4, 0, 0));
+            bin[e] = ev ? tb : -1;
+            occ |= ev ? (1ull << tb) : 0ull;
+        }
     }
     const float v_th = lane < a.T ? a.theta[lane] : 0.0f;
     float carry = ok ? a.bias[c] : 0.0f;
@@ -3695,18 +3745,32 @@ int launch_conv_small(vdttfs_ctx* ctx, float* out, const float* in, const float*
     if (blocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "conv_small: grid too large");
     // the bin scan covers exactly the receptive field of LeNet-5's conv1 (25)
     // and VGG-16's conv 0 (27), the 32-element limit otherwise
-#define VD_LAUNCH_SMALL(U, N) \
-    hipLaunchKernelGGL((k_conv_small<U, N>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a)
+    // every tap of every output pixel inside the map (no padding): the
+    // element offsets come from a table
+    const bool valid = sh.pad_h == 0 && sh.pad_w == 0 && sh.H_out <= sh.H_in - sh.K_h + 1 &&
+                       sh.W_out <= sh.W_in - sh.K_w + 1;
+    a.w_bytes = (int)((int64_t)a.nel * sh.C_out * 4);
+    for (int e = 0; e < kSmallMaxEl; ++e) a.dk[e] = 0;
+    for (int kh = 0, e = 0; kh < sh.K_h; ++kh)
+        for (int kw = 0; kw < sh.K_w; ++kw)
+            for (int ci = 0; ci < sh.C_in; ++ci, ++e) a.dk[e] = (kh * sh.W_in + kw) * sh.C_in + ci;
+#define VD_LAUNCH_SMALL(U, N, V) \
+    hipLaunchKernelGGL((k_conv_small<U, N, V>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a)
     if (a.P == 1) {
         if (a.nel == 27)
-            VD_LAUNCH_SMALL(true, 27);
+            VD_LAUNCH_SMALL(true, 27, false);
         else
-            VD_LAUNCH_SMALL(true, kSmallMaxEl);
+            VD_LAUNCH_SMALL(true, kSmallMaxEl, false);
+    } else if (valid) {
+        if (a.nel == 25)
+            VD_LAUNCH_SMALL(false, 25, true);
+        else
+            VD_LAUNCH_SMALL(false, kSmallMaxEl, true);
     } else {
         if (a.nel == 25)
-            VD_LAUNCH_SMALL(false, 25);
+            VD_LAUNCH_SMALL(false, 25, false);
         else
-            VD_LAUNCH_SMALL(false, kSmallMaxEl);
+            VD_LAUNCH_SMALL(false, kSmallMaxEl, false);
     }
 #undef VD_LAUNCH_SMALL
     VD_HIP(hipGetLastError());
