@@ -206,6 +206,8 @@ REG_CASES = [
     (48, 0.0, False, 10, 10, 3, 16, 3),    # T below 64
     (16, 8.0, True, 8, 8, 3, 64, 3),       # short window, fire start
     (64, 0.0, False, 12, 12, 1, 6, 5),     # LeNet conv1's shape (the built-in choice)
+    (64, 0.0, False, 9, 7, 2, 7, 3),       # no padding, 18 elements, nine pixels per wave (offset table)
+    (64, 16.0, True, 7, 9, 3, 12, 3),      # same padding, 27 elements, five pixels per wave (bounds tests)
 ]
 
 
