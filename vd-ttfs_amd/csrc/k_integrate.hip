@@ -2902,7 +2902,10 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
 // of gathers per 8 events rather than per bin.  Lanes of one pixel read the
 // same list entries.  E_proc / E_bin count per lane with the
 // same rules as k_stream (a neuron counts a bin's events while it was alive
-// at the start of the chunk / of the bin).
+// at the start of the chunk / of the bin).  The eight bins of a group are
+// unrolled, each with its end in a register: with the group's bin index a
+// loop variable, selecting the end had cost seven instructions per bin
+// (LeNet-5 conv2 at B=1024, A/B on one box: 0.209 -> 0.176 ms with its merge).
 template <bool COUNT, bool CULIF>
 __global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __restrict__ out,
                                                        const int2* __restrict__ list,
@@ -2946,27 +2949,28 @@ __global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __re
             float w[8];
             bool need = true;  // uniform
             float acc = 0.0f;
-            for (int g = 0; g < ng;) {  // uniform
-                int be = ends[0];
+            // the eight bins unrolled, so each reads its end from a register
 #pragma unroll
-                for (int q = 1; q < 8; ++q) be = g == q ? ends[q] : be;
-                if (need) {
+            for (int g = 0; g < 8; ++g) {
+                if (g >= ng) break;  // uniform
+                const int be = ends[g];
+                for (;;) {  // uniform: the window moves on while some lane's bin runs past it
+                    if (need) {
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) e[q] = L[wj + q];
+                        for (int q = 0; q < 8; ++q) e[q] = L[wj + q];
 #pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, e[q].x + voff, 0, 0));
-                    need = false;
-                }
+                        for (int q = 0; q < 8; ++q)
+                            w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, e[q].x + voff, 0, 0));
+                        need = false;
+                    }
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int idx = wj + q;
-                    acc = (idx >= s_ && idx < be) ? __builtin_fmaf(w[q], __int_as_float(e[q].y), acc) : acc;
-                }
-                if (__ballot(be > wj + 8)) {  // some lane's bin continues past the window
+                    for (int q = 0; q < 8; ++q) {
+                        const int idx = wj + q;
+                        acc = (idx >= s_ && idx < be) ? __builtin_fmaf(w[q], __int_as_float(e[q].y), acc) : acc;
+                    }
+                    if (__ballot(be > wj + 8) == 0) break;
                     wj = be > wj + 8 ? wj + 8 : be;
                     need = true;
-                    continue;
                 }
                 const int b = b8 + g;
                 const int t = t0 + b;
@@ -2994,7 +2998,6 @@ __global__ __launch_bounds__(256) void k_stream_narrow(StreamArgs a, float* __re
                 if (COUNT && chunk_end) alive_chunk = alive;
                 acc = 0.0f;
                 s_ = be;
-                ++g;
             }
             j = s_;
             // counting forwards keep going to the end of the chunk of the
