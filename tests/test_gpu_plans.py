@@ -73,7 +73,9 @@ def test_builtin_plans_and_rejections(gpu_ctx_factory):
         assert net.get_plan(0) == (REG, 1, 10)     # C_out 6: 10 pixels per wave
         assert net.get_plan(2) == (DENSE, 1, 4)    # 150 receptive elements: a list
         assert net.get_plan(6) == (FUSED, 1, 1)    # FC 84 -> 10: the shared-list kernel, one wave per image
-        assert net.get_plan(4) == (FUSED, 2, 1)    # FC 256 -> 120: the shared-list kernel
+        # FC 256 -> 120: the shared-list kernel; 16 images fit one round of
+        # waves, so two 64-wide waves per image rather than one 128-wide
+        assert net.get_plan(4) == (FUSED, 1, 1)
         with pytest.raises(vdttfs.VdttfsError):
             net.set_plan(0, 0, 0, 2)
         with pytest.raises(vdttfs.VdttfsError):

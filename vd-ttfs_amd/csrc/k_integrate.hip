@@ -3636,8 +3636,21 @@ bool shared_ok(const vdttfs_ctx* ctx, const IntegShape& sh, int gather) {
 // waves covers the layer; 64 per wave (four events per load) past that, so
 // that each c_out group of four waves holds a smaller share of the weights
 // in its XCD's L2, and where C_out <= 64 or is not a multiple of 4.
-int shared_gather(const IntegShape& sh) {
-    return (sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 256) ? 2 : 1;
+// For 64 < C_out <= 128 the pair gather is one wave per pixel, which builds
+// the list alone; where the launch fits one round of resident waves (at most
+// 32 per CU), two 64-wide waves that build together and stream half the
+// c_out each finish first (LeNet-5's FC 256 -> 120 and 120 -> 84 at B=1024,
+// 1,024 pixels: 0.025 / 0.017 -> 0.020 / 0.016 ms).
+namespace {
+int64_t cu_count(const vdttfs_ctx* ctx);
+}  // namespace
+int shared_gather(const vdttfs_ctx* ctx, const IntegShape& sh) {
+    if (!(sh.C_out % 4 == 0 && sh.C_out > 64 && sh.C_out <= 256)) return 1;
+    if (sh.C_out <= 128) {
+        const int64_t cus = cu_count(ctx);
+        if (cus > 0 && n_pixels(sh) * 2 <= cus * 32) return 1;
+    }
+    return 2;
 }
 
 // The kernel a fused plan with this gather runs: 1 the per-wave kernels
@@ -3835,7 +3848,7 @@ int64_t cu_count(const vdttfs_ctx* ctx) {
 // groups of 256 c_out) keep bucketize + merge, which build it once.
 bool shared_builtin(const vdttfs_ctx* ctx, const IntegShape& sh) {
     (void)ctx;
-    const int g = shared_gather(sh);
+    const int g = shared_gather(ctx, sh);
     const int cw = g == 4 ? 256 : (g == 2 ? 128 : 64);
     const int64_t n_cblk = (sh.C_out + cw - 1) / cw;
     const int waves = shared_waves(n_cblk, g);
@@ -3928,7 +3941,7 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
         // gather (shared_gather)
         const int pw = (dense || quad_wide_ok(ctx, sh)) && fused_ok(ctx, sh, p.gather) ? 1 : 0;
         if ((req.path == 0 || req.path == VDTTFS_PATH_FUSED) && !pw) {
-            const int g = shared_gather(sh);
+            const int g = shared_gather(ctx, sh);
             if (shared_ok(ctx, sh, g) && (req.path == VDTTFS_PATH_FUSED || shared_builtin(ctx, sh))) p.gather = g;
         }
     }
