@@ -2755,9 +2755,9 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     // Every spike-time and weight load is issued before any is used (no
     // branch between them; elements outside the map load its first word and
     // are masked), so a lane waits for two rounds of loads, not one per
-    // element: the spike times and weights, then the decay values.
-    // an instantiation whose NEL is not the 32-element limit runs only for
-    // fields of exactly NEL elements
+    // element: the spike times and weights, then the decay values.  An
+    // instantiation whose NEL is not the 32-element limit runs only for
+    // fields of exactly NEL elements (EXACT).
     constexpr bool EXACT = NEL != kSmallMaxEl;
     int bin[NEL];
     float wv[NEL], av[NEL];
