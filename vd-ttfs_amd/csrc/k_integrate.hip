@@ -222,9 +222,11 @@ constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 // tail zeroed) and its T+1 bin starts into `bs`, and returns the list length.
 // `cur` (T ints) and `kinfo` (2 * KMAX ints) are the wave's LDS scratch.  The
 // outputs are HBM (k_merge_dense) or the wave's LDS (k_stream_dense).
+// `msk` (2T words, or null): LDS bit masks for the ranks in pass 2; without
+// them the ranks come from a bit-ballot multisplit.
 template <int KMAX, int NB, class ListPtr, class BinPtr>
 __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo,
-                                           ListPtr out, BinPtr bs) {
+                                           ListPtr out, BinPtr bs, unsigned* msk = nullptr) {
     const int lane = lane_id();
     const int q = fdiv((int)pix, a.div_w);
     const int w_out = (int)pix - q * a.W_out;
@@ -249,7 +251,13 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
             kinfo[KMAX + slot] = lane * a.C_in;  // first weight row of the tap
         }
     }
-    for (int t = lane; t < a.T; t += 64) cur[t] = 0;
+    for (int t = lane; t < a.T; t += 64) {
+        cur[t] = 0;
+        if (msk) {
+            msk[2 * t] = 0;
+            msk[2 * t + 1] = 0;
+        }
+    }
     wave_sync();
     const int nel = nk * a.C_in;  // <= KMAX * 64 (C_in <= 64)
     // Elements f = chunk * 64 + lane are loaded a batch of NB chunks at a
@@ -335,17 +343,31 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
             const bool valid = c0 + c < n_chunks && b != 0xFF;
             uint64_t m = __ballot(valid);
             if (m != 0) {  // uniform (also false for chunks past the end)
-                for (int bit = 0; bit < a.nbits; ++bit) {
-                    const bool set = valid && ((b >> bit) & 1);
-                    const uint64_t bb = __ballot(set);
-                    m &= set ? bb : ~bb;
+                if (msk) {
+                    // the lanes of the chunk in bin b: each ORs its lane bit
+                    // into the bin's 64-bit mask (OR commutes, so the order the
+                    // LDS serves same-address lanes in does not matter) and
+                    // reads the mask back; the bin's first lane clears it
+                    // after the cursor update below
+                    if (valid) atomicOr(&msk[2 * b + (lane >> 5)], 1u << (lane & 31));
+                    wave_sync();
+                    m = valid ? *reinterpret_cast<const uint64_t*>(&msk[2 * b]) : 0ull;
+                } else {
+                    for (int bit = 0; bit < a.nbits; ++bit) {
+                        const bool set = valid && ((b >> bit) & 1);
+                        const uint64_t bb = __ballot(set);
+                        m &= set ? bb : ~bb;
+                    }
                 }
                 if (valid) {
                     const int pos = cur[b] + __popcll(m & lt);
                     out[pos] = make_int2((pk[c] >> 16) * a.rowbytes, __float_as_int(al[c]));
                 }
                 wave_sync();
-                if (valid && (m & lt) == 0) cur[b] += __popcll(m);
+                if (valid && (m & lt) == 0) {
+                    cur[b] += __popcll(m);
+                    if (msk) *reinterpret_cast<uint64_t*>(&msk[2 * b]) = 0ull;
+                }
                 wave_sync();
             }
         }
@@ -358,12 +380,13 @@ __device__ __forceinline__ int dense_build(const DenseMergeArgs& a, int64_t pix,
 template <int KMAX>
 __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_dense(DenseMergeArgs a) {
     __shared__ int cur_all[kMergeWaves][kDenseMaxBins];
+    __shared__ __align__(8) unsigned msk_all[kMergeWaves][2 * kDenseMaxBins];
     __shared__ int kinfo_all[kMergeWaves][2 * KMAX];
     const int wave = uniform(threadIdx.x >> 6);
     const int64_t pix = (int64_t)blockIdx.x * kMergeWaves + wave;
     if (pix >= a.n_pix) return;  // uniform per wave
     (void)dense_build<KMAX, 9>(a, pix, cur_all[wave], kinfo_all[wave], a.list + pix * a.cap,
-                            a.bstart + pix * (int64_t)(a.T + 1));
+                            a.bstart + pix * (int64_t)(a.T + 1), msk_all[wave]);
 }
 
 // ---------------------------------------------------------------------------
