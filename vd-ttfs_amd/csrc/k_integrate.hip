@@ -4018,8 +4018,12 @@ int resolve_plan(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& 
             // (0.447 -> 0.478 and 0.349 -> 0.415 ms).
             const int vec = p.gather == 4 ? 4 : (p.gather == 2 ? 2 : 1);
             const int64_t n_cblk = p.gather == 2 ? (sh.C_out + 127) / 128 : (sh.C_out + 64 * vec - 1) / (64 * vec);
+            // Past 8 c_out blocks an XCD streams one block at a time over all
+            // the pixels (map_block), so only that block's waves are in
+            // flight on it and the rule does not hold: config 5's FC 4096 x
+            // 4096 at B=512 (16 blocks) 0.147 -> 0.109 ms at one pixel per wave.
             const int64_t cap = stream_wave_capacity(ctx, p.gather);
-            if (cap > 0 && n_pix * n_cblk > cap && (n_pix + 1) / 2 * n_cblk <= cap) p.ppw = 2;
+            if (cap > 0 && n_cblk < 8 && n_pix * n_cblk > cap && (n_pix + 1) / 2 * n_cblk <= cap) p.ppw = 2;
         }
     }
     *out = p;
