@@ -261,6 +261,25 @@ int vdttfs_net_layer_output(vdttfs_net* net, int layer, const float** d_out, int
  * vdttfs_layer_forward), retained events N_ev and bucket columns N_cols. */
 int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint64_t* ebin,
                      uint64_t* n_ev, uint64_t* n_cols);
+/* Pool fusion.  No counterpart in the reference, whose 2x2 min pools are
+ * kernels of their own between the layers (T2V:192-209, launched per pool
+ * layer).  A fused pool layer (not the first or last layer) whose next
+ * layer runs the fused list build -- the shared-list kernel, or the
+ * per-wave kernel past 64 receptive elements, under a LUT neuron -- is
+ * computed inside that build from the pool's input (each receptive element
+ * the min over its 2x2 window, compared as the pool kernel does), so the
+ * pooled map is not written; other pools run as their own pass.  Outputs
+ * are the same either way.  vdttfs_net_layer_output of a fused pool layer
+ * writes its map then (stream-ordered).  Counting forwards never fuse.
+ * mode: OFF (the default) none; ALL every pool the next build can take;
+ * AUTO those whose pooled map is 1x1 (an FC layer's one window per
+ * channel), where the build's extra loads are fewest.  On VGG-16 B=256 the
+ * builds of the wider layers lose more to the four loads per element than
+ * the pool's own pass takes (ALL: forward +0.6%), and AUTO measured even. */
+#define VDTTFS_POOL_FUSE_OFF  0
+#define VDTTFS_POOL_FUSE_ALL  1
+#define VDTTFS_POOL_FUSE_AUTO 2
+int vdttfs_net_set_pool_fusion(vdttfs_net* net, int mode);
 /* Event timing of integrator launches: when enabled, forward() brackets
  * each integrator launch with HIP events on the context stream; read_timing
  * synchronises and returns the summed milliseconds and launch count since

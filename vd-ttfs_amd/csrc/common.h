@@ -154,11 +154,22 @@ int fused_kind(const vdttfs_ctx* ctx, const IntegShape& s, int gather);
 // lists built from the dense map) rather than bucketize +
 // launch_integrate_bins, with or without counters.
 bool plan_from_dense(const vdttfs_ctx* ctx, const IntegShape& s, const LaunchPlan& p, bool counters);
+// A 2x2 min pool (T2V:192-209) fused into a layer's list build: `in` of
+// launch_integrate_dense is then the pool's input, H_u x W_u x C_in per
+// image, and the layer reads its min windows (H_in = H_u / 2, W_in =
+// W_u / 2; an FC layer's input is then one 1 x 1 window).
+struct PoolIn {
+    int H_u, W_u;
+};
+// Whether the layer under resolved plan p (no counters, LUT neuron) can take
+// the pool in its build: the shared-list kernel, or the per-wave kernel past
+// 64 receptive elements, with the pool's input below 2^31 bytes.
+bool pool_fusable(const vdttfs_ctx* ctx, const IntegShape& s, const LaunchPlan& p, int H_u, int W_u);
 int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
                            int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
                            const float* theta, int t_min, const IntegShape& s,
                            unsigned long long* counters, const CulifNeuron* culif = nullptr,
-                           const LaunchPlan* plan = nullptr);
+                           const LaunchPlan* plan = nullptr, const PoolIn* pool = nullptr);
 
 int launch_pool_min(vdttfs_ctx* ctx, const float* in, float* out, int B, int H_in, int W_in, int C);
 int launch_fc_vmem(vdttfs_ctx* ctx, const float* in, float* out, const float* W, const float* bias,

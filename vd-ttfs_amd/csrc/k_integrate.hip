@@ -187,10 +187,11 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(MergeArgs a) {
 // gives the bin starts, pass 2 (re-reading the chunk, now in cache) places
 // each event at its bin's
 // cursor plus its rank among the chunk's lanes of the same bin.  The rank
-// comes from a multisplit of bit ballots (same-bin mask = AND over the bin's
-// bits of the matching ballot), so the order within a bin is (kh, kw, cin) --
-// the reference's per-bin fma order.  Neighbouring pixels read the same
-// columns, which stay in L2.
+// comes from the bin's LDS bit mask of the chunk's lanes (k_merge_dense), or
+// from a multisplit of bit ballots (same-bin mask = AND over the bin's bits
+// of the matching ballot; k_stream_dense), so the order within a bin is
+// (kh, kw, cin) -- the reference's per-bin fma order.  Neighbouring pixels
+// read the same columns, which stay in L2.
 struct DenseMergeArgs {
     int2* list;            // [n_pix][cap]
     int32_t* bstart;       // [n_pix][T+1]
@@ -208,6 +209,12 @@ struct DenseMergeArgs {
     const uint8_t* fired;  // CuLIF: per input site, nonzero where a channel spiked (or null)
     FastDiv div_w, div_h;  // by W_out, H_out (n_pix < 2^31)
     int in_bytes;          // bytes of `in` (k_stream_quad: below 2^31), else 0
+    // A 2x2 min pool fused into the list build (k_stream_quad<..., POOL>):
+    // `in` is then the pool's input [B][H_u][W_u][C_in], and the map the
+    // layer reads at (hi, wi, ci) is its min over rows 2hi, 2hi+1 and columns
+    // 2wi, 2wi+1 (in_bytes covers the pool's input); pdx and pdy are the byte
+    // steps to a window's next column and next row.
+    int H_u, W_u, pdx, pdy;
 };
 
 constexpr int kDenseMaxBins = 256;
@@ -216,6 +223,39 @@ constexpr int kQuadMaxCin = 128;  // k_stream_quad's list build: 18 chunks of 64
 // quad_build packs an event's weight row (tap * C_in + cin < 9 * kQuadMaxCin)
 // into bits 21..31 of its register
 static_assert(9 * kQuadMaxCin <= (1 << 11), "quad_build's 11-bit weight-row field");
+
+// Spike time of one element of the map a list build reads, at byte offset
+// off of `in`.  POOL: off addresses the first element of the element's 2x2
+// window in the pool's input, and the time is k_pool_min4's: m = t where
+// t < m, from kInfTime, over (0,0), (0,1), (1,0), (1,1) (T2V:192-209).  The
+// four loads are issued together, their offsets in scalar registers.
+template <bool POOL>
+__device__ __forceinline__ float map_time(__amdgpu_buffer_rsrc_t rin, int off, const DenseMergeArgs& a) {
+    if constexpr (!POOL) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, 0, 0));
+    } else {
+        const float t0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, 0, 0));
+        const float t1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, a.pdx, 0));
+        const float t2 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, a.pdy, 0));
+        const float t3 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, off, a.pdx + a.pdy, 0));
+        float m = kInfTime;
+        if (t0 < m) m = t0;
+        if (t1 < m) m = t1;
+        if (t2 < m) m = t2;
+        if (t3 < m) m = t3;
+        return m;
+    }
+}
+
+// Input column of tap (hi, wi) of image img (in bounds): the map's, or with
+// POOL the first column of its 2x2 window in the pool's input.
+template <bool POOL>
+__device__ __forceinline__ int map_col(const DenseMergeArgs& a, int img, int hi, int wi) {
+    if constexpr (POOL)
+        return (img * a.H_u + 2 * hi) * a.W_u + 2 * wi;
+    else
+        return (img * a.H_in + hi) * a.W_in + wi;
+}
 constexpr size_t kFusedMaxLds = 64 * 1024;  // LDS of one k_stream_dense block
 
 // Builds pixel `pix`'s merged list into `out` (total + kListPad entries, the
@@ -1167,9 +1207,10 @@ __host__ __device__ inline int quad_wave_words(int nel_max, int T, bool alphas =
 // (VGG-16 conv 1 +0.7% with it).  ALPHA: entries are 16-bit rows beside
 // alphas (the LUT neuron); without, row byte offsets (the CuLIF neuron), and
 // a field without events returns 0 before the passes.
-template <int NB, bool OPAQUE, bool ALPHA>
+template <int NB, bool OPAQUE, bool ALPHA, bool POOL = false>
 __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, int* cur, int* kinfo, int* rows,
                                           int* alph, int* bs) {
+    static_assert(!(POOL && !ALPHA), "the pool is fused into LUT-neuron builds only");
     constexpr int KMAX = 9;
     int lane = lane_id();
     if constexpr (OPAQUE) asm volatile("" : "+v"(lane));
@@ -1185,7 +1226,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int kh = lane / a.K_w, kw = lane - kh * a.K_w;
             const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kw;
             v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
-            col = (img * a.H_in + hi) * a.W_in + wi;
+            col = map_col<POOL>(a, img, hi, wi);
         }
         const uint64_t m = __ballot(v);
         if constexpr (!ALPHA) {
@@ -1229,7 +1270,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
             const int ci = f - (int)__umul24((unsigned)k, (unsigned)a.C_in);  // k <= 8, C_in <= 128
             rw[c] = kinfo[KMAX + k] + ci;
             const int off = (kinfo[k] + ci) * 4;
-            xs[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? off : 0, 0, 0));
+            xs[c] = map_time<POOL>(rin, in ? off : 0, a);
         }
         // arrival_bin and alpha_index without branches: bin floor(t - tfs)
         // clamped below at 0 (floor commutes with the clamp), -1 for no
@@ -1392,6 +1433,7 @@ __device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
 // element and k0 + 1, chosen per lane; otherwise the entries come from the
 // wave's LDS tap table.  Elements past the end load the map's first word and
 // are no event.
+template <bool POOL>
 __device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, int nel, int nk, int tcol, int trow,
                                                const int* ktab, float& t, int& row) {
     const int lane = lane_id();
@@ -1403,8 +1445,7 @@ __device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, i
         const int k0 = __builtin_amdgcn_readfirstlane((int)(((float)(c * 64) + 0.5f) * a.inv_cin));
         const int ci = c * 64 - k0 * a.C_in + lane;
         row = __builtin_amdgcn_readlane(trow, k0) + ci;
-        t = __uint_as_float(
-            __builtin_amdgcn_raw_buffer_load_b32(rin, (__builtin_amdgcn_readlane(tcol, k0) + ci) * 4, 0, 0));
+        t = map_time<POOL>(rin, (__builtin_amdgcn_readlane(tcol, k0) + ci) * 4, a);
         return;  // f < nel: nel is a multiple of 64
     }
     const int k = in ? (int)(((float)f + 0.5f) * a.inv_cin) : 0;
@@ -1421,7 +1462,7 @@ __device__ __forceinline__ void shared_element(const DenseMergeArgs& a, int c, i
         ro = ktab[16 + k];
     }
     row = ro + ci;
-    t = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rin, in ? (co + ci) * 4 : 0, 0, 0));
+    t = map_time<POOL>(rin, in ? (co + ci) * 4 : 0, a);
     if (!in) t = kInfTime;
 }
 
@@ -1437,6 +1478,7 @@ __device__ __forceinline__ int shared_bin(const DenseMergeArgs& a, float t) {
 // nk, tcol and trow describe the in-bounds taps for shared_place: lane
 // s < nk holds tap s's input element offset col * C_in and first weight row
 // tap * C_in (taps compacted in (kh, kw) order).
+template <bool POOL>
 __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, int W, int wave, int* tables,
                                             int& v_end, int& nk, int& tcol, int& trow) {
     const int lane = lane_id();
@@ -1456,7 +1498,7 @@ __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, in
             const int kh = lane / a.K_w, kx = lane - kh * a.K_w;
             const int hi = h_out - a.pad_h + kh, wi = w_out - a.pad_w + kx;
             v = hi >= 0 && hi < a.H_in && wi >= 0 && wi < a.W_in;
-            col = (img * a.H_in + hi) * a.W_in + wi;
+            col = map_col<POOL>(a, img, hi, wi);
         }
         const uint64_t m = __ballot(v);
         nk = uniform(__popcll(m));
@@ -1487,7 +1529,7 @@ __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, in
         for (int i = 0; i < kSharedBatch; ++i) {
             t[i] = kInfTime;
             rw[i] = 0;
-            if (c0 + i < c_hi) shared_element(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
+            if (c0 + i < c_hi) shared_element<POOL>(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
         }
 #pragma unroll
         for (int i = 0; i < kSharedBatch; ++i) {
@@ -1516,7 +1558,7 @@ __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, in
 // barrier.  The cursors restart from the counts of pass 1, so a window's
 // positions do not depend on the windows before it.  NBAT chunk loads are
 // issued together.
-template <bool ALPHA, int NBAT>
+template <bool ALPHA, int NBAT, bool POOL>
 __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int wave, int* rows, int* alph,
                                              int* tables, int P0, int cap, int total, int nk, int tcol,
                                              int trow, float al_lane, float al_64) {
@@ -1564,7 +1606,7 @@ __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int
         for (int i = 0; i < NBAT; ++i) {
             t[i] = kInfTime;
             rw[i] = 0;
-            if (c0 + i < c_hi) shared_element(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
+            if (c0 + i < c_hi) shared_element<POOL>(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
         }
 #pragma unroll
         for (int i = 0; i < NBAT; ++i) {
@@ -1614,7 +1656,9 @@ __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int
     __syncthreads();
 }
 
-template <int GEO, int NB, bool CULIF>
+// POOL: a 2x2 min pool runs inside the list build, from the pool's input
+// (DenseMergeArgs::H_u, W_u, pdx, pdy), so the pooled map is never written.
+template <int GEO, int NB, bool CULIF, bool POOL = false>
 // The CuLIF pair kernel with 9 chunks (CuLIF-7 conv2, VALU-bound) is held to
 // 8 waves per SIMD: its 104 scalar registers would allow 7, and the 27 it
 // spills to VGPR lanes cost less than the wave (A/B on one box: 2.38 -> 2.29
@@ -1624,6 +1668,7 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
     DenseMergeArgs m, StreamArgs a, float* __restrict__ out, const float* __restrict__ theta, int nel_max) {
     static_assert(GEO == 4 || GEO == 2 || (GEO == 1 && NB <= 0),
                   "four events per load (64 c_out), two (128 c_out), or one (256 c_out, shared lists)");
+    static_assert(!(POOL && CULIF), "the pool is fused into LUT-neuron builds only");
     constexpr int OWN = 4 / GEO;  // c_out per lane
     constexpr int LPG = 8 / GEO;  // loads per group of 8 events
     // NB <= 0: one pixel per workgroup, its list shared by the workgroup's
@@ -1704,11 +1749,11 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
         int snk = 0, stcol = 0, strow = 0;  // SHARED: the pixel's taps
         int* tables = lds_words + shared_list_words(nel_max, T, !CULIF);
         if constexpr (SHARED) {
-            total = shared_count(m, (int)pix, blockDim.x >> 6, wave, tables, sv_end, snk, stcol, strow);
-            shared_place<!CULIF, kSharedBatch>(m, blockDim.x >> 6, wave, rows, alph, tables, 0, nel_max, total,
+            total = shared_count<POOL>(m, (int)pix, blockDim.x >> 6, wave, tables, sv_end, snk, stcol, strow);
+            shared_place<!CULIF, kSharedBatch, POOL>(m, blockDim.x >> 6, wave, rows, alph, tables, 0, nel_max, total,
                                                snk, stcol, strow, al_lane, al_64);
         } else {
-            total = quad_build<NB, (CULIF || NB > 9), !CULIF>(m, pix, cur, kinfo, rows, alph, bs);
+            total = quad_build<NB, (CULIF || NB > 9), !CULIF, POOL>(m, pix, cur, kinfo, rows, alph, bs);
             wave_sync();
         }
         if (CULIF && total == 0) {  // uniform
@@ -1943,7 +1988,7 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
                 if (jlim == INT_MAX) break;  // uniform: the last window
                 P0 += nel_max;
                 __syncthreads();  // every wave is done with this window
-                shared_place<!CULIF, 1>(m, blockDim.x >> 6, wave, rows, alph, tables, P0, nel_max, total, snk,
+                shared_place<!CULIF, 1, POOL>(m, blockDim.x >> 6, wave, rows, alph, tables, P0, nel_max, total, snk,
                                         stcol, strow, al_lane, al_64);
                 if (lane < T) v_end = sv_end - P0;
                 if (live) bend = __builtin_amdgcn_readlane(v_end, b);
@@ -3518,7 +3563,7 @@ int launch_stream_multi(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamAr
 }
 
 int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamArgs& a, float* out,
-                         const float* theta, int64_t nel_max, int gather, bool culif) {
+                         const float* theta, int64_t nel_max, int gather, bool culif, bool pool) {
     const int waves = shared_waves(a.n_cblk, gather);
     const int64_t n_grp = (a.n_cblk + waves - 1) / waves;
     const int64_t blocks = a.n_pix * n_grp;
@@ -3527,31 +3572,38 @@ int launch_stream_shared(vdttfs_ctx* ctx, const DenseMergeArgs& m, const StreamA
     const int cap = shared_cap(nel_max, waves, !culif, gather);
     const size_t lds = (size_t)shared_block_words(cap, m.T, !culif, waves) * sizeof(int);
     if (lds > kFusedMaxLds) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: shared list exceeds LDS");
-#define VD_LAUNCH_SHARED(G, NB, L)                                                                      \
-    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)blocks), dim3(64 * waves), lds, ctx->stream, \
+#define VD_LAUNCH_SHARED(G, NB, L, P)                                                                      \
+    hipLaunchKernelGGL((k_stream_quad<G, NB, L, P>), dim3((unsigned)blocks), dim3(64 * waves), lds, ctx->stream, \
                        m, a, out, theta, cap)
-#define VD_LAUNCH_SHARED_NB(G, L)       \
-    do {                                \
-        if (cap < nel_max)              \
-            VD_LAUNCH_SHARED(G, -1, L); \
-        else                            \
-            VD_LAUNCH_SHARED(G, 0, L);  \
+#define VD_LAUNCH_SHARED_NB(G, L, P)       \
+    do {                                   \
+        if (cap < nel_max)                 \
+            VD_LAUNCH_SHARED(G, -1, L, P); \
+        else                               \
+            VD_LAUNCH_SHARED(G, 0, L, P);  \
     } while (0)
+    if (culif && pool) return set_error(VDTTFS_E_INVALID, "integrate: the pool is fused into LUT-neuron builds only");
     if (gather == 4) {  // one event per load, four c_out per lane
         if (culif)
-            VD_LAUNCH_SHARED_NB(1, true);
+            VD_LAUNCH_SHARED_NB(1, true, false);
+        else if (pool)
+            VD_LAUNCH_SHARED_NB(1, false, true);
         else
-            VD_LAUNCH_SHARED_NB(1, false);
+            VD_LAUNCH_SHARED_NB(1, false, false);
     } else if (gather == 2) {
         if (culif)
-            VD_LAUNCH_SHARED_NB(2, true);
+            VD_LAUNCH_SHARED_NB(2, true, false);
+        else if (pool)
+            VD_LAUNCH_SHARED_NB(2, false, true);
         else
-            VD_LAUNCH_SHARED_NB(2, false);
+            VD_LAUNCH_SHARED_NB(2, false, false);
     } else {
         if (culif)
-            VD_LAUNCH_SHARED_NB(4, true);
+            VD_LAUNCH_SHARED_NB(4, true, false);
+        else if (pool)
+            VD_LAUNCH_SHARED_NB(4, false, true);
         else
-            VD_LAUNCH_SHARED_NB(4, false);
+            VD_LAUNCH_SHARED_NB(4, false, false);
     }
 #undef VD_LAUNCH_SHARED_NB
 #undef VD_LAUNCH_SHARED
@@ -4091,10 +4143,22 @@ int launch_integrate_bins(vdttfs_ctx* ctx, float* out, const vd_event* ev, const
     return launch_stream(ctx, out, list, cap, bstart, W, wbytes, bias, theta, t_min, sh, counters, culif, p);
 }
 
+bool pool_fusable(const vdttfs_ctx* ctx, const IntegShape& sh, const LaunchPlan& p, int H_u, int W_u) {
+    if (p.path != VDTTFS_PATH_FUSED) return false;
+    if (H_u / 2 != sh.H_in || W_u / 2 != sh.W_in || H_u < 2 || W_u < 2) return false;
+    if ((int64_t)sh.B * H_u * W_u * sh.C_in * 4 >= (INT64_C(1) << 31)) return false;
+    int64_t wbytes;
+    if (narrow_path_ok(sh, &wbytes) || !plan_lds_list(ctx, sh, p, false, false)) return false;
+    const int kind = fused_kind(ctx, sh, p.gather);
+    // the shared-list kernel, or the per-wave kernel of 9 or 18 chunks
+    return (kind == 2 && p.ppw != kMultiImages) || (kind == 1 && sh.K_h * sh.K_w * sh.C_in > 64);
+}
+
 int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const float* alpha, int2* list,
                            int64_t list_cap, int32_t* bstart, const float* W, const float* bias,
                            const float* theta, int t_min, const IntegShape& sh,
-                           unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan) {
+                           unsigned long long* counters, const CulifNeuron* culif, const LaunchPlan* plan,
+                           const PoolIn* pool) {
     int64_t wbytes;
     const bool narrow = narrow_path_ok(sh, &wbytes);
     const bool wide = !integrate_dense_ok(ctx, sh) && quad_wide_ok(ctx, sh);
@@ -4154,6 +4218,15 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
     m.div_h = make_fastdiv(sh.H_out);
     const int64_t in_bytes = (int64_t)sh.B * sh.H_in * sh.W_in * sh.C_in * 4;
     m.in_bytes = in_bytes < (INT64_C(1) << 31) ? (int)in_bytes : 0;
+    if (pool) {
+        if (counters || culif || !pool_fusable(ctx, sh, p, pool->H_u, pool->W_u))
+            return set_error(VDTTFS_E_INVALID, "integrate: this layer's list build cannot take the pool");
+        m.H_u = pool->H_u;
+        m.W_u = pool->W_u;
+        m.pdx = sh.C_in * 4;
+        m.pdy = pool->W_u * sh.C_in * 4;
+        m.in_bytes = (int)((int64_t)sh.B * pool->H_u * pool->W_u * sh.C_in * 4);  // < 2^31 (pool_fusable)
+    }
     const int64_t mblocks = (n_pix + kMergeWaves - 1) / kMergeWaves;
     if (mblocks > 0x7fffffff) return set_error(VDTTFS_E_UNSUPPORTED, "integrate: grid too large");
     if (narrow && !shared) {
@@ -4176,7 +4249,8 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
         if (shared && p.ppw == kMultiImages && !culif)
             return launch_stream_multi(ctx, m, a, out, theta, shared_nel_max(sh), sh);
         if (shared)
-            return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), p.gather, culif != nullptr);
+            return launch_stream_shared(ctx, m, a, out, theta, shared_nel_max(sh), p.gather, culif != nullptr,
+                                        pool != nullptr);
         // build the list in LDS and stream it there
         const int64_t fblocks = (n_pix + kMergeWaves * a.ppw - 1) / (kMergeWaves * a.ppw);
         if (!counters && m.in_bytes > 0) {
@@ -4187,19 +4261,31 @@ int launch_integrate_dense(vdttfs_ctx* ctx, float* out, const float* in, const f
             const int qw = (epi != 2 && nel_max <= 64) ? kQuadWaves : 1;
             const size_t qlds = (size_t)qw * quad_wave_words(nel_max, m.T, culif == nullptr) * sizeof(int);
             const int64_t qblocks = (n_pix + qw * a.ppw - 1) / (qw * a.ppw);
-#define VD_LAUNCH_QUAD(G, NB, L)                                                                           \
-    hipLaunchKernelGGL((k_stream_quad<G, NB, L>), dim3((unsigned)qblocks), dim3(64 * qw), qlds, \
+#define VD_LAUNCH_QUAD(G, NB, L, P)                                                                        \
+    hipLaunchKernelGGL((k_stream_quad<G, NB, L, P>), dim3((unsigned)qblocks), dim3(64 * qw), qlds, \
                        ctx->stream, m, a, out, theta, nel_max)
-#define VD_LAUNCH_QUAD_NB(G, L)          \
-    do {                                 \
-        if (nel_max <= 64)               \
-            VD_LAUNCH_QUAD(G, 1, L);     \
-        else if (nel_max <= 9 * 64)      \
-            VD_LAUNCH_QUAD(G, 9, L);     \
-        else                             \
-            VD_LAUNCH_QUAD(G, 18, L);    \
+#define VD_LAUNCH_QUAD_NB(G, L)              \
+    do {                                     \
+        if (nel_max <= 64)                   \
+            VD_LAUNCH_QUAD(G, 1, L, false);  \
+        else if (nel_max <= 9 * 64)          \
+            VD_LAUNCH_QUAD(G, 9, L, false);  \
+        else                                 \
+            VD_LAUNCH_QUAD(G, 18, L, false); \
     } while (0)
-            if (epi == 2) {
+            if (pool) {  // nel_max > 64 (pool_fusable)
+                if (nel_max <= 9 * 64) {
+                    if (epi == 2)
+                        VD_LAUNCH_QUAD(2, 9, false, true);
+                    else
+                        VD_LAUNCH_QUAD(4, 9, false, true);
+                } else {
+                    if (epi == 2)
+                        VD_LAUNCH_QUAD(2, 18, false, true);
+                    else
+                        VD_LAUNCH_QUAD(4, 18, false, true);
+                }
+            } else if (epi == 2) {
                 if (culif)
                     VD_LAUNCH_QUAD_NB(2, true);
                 else

@@ -30,6 +30,10 @@ struct NetLayer {
     int t_min = 0;
     int window = 0;  // integration window T'_l; 0 = the context's T
     LaunchPlan plan;  // requested launch plan; zero fields = built-in choice
+    // POOL: the last forward ran this pool inside the next layer's list
+    // build, so `out` is written only when asked for (from pool_src)
+    bool fused = false;
+    const float* pool_src = nullptr;
 };
 
 struct TimedPair {
@@ -54,6 +58,7 @@ struct vdttfs_net {
     int2* list = nullptr;
     int32_t* bstart = nullptr;
     bool timing = false;
+    int pool_fusion = VDTTFS_POOL_FUSE_OFF;  // which 2x2 pools run inside the next layer's list build
     std::vector<hipEvent_t> pool;
     size_t pool_used = 0;
     std::vector<TimedPair> pending;
@@ -185,12 +190,43 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
         VD_TRY(launch_encode_linear(ctx, d_img, net->enc, n_img));
     else
         cur = d_img;  // VDTTFS_ENCODE_TIMES: the input already holds spike times
+    // a pool whose launch waits for the next layer: that layer's list build
+    // takes it where it can (pool fusion), else it runs first
+    NetLayer* pend = nullptr;
     for (size_t i = 0; i < net->L.size(); ++i) {
         NetLayer& l = net->L[i];
         const vdttfs_layer_desc& d = l.d;
         WindowScope window(ctx, l.window);
+        PoolIn pin{};
+        const PoolIn* fuse = nullptr;  // the pending pool, taken by this layer's build
+        if (pend) {
+            bool take = false;
+            if (d.kind == VDTTFS_LAYER_CONV || d.kind == VDTTFS_LAYER_FC) {
+                LaunchPlan plan;
+                const IntegShape s = integ_shape(net, l);
+                take = resolve_plan(ctx, s, l.plan, &plan) == VDTTFS_OK && plan_from_dense(ctx, s, plan, false) &&
+                       pool_fusable(ctx, s, plan, pend->d.H_in, pend->d.W_in);
+            }
+            if (take) {
+                pin = PoolIn{pend->d.H_in, pend->d.W_in};
+                fuse = &pin;
+                pend->fused = true;
+                cur = pend->pool_src;
+            } else {
+                VD_TRY(launch_pool_min(ctx, pend->pool_src, pend->out, net->B, pend->d.H_in, pend->d.W_in,
+                                       pend->d.C_in));
+            }
+            pend = nullptr;
+        }
+        l.fused = false;
         if (d.kind == VDTTFS_LAYER_POOL) {
-            VD_TRY(launch_pool_min(ctx, cur, l.out, net->B, d.H_in, d.W_in, d.C_in));
+            l.pool_src = cur;
+            const bool want = net->pool_fusion == VDTTFS_POOL_FUSE_ALL ||
+                              (net->pool_fusion == VDTTFS_POOL_FUSE_AUTO && d.H_out == 1 && d.W_out == 1);
+            if (want && !count && i > 0 && i + 1 < net->L.size())
+                pend = &l;
+            else
+                VD_TRY(launch_pool_min(ctx, cur, l.out, net->B, d.H_in, d.W_in, d.C_in));
         } else if (d.kind == VDTTFS_LAYER_VMEM) {
             VD_TRY(launch_fc_vmem(ctx, cur, l.out, l.W, l.bias, l.alpha, net->B,
                                   d.H_in * d.W_in * d.C_in, d.C_out));
@@ -221,7 +257,7 @@ int forward_impl(vdttfs_net* net, const float* d_img, int32_t* d_pred, uint64_t*
             if (dense)
                 VD_TRY(launch_integrate_dense(ctx, l.out, cur, l.alpha, net->list, l.list_cap,
                                               net->bstart, l.W, l.bias, l.theta, l.t_min, s,
-                                              count ? ctx->d_counters : nullptr, nullptr, &plan));
+                                              count ? ctx->d_counters : nullptr, nullptr, &plan, fuse));
             else
                 VD_TRY(launch_integrate_bins(ctx, l.out, net->ev, net->off, net->list, l.list_cap,
                                              net->bstart, l.W, l.bias, l.theta, l.t_min, s,
@@ -434,7 +470,12 @@ int vdttfs_net_forward(vdttfs_net* net, const float* d_img, int32_t* d_pred) {
 int vdttfs_net_layer_output(vdttfs_net* net, int layer, const float** d_out, int64_t* elems) {
     if (!net || !d_out || layer < 0 || layer >= (int)net->L.size())
         return set_error(VDTTFS_E_INVALID, "net_layer_output: bad argument");
-    *d_out = net->L[layer].out;
+    NetLayer& l = net->L[layer];
+    if (l.fused) {  // a pool the last forward fused into the next build: write its map now
+        VD_TRY(launch_pool_min(net->ctx, l.pool_src, l.out, net->B, l.d.H_in, l.d.W_in, l.d.C_in));
+        l.fused = false;
+    }
+    *d_out = l.out;
     if (elems) *elems = net->L[layer].out_elems;
     return VDTTFS_OK;
 }
@@ -454,6 +495,14 @@ int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint6
         if (n_ev) n_ev[i] = c[i];
         if (n_cols) n_cols[i] = d[i];
     }
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_set_pool_fusion(vdttfs_net* net, int mode) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    if (mode != VDTTFS_POOL_FUSE_OFF && mode != VDTTFS_POOL_FUSE_ALL && mode != VDTTFS_POOL_FUSE_AUTO)
+        return set_error(VDTTFS_E_INVALID, "net_set_pool_fusion: unknown mode %d", mode);
+    net->pool_fusion = mode;
     return VDTTFS_OK;
 }
 

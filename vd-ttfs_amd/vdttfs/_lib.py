@@ -29,6 +29,7 @@ READOUT_ARGMIN, READOUT_ARGMAX, READOUT_ARGMIN_FIRST = 0, 1, 2
 CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL, CULIF_FC_REC, CULIF_FC = 0, 1, 2, 3, 4
 STEP_T1, STEP_T2, STEP_T3 = 1, 2, 3
 PATH_AUTO, PATH_BINS, PATH_DENSE, PATH_FUSED, PATH_REG, PATH_WINDOW = 0, 1, 2, 3, 4, 5
+POOL_FUSE_OFF, POOL_FUSE_ALL, POOL_FUSE_AUTO = 0, 1, 2
 
 
 class VdttfsError(RuntimeError):
@@ -177,6 +178,7 @@ SIGNATURES = {
     "vdttfs_stepnet_create_culif": [_vp, C.POINTER(CulifLayer), _i, _i, C.POINTER(_vp)],
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
+    "vdttfs_net_set_pool_fusion": [_vp, _i],
     "vdttfs_net_set_windows": [_vp, _vp, _i],
     "vdttfs_net_set_plan": [_vp, _i, _vp],
     "vdttfs_net_get_plan": [_vp, _i, _vp],

@@ -344,6 +344,12 @@ class Net:
     def set_timing(self, on: bool):
         check(lib().vdttfs_net_set_timing(self.handle, int(on)))
 
+    def set_pool_fusion(self, mode: int):
+        """Which 2x2 pools run inside the next layer's list build
+        (vdttfs_net_set_pool_fusion: POOL_FUSE_OFF, the default, _ALL or
+        _AUTO); the outputs are the same."""
+        check(lib().vdttfs_net_set_pool_fusion(self.handle, int(mode)))
+
     def set_windows(self, windows=None):
         """Per-layer integration windows T'_l (vdttfs_net_set_windows): one
         entry per layer, 0 or T for the full window, pools ignored; None resets."""
