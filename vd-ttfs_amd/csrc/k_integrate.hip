@@ -1406,6 +1406,7 @@ __device__ __forceinline__ int quad_build(const DenseMergeArgs& a, int64_t pix, 
 constexpr int kSharedMaxWaves = 4;
 constexpr int kSharedWaveWords = 64 + 64 + 128 + 32;
 constexpr int kSharedBatch = 8;  // chunk loads a wave issues before using any
+constexpr int kSharedKeep = 16;  // chunks per wave whose pass-1 results pass 2 takes from registers
 
 __host__ __device__ inline int shared_list_words(int nel_max, int T, bool alphas) {
     return (quad_list_words(nel_max, T, alphas) + 3) & ~3;
@@ -1472,15 +1473,30 @@ __device__ __forceinline__ int shared_bin(const DenseMergeArgs& a, float t) {
     return (t < kInfTime && tb < a.T) ? tb : -1;
 }
 
+// The first KEEP chunks of a wave's range, as pass 1 found them, held in
+// registers for pass 2 (which then neither reloads nor re-bins them): bin
+// (bits 0..6, 0x7F: no event), decay-LUT index (7..13), weight row (14..29).
+template <int KEEP>
+struct SharedKeep {
+    int v[KEEP > 0 ? KEEP : 1];
+};
+__device__ __forceinline__ int keep_pack(int b, int ai, int row) { return (row << 14) | (ai << 7) | (b & 0x7F); }
+
+// Decay-LUT index of an event at time t in bin b >= 0: the bin, or
+// clamp((int)t, 0, T) by spike time; 0 for no event.
+__device__ __forceinline__ int shared_alpha_index(const DenseMergeArgs& a, float t, int b) {
+    return b < 0 ? 0 : (a.alpha_by_time ? (int)fminf(fmaxf(t, 0.0f), (float)a.T) : b);
+}
+
 // Pass 1 and the scan of the shared-list build, with every wave of the
 // workgroup (it ends with a workgroup barrier).  Returns the pixel's list
 // length; v_end gets, in lane b < T, the end of bin b (INT_MAX elsewhere);
 // nk, tcol and trow describe the in-bounds taps for shared_place: lane
 // s < nk holds tap s's input element offset col * C_in and first weight row
 // tap * C_in (taps compacted in (kh, kw) order).
-template <bool POOL>
+template <bool POOL, int KEEP>
 __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, int W, int wave, int* tables,
-                                            int& v_end, int& nk, int& tcol, int& trow) {
+                                            int& v_end, int& nk, int& tcol, int& trow, SharedKeep<KEEP>& keep) {
     const int lane = lane_id();
     const int T = a.T;
     int* mine = tables + kSharedWaveWords * wave;
@@ -1520,9 +1536,32 @@ __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, in
     const int c_lo = (int)((unsigned)(n_chunks * wave) / (unsigned)W);
     const int c_hi = (int)((unsigned)(n_chunks * (wave + 1)) / (unsigned)W);
     // pass 1: this wave's events per bin (bin 0 from ballots; the counting
-    // atomics return nothing, so nothing waits on them)
+    // atomics return nothing, so nothing waits on them); the first KEEP
+    // chunks are kept in registers
+    static_assert(KEEP % kSharedBatch == 0, "whole batches are kept");
     int n0 = 0;
-    for (int c0 = c_lo; c0 < c_hi; c0 += kSharedBatch) {  // uniform
+#pragma unroll
+    for (int bt = 0; bt < KEEP / kSharedBatch; ++bt) {
+        const int c0 = c_lo + bt * kSharedBatch;
+        if (c0 < c_hi) {  // uniform
+            float t[kSharedBatch];
+            int rw[kSharedBatch];
+#pragma unroll
+            for (int i = 0; i < kSharedBatch; ++i) {
+                t[i] = kInfTime;
+                rw[i] = 0;
+                if (c0 + i < c_hi) shared_element<POOL>(a, c0 + i, nel, nk, tcol, trow, ktab, t[i], rw[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < kSharedBatch; ++i) {
+                const int b = c0 + i < c_hi ? shared_bin(a, t[i]) : -1;
+                n0 += __popcll(__ballot(b == 0));
+                if (b > 0) atomicAdd(&cnt[b], 1);
+                keep.v[bt * kSharedBatch + i] = keep_pack(b, shared_alpha_index(a, t[i], b), rw[i]);
+            }
+        }
+    }
+    for (int c0 = c_lo + KEEP; c0 < c_hi; c0 += kSharedBatch) {  // uniform
         float t[kSharedBatch];
         int rw[kSharedBatch];
 #pragma unroll
@@ -1558,10 +1597,10 @@ __device__ __forceinline__ int shared_count(const DenseMergeArgs& a, int pix, in
 // barrier.  The cursors restart from the counts of pass 1, so a window's
 // positions do not depend on the windows before it.  NBAT chunk loads are
 // issued together.
-template <bool ALPHA, int NBAT, bool POOL>
+template <bool ALPHA, int NBAT, bool POOL, int KEEP>
 __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int wave, int* rows, int* alph,
                                              int* tables, int P0, int cap, int total, int nk, int tcol,
-                                             int trow, float al_lane, float al_64) {
+                                             int trow, float al_lane, float al_64, const SharedKeep<KEEP>& keep) {
     const int lane = lane_id();
     const int T = a.T;
     int* mine = tables + kSharedWaveWords * wave;
@@ -1599,7 +1638,51 @@ __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int
     // result, no wait).
     const uint64_t lt = lanemask_lt();
     const unsigned bit = 1u << (lane & 31);
-    for (int c0 = c_lo; c0 < c_hi; c0 += NBAT) {  // uniform
+    // one chunk's events: bin b (-1: none), weight row rw, decay-LUT index ai
+    auto place = [&](int b, int rw, int ai) {
+        float al = 0.0f;
+        if constexpr (ALPHA) al = __shfl(al_lane, ai & 63, 64);
+        const uint64_t z0 = __ballot(b == 0);
+        int pos = cur0 + __popcll(z0 & lt);
+        cur0 += __popcll(z0);
+        const bool oth = b > 0;
+        if (__ballot(oth) != 0) {  // uniform
+            if (oth) atomicOr(&msk[2 * b + (lane >> 5)], bit);
+            lds_order();
+            uint64_t mm = 0;
+            int cb = 0;
+            if (oth) {
+                mm = *reinterpret_cast<const uint64_t*>(&msk[2 * b]);
+                cb = cur[b];
+            }
+            lds_order();
+            if (oth) pos = cb + __popcll(mm & lt);
+            if (oth && (mm >> lane) == 1ull) {  // the bin's last lane in this chunk
+                atomicAdd(&cur[b], __popcll(mm));
+                const int z = vzero();
+                *reinterpret_cast<int2*>(&msk[2 * b]) = make_int2(z, z);
+            }
+            lds_order();
+        }
+        const int q = pos - P0;
+        if (b >= 0 && q >= 0 && q < cap) {
+            if constexpr (ALPHA) {
+                reinterpret_cast<unsigned short*>(rows)[q] = (unsigned short)rw;
+                alph[q] = __float_as_int(ai == 64 ? al_64 : al);
+            } else {
+                rows[q] = (int)__umul24((unsigned)rw, (unsigned)a.rowbytes);
+            }
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < KEEP; ++j) {
+        if (c_lo + j < c_hi) {  // uniform
+            const unsigned pk = (unsigned)keep.v[j];
+            const int b7 = (int)(pk & 0x7F);
+            place(b7 == 0x7F ? -1 : b7, (int)(pk >> 14), (int)((pk >> 7) & 0x7F));
+        }
+    }
+    for (int c0 = c_lo + KEEP; c0 < c_hi; c0 += NBAT) {  // uniform
         float t[NBAT];
         int rw[NBAT];
 #pragma unroll
@@ -1612,44 +1695,7 @@ __device__ __forceinline__ void shared_place(const DenseMergeArgs& a, int W, int
         for (int i = 0; i < NBAT; ++i) {
             if (c0 + i < c_hi) {  // uniform
                 const int b = shared_bin(a, t[i]);
-                float al = 0.0f;
-                int ai = 0;
-                if constexpr (ALPHA) {
-                    // decay-LUT index: the bin, or clamp((int)t, 0, T) by spike time
-                    ai = b < 0 ? 0 : (a.alpha_by_time ? (int)fminf(fmaxf(t[i], 0.0f), (float)T) : b);
-                    al = __shfl(al_lane, ai & 63, 64);
-                }
-                const uint64_t z0 = __ballot(b == 0);
-                int pos = cur0 + __popcll(z0 & lt);
-                cur0 += __popcll(z0);
-                const bool oth = b > 0;
-                if (__ballot(oth) != 0) {  // uniform
-                    if (oth) atomicOr(&msk[2 * b + (lane >> 5)], bit);
-                    lds_order();
-                    uint64_t mm = 0;
-                    int cb = 0;
-                    if (oth) {
-                        mm = *reinterpret_cast<const uint64_t*>(&msk[2 * b]);
-                        cb = cur[b];
-                    }
-                    lds_order();
-                    if (oth) pos = cb + __popcll(mm & lt);
-                    if (oth && (mm >> lane) == 1ull) {  // the bin's last lane in this chunk
-                        atomicAdd(&cur[b], __popcll(mm));
-                        const int z = vzero();
-                        *reinterpret_cast<int2*>(&msk[2 * b]) = make_int2(z, z);
-                    }
-                    lds_order();
-                }
-                const int q = pos - P0;
-                if (b >= 0 && q >= 0 && q < cap) {
-                    if constexpr (ALPHA) {
-                        reinterpret_cast<unsigned short*>(rows)[q] = (unsigned short)rw[i];
-                        alph[q] = __float_as_int(ai == 64 ? al_64 : al);
-                    } else {
-                        rows[q] = (int)__umul24((unsigned)rw[i], (unsigned)a.rowbytes);
-                    }
-                }
+                place(b, rw[i], ALPHA ? shared_alpha_index(a, t[i], b) : 0);
             }
         }
     }
@@ -1749,9 +1795,10 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
         int snk = 0, stcol = 0, strow = 0;  // SHARED: the pixel's taps
         int* tables = lds_words + shared_list_words(nel_max, T, !CULIF);
         if constexpr (SHARED) {
-            total = shared_count<POOL>(m, (int)pix, blockDim.x >> 6, wave, tables, sv_end, snk, stcol, strow);
+            SharedKeep<kSharedKeep> keep;
+            total = shared_count<POOL>(m, (int)pix, blockDim.x >> 6, wave, tables, sv_end, snk, stcol, strow, keep);
             shared_place<!CULIF, kSharedBatch, POOL>(m, blockDim.x >> 6, wave, rows, alph, tables, 0, nel_max, total,
-                                               snk, stcol, strow, al_lane, al_64);
+                                                     snk, stcol, strow, al_lane, al_64, keep);
         } else {
             total = quad_build<NB, (CULIF || NB > 9), !CULIF, POOL>(m, pix, cur, kinfo, rows, alph, bs);
             wave_sync();
@@ -1989,7 +2036,7 @@ __attribute__((amdgpu_waves_per_eu(CULIF && GEO == 2 && NB == 9 ? 8 : 1))) void 
                 P0 += nel_max;
                 __syncthreads();  // every wave is done with this window
                 shared_place<!CULIF, 1, POOL>(m, blockDim.x >> 6, wave, rows, alph, tables, P0, nel_max, total, snk,
-                                        stcol, strow, al_lane, al_64);
+                                              stcol, strow, al_lane, al_64, SharedKeep<0>{});
                 if (lane < T) v_end = sv_end - P0;
                 if (live) bend = __builtin_amdgcn_readlane(v_end, b);
             }
