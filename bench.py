@@ -464,6 +464,7 @@ def bench_ttfs(args) -> int:
     if args.plans:
         from vdttfs import tune
         tune.apply_plans(net, tune.load_plans(args.plans, w, B))
+        tune.apply_pool_fusion(net, tune.load_pool_fusion(args.plans, w, B))
     d_img = ctx.to_device(img)
     d_pred = ctx.empty(B, np.int32)
     log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "

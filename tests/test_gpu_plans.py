@@ -166,6 +166,10 @@ def test_tuner_lenet(gpu_ctx_factory):
     assert all(r["ms_per_batch"] > 0 for r in rows)
     r = tune.tune_plans(w, img, B, reps=1, rounds=1)
     assert r["tuned_identical"]
+    # LeNet-5's pools feed the dense-merge conv and a flattened FC: no build takes them
+    assert set(r["pool_fusion"]["modes"]) == {"off", "auto", "all"}
+    assert all(v["identical"] and v["ms"] > 0 for v in r["pool_fusion"]["modes"].values())
+    assert r["pool_fusion"]["best"] in ("off", "auto", "all")
     assert [L["layer"] for L in r["layers"]] == [0, 2, 4, 5, 6]
     for L in r["layers"]:
         assert L["all_identical"] and L["best"] is not None

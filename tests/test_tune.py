@@ -28,6 +28,16 @@ def test_load_plans_checks_workload(tmp_path):
         tune.load_plans(str(f), models.lenet5(T=32), 64)  # another window
     with pytest.raises(ValueError):
         tune.load_plans(str(f), models.vgg16(), 64)  # another network
+    assert tune.load_pool_fusion(str(f), w, 64) is None  # files without a pool-fusion mode
+    for name in ("off", "auto", "all"):
+        f.write_text(json.dumps({"workload": w.name, "batch": 64, "T": w.consts.T, "plans": plans,
+                                 "pool_fusion": name}))
+        assert tune.load_pool_fusion(str(f), w, 64) == name
+        assert tune.POOL_FUSION[name] in (vdttfs.POOL_FUSE_OFF, vdttfs.POOL_FUSE_AUTO, vdttfs.POOL_FUSE_ALL)
+    f.write_text(json.dumps({"workload": w.name, "batch": 64, "T": w.consts.T, "plans": plans,
+                             "pool_fusion": "some"}))
+    with pytest.raises(ValueError):
+        tune.load_pool_fusion(str(f), w, 64)
 
 
 def test_committed_vgg_plans_fit_the_benchmark():

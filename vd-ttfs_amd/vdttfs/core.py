@@ -18,7 +18,7 @@ from ._lib import (Consts, CulifLayer, LayerDesc, VdttfsError, check, lib, INF_T
                    LAYER_CONV, LAYER_FC, LAYER_POOL, LAYER_VMEM, ENCODE_LINEAR, ENCODE_LOG, ENCODE_TIMES,
                    READOUT_ARGMIN, READOUT_ARGMAX, CULIF_RAW_CONV, CULIF_CONV, CULIF_POOL,
                    CULIF_FC_REC, CULIF_FC, STEP_T1, STEP_T2, STEP_T3, LayerPlan, PATH_AUTO, PATH_BINS, PATH_DENSE,
-                   PATH_FUSED, PATH_REG, PATH_WINDOW)
+                   PATH_FUSED, PATH_REG, PATH_WINDOW, POOL_FUSE_OFF, POOL_FUSE_ALL, POOL_FUSE_AUTO)
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:

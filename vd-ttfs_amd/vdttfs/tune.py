@@ -15,7 +15,9 @@ c_out a lane gathers per event (1, 2 events per load, or 4), and how many
 output pixels a wave integrates.  The tuner sweeps them per layer with the
 reference's procedure -- minimum of three timed rounds, outputs compared bit
 for bit with the built-in choice -- and reports the best plan per layer and
-the whole forward under the tuned plans.
+the whole forward under the tuned plans; then, under those plans, which 2x2
+pools run inside the next layer's list build (vdttfs_net_set_pool_fusion:
+off, auto or all), timed on the whole forward.
 
   python -m vdttfs.tune --workload vgg16 --batch 256
   python -m vdttfs.tune --workload lenet5 --deltas 4 8 16 32 64
@@ -36,6 +38,7 @@ from . import core, models
 
 PATHS = {core.PATH_BINS: "bins", core.PATH_DENSE: "dense", core.PATH_FUSED: "fused", core.PATH_REG: "reg",
          core.PATH_WINDOW: "window"}
+POOL_FUSION = {"off": core.POOL_FUSE_OFF, "auto": core.POOL_FUSE_AUTO, "all": core.POOL_FUSE_ALL}
 
 
 def _min_round_ms(ctx, net, x, d_pred, reps, rounds, per_layer):
@@ -141,12 +144,23 @@ def tune_plans(w, img, B, reps=3, rounds=3):
                     net.set_plan(i, *p)
             fwd_tuned = float(_min_round_ms(ctx, net, x, d_pred, reps, rounds, False))
             tuned_same = all(np.array_equal(net.layer_output(i), ref[i]) for i in range(n))
+            # pool fusion under the tuned plans: the whole forward per mode
+            # (a fused pool's map is written when layer_output asks for it)
+            fusion = {}
+            for name, mode in POOL_FUSION.items():
+                net.set_pool_fusion(mode)
+                ms = float(_min_round_ms(ctx, net, x, d_pred, reps, rounds, False))
+                same = all(np.array_equal(net.layer_output(i), ref[i]) for i in range(n))
+                fusion[name] = {"ms": ms, "identical": same}
+            net.set_pool_fusion(core.POOL_FUSE_OFF)
+            ok = [k for k, v in fusion.items() if v["identical"]]
+            best_fusion = min(ok, key=lambda k: fusion[k]["ms"]) if ok else "off"
             x.free()
             d_pred.free()
         finally:
             net.close()
     return {"layers": rows, "forward_ms": {"auto": fwd_auto, "tuned": fwd_tuned},
-            "tuned_identical": tuned_same,
+            "tuned_identical": tuned_same, "pool_fusion": {"modes": fusion, "best": best_fusion},
             "plans": [_plan_dict(p) if w.layers[i].kind in (core.LAYER_CONV, core.LAYER_FC) else None
                       for i, p in enumerate(best_plans)]}
 
@@ -168,14 +182,33 @@ def apply_plans(net, plans):
             net.set_plan(i, _path_id(p["path"]), p["gather"], p["ppw"])
 
 
-def load_plans(path, w, B):
-    """Plans written by --out, checked against the workload and batch."""
+def apply_pool_fusion(net, name):
+    """Sets the pool-fusion mode of a tune result ("off", "auto" or "all";
+    None leaves the network's default)."""
+    if name is not None:
+        net.set_pool_fusion(POOL_FUSION[name])
+
+
+def _load(path, w, B):
     with open(path) as f:
         d = json.load(f)
     if d.get("workload") != w.name or d.get("batch") != B or d.get("T") != w.consts.T:
         raise ValueError(f"{path}: plans for {d.get('workload')} B={d.get('batch')} T={d.get('T')}, "
                          f"not {w.name} B={B} T={w.consts.T}")
-    return d["plans"]
+    return d
+
+
+def load_plans(path, w, B):
+    """Plans written by --out, checked against the workload and batch."""
+    return _load(path, w, B)["plans"]
+
+
+def load_pool_fusion(path, w, B):
+    """The pool-fusion mode written by --out, or None (files without one)."""
+    name = _load(path, w, B).get("pool_fusion")
+    if name is not None and name not in POOL_FUSION:
+        raise ValueError(f"{path}: unknown pool fusion {name!r}")
+    return name
 
 
 def main(argv=None) -> int:
@@ -198,7 +231,8 @@ def main(argv=None) -> int:
         r.update(tune_plans(w, img, B, a.reps, a.rounds))
         if a.out:
             with open(a.out, "w") as f:
-                json.dump({"workload": w.name, "batch": B, "T": w.consts.T, "plans": r["plans"]}, f, indent=1)
+                json.dump({"workload": w.name, "batch": B, "T": w.consts.T, "plans": r["plans"],
+                           "pool_fusion": r["pool_fusion"]["best"]}, f, indent=1)
     print(json.dumps(r), flush=True)
     return 0
 
