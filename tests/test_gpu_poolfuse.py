@@ -137,13 +137,14 @@ def mixed_layers(rng, T):
         return vdttfs.Layer(POOL, H, H, c, H // 2, H // 2, c)
 
     return [conv(11, 3, 24, T / 4, 0.0),       # 0
-            pool(11, 24),                      # 1 -> 5x5, into a 216-element per-wave build
-            conv(5, 24, 40, T / 3, 1.5),       # 2
-            pool(5, 40),                       # 3 -> 2x2, into a shared build (C_out 150)
-            conv(2, 40, 150, T / 5, 0.5),      # 4
-            pool(2, 150),                      # 5 -> 1x1, into the FC layer
-            fc(150, 96, T / 4, 2.0),           # 6
-            fc(96, 70, T / 2, 0.0),            # 7
+            pool(11, 24),                      # 1 -> 5x5, into a per-wave build of 9 chunks (216 elements)
+            conv(5, 24, 96, T / 3, 1.5),       # 2
+            pool(5, 96),                       # 3 -> 2x2, into a per-wave build of 18 chunks (864 elements)
+            conv(2, 96, 64, T / 5, 0.5),       # 4
+            conv(2, 64, 150, T / 4, 1.0),      # 5: a shared build (C_out 150)
+            pool(2, 150),                      # 6 -> 1x1, into the FC layer's shared build
+            fc(150, 96, T / 4, 2.0),           # 7
+            fc(96, 70, T / 2, 0.0),            # 8
             ]
 
 
@@ -166,7 +167,7 @@ def test_pool_fusion_mixed_net(gpu_ctx_factory, task2):
 
     ref = oracle.net_forward(oc, layers, B, t, img_elems, oracle.ENC_TIMES, T / 4.0, 0.0,
                              oracle.READ_ARGMIN, same_pad=True, keep_layers=True)
-    for i in (0, 2, 4, 6):
+    for i in (0, 2, 4, 5, 7):
         frac = float(np.mean(ref["outs"][i] < 9999.0))
         assert 0.02 < frac < 0.98, f"layer {i} fires {frac}"
     ctx = gpu_ctx_factory(tc)
@@ -175,9 +176,10 @@ def test_pool_fusion_mixed_net(gpu_ctx_factory, task2):
         x = ctx.to_device(t)
         assert forward_check(ctx, net, layers, x, None, ref, "off") == set()
         net.set_pool_fusion(vdttfs.POOL_FUSE_AUTO)
-        assert forward_check(ctx, net, layers, x, None, ref, "auto") == {5}
+        assert forward_check(ctx, net, layers, x, None, ref, "auto") == {6}
         net.set_pool_fusion(vdttfs.POOL_FUSE_ALL)
-        assert forward_check(ctx, net, layers, x, None, ref, "built-in") == {1, 3, 5}
+        assert net.get_plan(2)[0] == net.get_plan(4)[0] == vdttfs.PATH_FUSED
+        assert forward_check(ctx, net, layers, x, None, ref, "built-in") == {1, 3, 6}
         cands = {i: tune.candidates(net, i) for i, l in enumerate(layers) if l.kind in (CONV, FC)}
         for r in range(max(len(c) for c in cands.values())):
             for i, c in cands.items():
@@ -187,13 +189,13 @@ def test_pool_fusion_mixed_net(gpu_ctx_factory, task2):
             net.set_plan(i)
         # per-layer windows (the separate-pool engine path under windows is
         # pinned against the oracle by the calibrator's tests): fused equals it
-        net.set_windows([40, 0, 48, 0, 0, 0, 33, 64])
+        net.set_windows([40, 0, 48, 0, 0, 56, 0, 33, 64])
         net.set_pool_fusion(vdttfs.POOL_FUSE_OFF)
         net.forward(x)
         ctx.synchronize()
         base = {"outs": [net.layer_output(i) for i in range(len(layers))]}
         net.set_pool_fusion(vdttfs.POOL_FUSE_ALL)
-        assert forward_check(ctx, net, layers, x, None, base, "windows") == {1, 3, 5}
+        assert forward_check(ctx, net, layers, x, None, base, "windows") == {1, 3, 6}
         x.free()
     finally:
         net.close()
