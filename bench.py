@@ -465,6 +465,8 @@ def bench_ttfs(args) -> int:
         from vdttfs import tune
         tune.apply_plans(net, tune.load_plans(args.plans, w, B))
         tune.apply_pool_fusion(net, tune.load_pool_fusion(args.plans, w, B))
+    if args.graphs:
+        net.set_graphs(True)
     d_img = ctx.to_device(img)
     d_pred = ctx.empty(B, np.int32)
     log(f"bench: {w.name} B={B} T={w.consts.T} delta={w.consts.delta} tfs={w.consts.tfs} "
@@ -534,7 +536,8 @@ def bench_ttfs(args) -> int:
         "config": {"workload": workload, "key": key,
                    "batch": B, "T": w.consts.T, "delta": w.consts.delta, "tfs": w.consts.tfs,
                    "seed": w.seed, "parallelism": "none (one GPU)",
-                   "plans": os.path.relpath(args.plans, ROOT) if args.plans else "built-in"},
+                   "plans": os.path.relpath(args.plans, ROOT) if args.plans else "built-in",
+                   "launch": "HIP graph replay" if args.graphs else "stream launches"},
         "roofline": {
             "bound": "hbm",
             "achieved": hbm,
@@ -879,6 +882,8 @@ def main() -> int:
     ap.add_argument("--plans", default=None,
                     help="vgg16/lenet5: per-layer launch plans written by python -m vdttfs.tune --out "
                          "(default: the library's built-in choice)")
+    ap.add_argument("--graphs", action="store_true",
+                    help="vgg16/lenet5: forwards captured into a HIP graph and replayed (vdttfs_net_set_graphs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size copy used to scale FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--gather-probe", action="store_true",

@@ -280,6 +280,16 @@ int vdttfs_net_count(vdttfs_net* net, const float* d_img, uint64_t* eproc, uint6
 #define VDTTFS_POOL_FUSE_ALL  1
 #define VDTTFS_POOL_FUSE_AUTO 2
 int vdttfs_net_set_pool_fusion(vdttfs_net* net, int mode);
+/* HIP graphs.  No counterpart in the reference, which launches every kernel
+ * of every batch from the host.  enable != 0: vdttfs_net_forward captures
+ * the forward (encode, layers, readout) on the context stream into a HIP
+ * graph the first time it sees a (d_img, d_pred) pair under the network's
+ * current plans, windows and pool fusion, and replays that graph afterwards;
+ * up to four pairs are kept, and changing a plan, the windows or the pool
+ * fusion drops them.  The graph holds kernel launches only (no memset or
+ * copy nodes).  Outputs are the same as without.  Forwards with event timing
+ * on, and counting forwards, run without graphs.  Default 0. */
+int vdttfs_net_set_graphs(vdttfs_net* net, int enable);
 /* Event timing of integrator launches: when enabled, forward() brackets
  * each integrator launch with HIP events on the context stream; read_timing
  * synchronises and returns the summed milliseconds and launch count since

@@ -42,6 +42,19 @@ struct TimedPair {
     int layer;
 };
 
+// A forward captured into a HIP graph for one (input, prediction) pair of
+// pointers under one configuration of the network (`gen`), with the host-side
+// state the capture left: which pools it fused, and from which maps.
+struct GraphEntry {
+    const float* img = nullptr;
+    int32_t* pred = nullptr;
+    unsigned gen = 0;
+    hipGraphExec_t exec = nullptr;
+    std::vector<unsigned char> fused;
+    std::vector<const float*> pool_src;
+};
+constexpr size_t kMaxGraphs = 4;  // (input, prediction) pairs kept per network
+
 }  // namespace
 
 struct vdttfs_net {
@@ -59,6 +72,9 @@ struct vdttfs_net {
     int32_t* bstart = nullptr;
     bool timing = false;
     int pool_fusion = VDTTFS_POOL_FUSE_OFF;  // which 2x2 pools run inside the next layer's list build
+    bool graphs_on = false;  // forwards replay captured HIP graphs
+    unsigned gen = 0;        // configuration generation: plans, windows, pool fusion
+    std::vector<GraphEntry> graphs;
     std::vector<hipEvent_t> pool;
     size_t pool_used = 0;
     std::vector<TimedPair> pending;
@@ -303,6 +319,7 @@ void release(vdttfs_net* net) {
         for (void* q : p)
             if (q) (void)hipFree(q);
     }
+    for (GraphEntry& g : net->graphs) (void)hipGraphExecDestroy(g.exec);
     if (net->enc) (void)hipFree(net->enc);
     if (net->ev) (void)hipFree(net->ev);
     if (net->off) (void)hipFree(net->off);
@@ -461,10 +478,77 @@ int vdttfs_net_destroy(vdttfs_net* net) {
     return VDTTFS_OK;
 }
 
+namespace {
+
+// Captures one forward on the context stream into a graph and instantiates it.
+int capture_forward(vdttfs_net* net, const float* d_img, int32_t* d_pred, GraphEntry* g) {
+    vdttfs_ctx* ctx = net->ctx;
+    VD_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    const int rc = forward_impl(net, d_img, d_pred, nullptr, nullptr, nullptr, nullptr);
+    hipGraph_t graph = nullptr;
+    const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
+    if (rc != VDTTFS_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (ec != hipSuccess || !graph)
+        return set_error(VDTTFS_E_HIP, "net_forward: graph capture failed: %s", hipGetErrorString(ec));
+    const hipError_t ei = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) return set_error(VDTTFS_E_HIP, "net_forward: graph instantiation failed: %s", hipGetErrorString(ei));
+    g->img = d_img;
+    g->pred = d_pred;
+    g->gen = net->gen;
+    g->fused.resize(net->L.size());
+    g->pool_src.resize(net->L.size());
+    for (size_t i = 0; i < net->L.size(); ++i) {
+        g->fused[i] = net->L[i].fused ? 1 : 0;
+        g->pool_src[i] = net->L[i].pool_src;
+    }
+    return VDTTFS_OK;
+}
+
+}  // namespace
+
 int vdttfs_net_forward(vdttfs_net* net, const float* d_img, int32_t* d_pred) {
     if (!net || !d_img) return set_error(VDTTFS_E_INVALID, "net_forward: null argument");
     VD_TRY(check_ctx(net->ctx));
-    return forward_impl(net, d_img, d_pred, nullptr, nullptr, nullptr, nullptr);
+    if (!net->graphs_on || net->timing) return forward_impl(net, d_img, d_pred, nullptr, nullptr, nullptr, nullptr);
+    // graphs of an older configuration are dropped; a pair of pointers seen
+    // before replays its graph, a new one is captured (the oldest evicted)
+    for (size_t i = 0; i < net->graphs.size();) {
+        if (net->graphs[i].gen != net->gen) {
+            (void)hipGraphExecDestroy(net->graphs[i].exec);
+            net->graphs.erase(net->graphs.begin() + (long)i);
+        } else {
+            ++i;
+        }
+    }
+    GraphEntry* hit = nullptr;
+    for (GraphEntry& g : net->graphs)
+        if (g.img == d_img && g.pred == d_pred) hit = &g;
+    if (!hit) {
+        if (net->graphs.size() == kMaxGraphs) {
+            (void)hipGraphExecDestroy(net->graphs.front().exec);
+            net->graphs.erase(net->graphs.begin());
+        }
+        GraphEntry g;
+        VD_TRY(capture_forward(net, d_img, d_pred, &g));
+        net->graphs.push_back(std::move(g));
+        hit = &net->graphs.back();
+    }
+    VD_HIP(hipGraphLaunch(hit->exec, net->ctx->stream));
+    for (size_t i = 0; i < net->L.size(); ++i) {  // the forward's host-side state, as the capture left it
+        net->L[i].fused = hit->fused[i] != 0;
+        net->L[i].pool_src = hit->pool_src[i];
+    }
+    return VDTTFS_OK;
+}
+
+int vdttfs_net_set_graphs(vdttfs_net* net, int enable) {
+    if (!net) return set_error(VDTTFS_E_INVALID, "null net");
+    net->graphs_on = enable != 0;
+    return VDTTFS_OK;
 }
 
 int vdttfs_net_layer_output(vdttfs_net* net, int layer, const float** d_out, int64_t* elems) {
@@ -503,6 +587,7 @@ int vdttfs_net_set_pool_fusion(vdttfs_net* net, int mode) {
     if (mode != VDTTFS_POOL_FUSE_OFF && mode != VDTTFS_POOL_FUSE_ALL && mode != VDTTFS_POOL_FUSE_AUTO)
         return set_error(VDTTFS_E_INVALID, "net_set_pool_fusion: unknown mode %d", mode);
     net->pool_fusion = mode;
+    ++net->gen;
     return VDTTFS_OK;
 }
 
@@ -527,6 +612,7 @@ int vdttfs_net_set_windows(vdttfs_net* net, const int32_t* windows, int n_layers
         const int w = windows && net->L[i].d.kind != VDTTFS_LAYER_POOL ? windows[i] : 0;
         net->L[i].window = w == T ? 0 : w;
     }
+    ++net->gen;
     return VDTTFS_OK;
 }
 
@@ -549,6 +635,7 @@ int vdttfs_net_set_plan(vdttfs_net* net, int layer, const vdttfs_layer_plan* pla
     LaunchPlan resolved;
     VD_TRY(resolve_plan(net->ctx, integ_shape(net, l), req, &resolved));
     l.plan = req;
+    ++net->gen;
     return VDTTFS_OK;
 }
 

@@ -179,6 +179,7 @@ SIGNATURES = {
     "vdttfs_net_count": [_vp, _vp, _u64p, _u64p, _u64p, _u64p],
     "vdttfs_net_set_timing": [_vp, _i],
     "vdttfs_net_set_pool_fusion": [_vp, _i],
+    "vdttfs_net_set_graphs": [_vp, _i],
     "vdttfs_net_set_windows": [_vp, _vp, _i],
     "vdttfs_net_set_plan": [_vp, _i, _vp],
     "vdttfs_net_get_plan": [_vp, _i, _vp],

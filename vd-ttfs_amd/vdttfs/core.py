@@ -344,6 +344,11 @@ class Net:
     def set_timing(self, on: bool):
         check(lib().vdttfs_net_set_timing(self.handle, int(on)))
 
+    def set_graphs(self, on: bool):
+        """Forwards captured into HIP graphs and replayed per (input,
+        prediction) pair (vdttfs_net_set_graphs); same outputs."""
+        check(lib().vdttfs_net_set_graphs(self.handle, int(on)))
+
     def set_pool_fusion(self, mode: int):
         """Which 2x2 pools run inside the next layer's list build
         (vdttfs_net_set_pool_fusion: POOL_FUSE_OFF, the default, _ALL or
