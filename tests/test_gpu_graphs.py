@@ -1,7 +1,8 @@
 """HIP-graph forwards (vdttfs_net_set_graphs): every replay of a captured
 forward equals the eager forward layer by layer, with eager work and
 synchronisations between the replays, for two input/prediction pairs at
-once; a plan change recaptures; pool fusion's lazily written pool maps stay
+once; a plan or window change recaptures; more pairs than the network keeps
+evict the oldest and stay correct; pool fusion's lazily written pool maps stay
 right across replays, counting forwards and eager forwards in between.  The
 eager forwards these are compared with are pinned against the oracle by the
 network and plan tests; the last layer and the predictions are checked
@@ -84,6 +85,28 @@ def test_graph_replays_match_eager(gpu_ctx_factory, name, B):
             ctx.synchronize()
             check(net, refs[0], preds[0], ps[0], f"after set_plan, replay {r}")
         net.set_plan(last)
+        # windows recapture too: equal to the eager forward under the same windows
+        wins = [0 if l.kind == vdttfs.LAYER_POOL else 48 for l in w.layers]
+        net.set_windows(wins)
+        net.set_graphs(False)
+        net.forward(xs[0], ps[0])
+        ctx.synchronize()
+        wref, wpred = outputs(net, n), ps[0].download()
+        net.set_graphs(True)
+        for r in range(2):
+            net.forward(xs[0], ps[0])
+            ctx.synchronize()
+            check(net, wref, wpred, ps[0], f"windows, replay {r}")
+        net.set_windows(None)
+        # more (input, prediction) pairs than the network keeps graphs for
+        extra = [ctx.empty(B, np.int32) for _ in range(5)]
+        for r in range(2):
+            for p in extra:
+                net.forward(xs[0], p)
+                ctx.synchronize()
+                check(net, refs[0], preds[0], p, f"pair eviction, round {r}")
+        for p in extra:
+            p.free()
         # pool fusion: the pools' maps are written on request, also after replays
         net.set_pool_fusion(vdttfs.POOL_FUSE_ALL)
         for r in range(3):
