@@ -23,6 +23,20 @@ def header_symbols():
     return sorted(set(re.findall(r"\b(vdttfs_[a-z0-9_]+)\s*\(", src)))
 
 
+def test_python_constants_match_the_header():
+    """Every integer #define VDTTFS_X of the header that the Python mirror
+    names X carries the same value there (paths, layer kinds, encoders,
+    readouts, step modes, pool-fusion modes, error codes)."""
+    src = open(os.path.join(ROOT, "include", "vdttfs.h")).read()
+    defs = dict((k, int(v)) for k, v in re.findall(r"#define\s+VDTTFS_(\w+)\s+(-?\d+)\b", src))
+    shared = [k for k in defs if hasattr(_lib, k)]
+    assert len(shared) >= 20, shared
+    for k in shared:
+        assert getattr(_lib, k) == defs[k], k
+    for k in ("POOL_FUSE_OFF", "POOL_FUSE_ALL", "POOL_FUSE_AUTO", "PATH_FUSED", "PATH_WINDOW"):
+        assert k in shared
+
+
 def test_library_exports_every_declared_symbol():
     syms = header_symbols()
     assert len(syms) >= 40
